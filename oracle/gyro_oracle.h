@@ -1,0 +1,120 @@
+/*
+ * CPU oracle for the routed-expert MoE path: TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's CPU engine for this path. Only tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it, and only as the
+ * checker or the timed CPU baseline. The product (gyro-dx_amd/) never links or calls it.
+ *
+ * Every function cites the reference file:line it restates. Pinning of each function
+ * (what fixes its output independently of this restatement) is listed in oracle/README.md.
+ */
+#ifndef GYRO_ORACLE_H
+#define GYRO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes mirror the error set of src/gyro.zig:43-53. */
+enum {
+    GO_OK = 0,
+    GO_UNSUPPORTED_TYPE = -1,
+    GO_MISSING_STATE_BITS = -2,
+    GO_UNSUPPORTED_STATE_BITS = -3,
+    GO_INVALID_ROW_LENGTH = -4,
+    GO_INVALID_SOURCE_LENGTH = -5,
+    GO_INVALID_BLOCK_SIZE = -7,
+    GO_INVALID_SIGNS_LENGTH = -8,
+    GO_INVALID_SIGN = -9,
+};
+
+/* Installs the normative codebook (8192 bytes of little-endian binary16, src/gyro_codebook.f16)
+ * and expands it to fp32 as src/kernels.zig:14-23 does. Returns GO_INVALID_SOURCE_LENGTH if the
+ * length is not 8192. Must be called before any decode. */
+int go_init(const uint8_t *codebook, size_t len);
+
+/* Type table (src/gyro.zig:32-41): returns 0 for an unknown id. */
+int go_type_info(uint32_t id, uint32_t *k, uint32_t *steps, uint32_t *block_bytes);
+/* src/gyro.zig:70-76; 0 on error. */
+uint64_t go_row_bytes(uint32_t id, uint64_t weights);
+/* src/gyro.zig:127-141. */
+float go_fp16_to_fp32(uint16_t half);
+/* src/gyro.zig:107-117. */
+uint32_t go_trellis_state(uint32_t id, const uint8_t *stream, uint32_t step);
+/* Strict decoder, src/gyro.zig:81-105. state_bits < 0 means "missing". */
+int go_decode_row(uint32_t id, int32_t state_bits, const uint8_t *src, size_t src_len,
+                  float *dst, size_t n);
+/* Strict rotation, src/gyro.zig:143-195. signs may be NULL (identity). */
+int go_rotate(float *v, size_t n, size_t block, const int8_t *signs);
+int go_unrotate(float *v, size_t n, size_t block, const int8_t *signs);
+
+/* Engine-level helpers (src/kernels.zig). */
+void go_rotate_f32signs(float *x, size_t n, size_t block, const float *signs); /* :316-338 */
+void go_softmax(float *x, size_t n);                                             /* :340-349 */
+float go_silu(float x);                                                          /* :307-309 */
+float go_sigmoid(float x);                                                       /* :303-305 */
+float go_dot_f32(const float *row, const float *x, size_t n);                    /* :72-84 */
+float go_dot_bf16(const uint16_t *row, const float *x, size_t n);                /* :86-105 */
+float go_dot_dense(const float *a, const float *b, size_t n);                    /* :253-261 */
+float go_dot_row(uint32_t type_id, const uint8_t *row, const float *x, size_t cols); /* :201-210 */
+void go_decode_row_fast(uint32_t type_id, const uint8_t *row, float *out, size_t cols); /* :213-235 */
+void go_rms_norm(float *out, const float *x, const float *w, size_t n, float eps);  /* :281-291 */
+/* src/engine.zig:670-687: top-k by value, ties to the lower index. */
+void go_topk(const float *values, size_t n, uint32_t *ids, float *weights, size_t k);
+
+/* One MoE layer as src/engine.zig:520-653 computes it. Expert matrices: per expert and
+ * projection, a pointer to its packed rows and its type id (144..151), so a layer may mix
+ * types. Gate/up rows have E columns (F rows per expert); down rows have F columns
+ * (E rows per expert). */
+typedef struct go_layer {
+    uint32_t E, F, n_expert, n_used;
+    float expert_weights_scale;
+    const float *router;          /* [n_expert][E] fp32 */
+    const float *router_bias;     /* [n_expert] added to the logits, or NULL */
+    const uint8_t *const *gate;   /* [n_expert] -> F rows */
+    const uint8_t *const *up;     /* [n_expert] -> F rows */
+    const uint8_t *const *down;   /* [n_expert] -> E rows */
+    const uint32_t *gate_type, *up_type, *down_type; /* [n_expert] */
+    const float *gate_signs;      /* [E] or NULL */
+    const float *down_signs;      /* [F] or NULL */
+    /* Shared expert (optional, bf16 weights): SF = 0 disables it. */
+    uint32_t SF;
+    const uint16_t *sh_gate, *sh_up; /* [SF][E] bf16 */
+    const uint16_t *sh_down;         /* [E][SF] bf16 */
+    const float *sh_gate_inp;        /* [E] fp32 */
+    float sh_gate_const;             /* used when sh_gate_inp is NULL: gate = this value */
+} go_layer;
+
+/* Optional intermediate outputs of go_moe_ffn (any pointer may be NULL). */
+typedef struct go_trace {
+    float *logits;          /* [n][n_expert] router logits before softmax */
+    uint32_t *route_ids;    /* [n][n_used] */
+    float *route_w;         /* [n][n_used] */
+    uint32_t *route_order;  /* [n*n_used] */
+    uint32_t *order_start;  /* [n_expert+1] */
+    float *xh;              /* [n][E] rotated expert input */
+    float *act;             /* [n*n_used][F] down input (after SwiGLU and rotation) */
+    float *down;            /* [n*n_used][E] */
+    float *moe_out;         /* [n][E] routed output before the shared expert */
+} go_trace;
+
+/* Runs the layer on n tokens: out[n][E]. threads = pool size including the caller.
+ * Returns 0, or a negative code for invalid arguments. */
+int go_moe_ffn(const go_layer *layer, const float *x, size_t n, float *out, go_trace *trace,
+               uint32_t threads);
+
+/* fp64 dense reference of the routed and shared experts for given routes: decodes every
+ * selected expert row bit-exactly to fp32 and accumulates in fp64. out[n][E] in fp64. */
+int go_moe_dense_f64(const go_layer *layer, const float *x, size_t n, const uint32_t *route_ids,
+                     const float *route_w, double *out);
+
+/* Router logits in fp64 for margin checks: logits[n][n_expert]. */
+void go_router_f64(const go_layer *layer, const float *x, size_t n, double *logits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
