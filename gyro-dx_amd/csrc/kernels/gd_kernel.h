@@ -1,0 +1,101 @@
+// Device-side conventions shared by every gyro_native pipeline (gfx950, wave64).
+//
+// A pipeline is one code object exporting `gd_main(GdArgs)` and `gd_workgroup[3]`. GdArgs
+// carries the device table of buffer base pointers and up to 60 32-bit constants, the same
+// constant layouts the reference's HLSL kernels read from root constants
+// (shaders/engine/common.hlsli:9-14): buffers are named by table index; element offsets count
+// 4-byte words unless a kernel says bytes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct GdArgs {
+    const uint64_t *table;
+    uint32_t c[60];
+};
+
+#define GD_PIPELINE(WG)                                                   \
+    extern "C" __constant__ uint32_t gd_workgroup[3] = {WG, 1, 1};        \
+    extern "C" __global__ __launch_bounds__(WG) void gd_main(const GdArgs a)
+
+template <typename T>
+__device__ __forceinline__ T *gd_buf(const GdArgs &a, uint32_t index) {
+    return reinterpret_cast<T *>(a.table[index]);
+}
+
+__device__ __forceinline__ float gd_bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t gd_f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// binary16 -> binary32 through the hardware conversion (exact for every finite value; the
+// fp16 denormal mode is IEEE on gfx950).
+__device__ __forceinline__ float gd_half(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// binary16 -> binary32 in integer arithmetic, the normative conversion of src/gyro.zig:127-141.
+__device__ __forceinline__ float gd_half_exact(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exponent = (h >> 10) & 31u;
+    uint32_t mantissa = h & 1023u;
+    if (exponent == 31u) return gd_bits_f32(sign | 0x7f800000u | (mantissa << 13));
+    if (exponent != 0u) return gd_bits_f32(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+    if (mantissa == 0u) return gd_bits_f32(sign);
+    // Subnormal: shift the leading one into bit 10 (clz of a value below 1024).
+    uint32_t shift = __builtin_clz(mantissa) - 21u;
+    mantissa <<= shift;
+    return gd_bits_f32(sign | ((113u - shift) << 23) | ((mantissa & 1023u) << 13));
+}
+
+__device__ __forceinline__ float gd_silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float gd_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float gd_silu_accurate(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gd_sigmoid_accurate(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Gyro type table, src/gyro.zig:32-41: k (new bits per step), steps, block bytes.
+struct GyroType {
+    uint32_t k, steps, block_bytes;
+};
+__device__ __forceinline__ bool gd_type(uint32_t id, GyroType &t) {
+    switch (id) {
+        case 144: t = {8, 32, 34}; return true;
+        case 145: t = {6, 32, 26}; return true;
+        case 146: t = {7, 32, 30}; return true;
+        case 147: t = {5, 64, 42}; return true;
+        case 148: t = {6, 64, 50}; return true;
+        case 149: t = {7, 64, 58}; return true;
+        case 150: t = {5, 32, 22}; return true;
+        case 151: t = {4, 32, 18}; return true;
+        default: t = {0, 0, 0}; return false;
+    }
+}
+
+// 16-bit trellis state of a step (src/gyro.zig:107-117) read from a byte stream.
+__device__ __forceinline__ uint32_t gd_state(const uint8_t *stream, const GyroType &t, uint32_t id,
+                                             uint32_t step) {
+    if (id == 144u) return ((uint32_t)stream[(step + 31u) & 31u] << 8) | stream[step];
+    uint32_t len = t.steps * t.k / 8u;
+    uint32_t off = (t.steps - 1u - step) * t.k;
+    uint32_t byte = off >> 3;
+    uint32_t b1 = byte + 1u >= len ? byte + 1u - len : byte + 1u;
+    uint32_t b2 = byte + 2u >= len ? byte + 2u - len : byte + 2u;
+    uint32_t word = (uint32_t)stream[byte] | ((uint32_t)stream[b1] << 8) | ((uint32_t)stream[b2] << 16);
+    return (word >> (off & 7u)) & 0xffffu;
+}
+
+// Multiplicative hash of SPEC section 5: one product serves both codebook indices.
+__device__ __forceinline__ uint32_t gd_hash(uint32_t state) { return (state & 0x7fffu) * 0x9e3779b1u; }
+
+// Wave64 reductions.
+__device__ __forceinline__ float gd_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float gd_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// 1 / sqrt(128) rounded to binary32, the normalisation of a 128-point Walsh-Hadamard block.
+#define GD_INV_SQRT128 0.0883883461356163f

@@ -1,0 +1,97 @@
+// Building blocks of the MI355X fast paths: TQ2_T trellis states from packed stream words,
+// the hash and LDS codebook addressing in 24-bit integer arithmetic, and the per-layer
+// expert descriptor table.
+#pragma once
+#include "gd_kernel.h"
+
+// Expert descriptor: device addresses of one expert's gate, up and down rows, and their Gyro
+// types (one byte each, projection p in bits 8p..8p+7). 32 bytes per expert.
+struct ExpertDesc {
+    uint64_t gate, up, down;
+    uint32_t types;
+    uint32_t pad;
+};
+
+// Two 15-bit TQ2_T states from stream word q (bytes 4i..4i+3) and the previous word qp:
+// lo16 = state of step 4i (+0) or 4i+2 (+2), hi16 = the following step, before masking.
+// v_perm_b32 picks bytes from {q : qp}; pool bytes 0-3 are qp, 4-7 are q.
+__device__ __forceinline__ uint32_t tq2_pair01(uint32_t q, uint32_t qp) {
+    return __builtin_amdgcn_perm(q, qp, 0x04050304u);  // [b4i, b4i-1, b4i+1, b4i]
+}
+__device__ __forceinline__ uint32_t tq2_pair23(uint32_t q) {
+    return __builtin_amdgcn_perm(q, q, 0x06070506u);   // [b4i+2, b4i+1, b4i+3, b4i+2]
+}
+
+// LDS byte addresses of the two codebook pairs of a 15-bit state s (SPEC section 5):
+// x = s * 0x9E3779B1 mod 2^32 = p + ((s * 0x9E) << 24) with p = s * 0x3779B1 (24-bit product);
+// idx1 * 4 = (x >> 8) & 0x1ffc only sees p; idx0 * 4 = (x >> 19) & 0x1ffc
+//          = ((p >> 19) + s * (0x9E << 5)) & 0x1ffc.
+__device__ __forceinline__ void cb_addr(uint32_t s, uint32_t &a0, uint32_t &a1) {
+    const uint32_t p = __umul24(s, 0x3779B1u);
+    a1 = (p >> 8) & 0x1ffcu;
+    a0 = (__umul24(s, 0x13C0u) + (p >> 19)) & 0x1ffcu;
+}
+__device__ __forceinline__ uint32_t cb_addr0(uint32_t s) {
+    const uint32_t p = __umul24(s, 0x3779B1u);
+    return (__umul24(s, 0x13C0u) + (p >> 19)) & 0x1ffcu;
+}
+
+__device__ __forceinline__ uint32_t lds_word(const uint32_t *book_base, uint32_t byte_addr) {
+    return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(book_base) + byte_addr);
+}
+
+// fp16 half of a codebook word times an fp32 activation, accumulated in fp32 (v_fma_mix_f32).
+__device__ __forceinline__ float fma_lo(uint32_t w, float x, float acc) {
+    return __builtin_fmaf(gd_half(w & 0xffffu), x, acc);
+}
+__device__ __forceinline__ float fma_hi(uint32_t w, float x, float acc) {
+    return __builtin_fmaf(gd_half(w >> 16), x, acc);
+}
+
+// Read-only global data viewed through the constant address space: wave-uniform loads of it
+// become scalar loads (the scalar cache is invalidated at every dispatch). Only for buffers
+// that no wave writes during the dispatch.
+typedef const __attribute__((address_space(4))) float cfloat;
+__device__ __forceinline__ cfloat *as_const(const float *p) { return (cfloat *)(uintptr_t)p; }
+
+// Dot of one TQ2_T block's 32 steps with 128 activations, given the 8 stream words; returns
+// the unscaled sum of codebook * x. X is either a uniform cfloat* (scalar loads) or an LDS
+// pointer.
+template <typename XP>
+__device__ __forceinline__ float tq2_block_dot(const uint32_t q[8], const uint32_t *book, XP x) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t qp = q[(i + 7) & 7];
+        const uint32_t p01 = tq2_pair01(q[i], qp), p23 = tq2_pair23(q[i]);
+        const uint32_t s[4] = {p01 & 0x7fffu, __builtin_amdgcn_ubfe(p01, 16, 15), p23 & 0x7fffu,
+                               __builtin_amdgcn_ubfe(p23, 16, 15)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t a0, a1;
+            cb_addr(s[j], a0, a1);
+            const uint32_t w0 = lds_word(book, a0), w1 = lds_word(book, a1);
+            const XP xs = x + (i * 4 + j) * 4;
+            acc0 = fma_lo(w0, xs[0], acc0);
+            acc1 = fma_hi(w0, xs[1], acc1);
+            acc0 = fma_lo(w1, xs[2], acc0);
+            acc1 = fma_hi(w1, xs[3], acc1);
+        }
+    }
+    return acc0 + acc1;
+}
+
+// Extracts the scale and the 8 aligned stream words of a 34-byte block that starts at byte
+// offset `off` (even) inside the 32-bit words d[] (d[0] holds bytes off & ~3 ..).
+// Blocks at offsets 0 mod 4 have their stream at 2 mod 4, and vice versa.
+__device__ __forceinline__ void tq2_unpack(const uint32_t *d, bool odd_half, float &scale, uint32_t q[8]) {
+    if (!odd_half) {  // block starts at a word boundary: scale = d0.lo, stream at byte 2
+        scale = gd_half(d[0] & 0xffffu);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(d[j + 1], d[j], 2);
+    } else {  // block starts at byte 2 of d0: scale = d0.hi, stream word-aligned at d1
+        scale = gd_half(d[0] >> 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = d[j + 1];
+    }
+}

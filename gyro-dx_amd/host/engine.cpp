@@ -1,0 +1,510 @@
+// MoE layer engine above the gyro_native ABI: resident experts in slot arenas, the reference
+// dispatch sequence of src/gpu_engine.zig:1052-1119, and the MI355X decode and grouped-GEMM
+// paths. C entry points are declared in include/gyro_moe.h.
+#include <dirent.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "device.h"
+#include "gyro_moe.h"
+
+namespace gyro {
+namespace {
+
+// src/gyro.zig:32-41.
+uint32_t block_bytes_of(uint32_t type_id) {
+    switch (type_id) {
+        case 144: return 34;
+        case 145: return 26;
+        case 146: return 30;
+        case 147: return 42;
+        case 148: return 50;
+        case 149: return 58;
+        case 150: return 22;
+        case 151: return 18;
+        default: return 0;
+    }
+}
+
+uint32_t bits(float v) {
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    return u;
+}
+
+constexpr uint32_t kNone = 0xffffffffu;
+constexpr uint64_t kArenaLimit = 2ull << 30;  // src/gpu_engine.zig:601
+constexpr uint32_t kMaxArenas = 8;            // src/gpu_engine.zig:617
+constexpr uint32_t kStagingBytes = 32u << 20;
+
+struct ExpertDesc {
+    uint64_t gate, up, down;
+    uint32_t types;
+    uint32_t pad;
+};
+static_assert(sizeof(ExpertDesc) == 32, "expert descriptor layout");
+
+struct Layer {
+    Buffer router, bias, signs, xtab;
+    bool has_bias = false, has_gate_signs = false, has_down_signs = false;
+    float scale = 0;
+    uint32_t type_id = 0;     // uniform Gyro type, 0 when projections mix types
+    uint32_t gate_bytes = 0;  // per projection, uniform types only
+    uint64_t base = 0;        // device address of expert 0's bundle; expert e at base + e * stride
+};
+
+std::vector<uint8_t> read_file(const std::string &path) {
+    std::ifstream f(path, std::ios::binary);
+    return std::vector<uint8_t>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+}
+
+}  // namespace
+
+class Engine {
+  public:
+    Device dev;
+    std::map<std::string, gd_pipeline *> pipes;
+    std::string error;
+    uint32_t max_tok = 0;
+    uint32_t E = 0, F = 0, NE = 0, U = 0;
+    std::vector<Layer> layers;
+    // Expert arenas (src/gpu_engine.zig:593-650).
+    std::vector<Buffer> arenas;
+    uint32_t slot_stride = 0, per_arena = 0, used_slots = 0;
+    Buffer lookup;
+    // Shared buffers.
+    Buffer staging, codebook, zeros;
+    Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
+    Buffer tokens, outputs;
+    uint32_t n_tokens = 0;
+    uint32_t parts = 0;
+
+    gd_pipeline *pipe(const char *name) {
+        auto it = pipes.find(name);
+        if (it == pipes.end()) throw NativeError(-1, std::string("pipeline missing: ") + name);
+        return it->second;
+    }
+
+    void dispatch(const char *name, const std::vector<uint32_t> &c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
+        dev.dispatch(pipe(name), c.data(), (uint32_t)c.size(), x, y, z);
+    }
+
+    void load_kernels(const std::string &dir) {
+        DIR *d = opendir(dir.c_str());
+        if (!d) throw NativeError(-1, "kernel directory not found: " + dir);
+        while (dirent *ent = readdir(d)) {
+            std::string name = ent->d_name;
+            if (name.size() > 3 && name.compare(name.size() - 3, 3, ".co") == 0) {
+                std::vector<uint8_t> code = read_file(dir + "/" + name);
+                pipes[name.substr(0, name.size() - 3)] = dev.pipeline(code);
+            }
+        }
+        closedir(d);
+    }
+
+    // Copies host bytes into a device buffer through the mapped staging buffer and the
+    // bit-exact copy of the elementwise pipeline (as src/gpu_engine.zig:447-461 uploads the
+    // codebook).
+    void upload(const Buffer &dst, uint64_t dst_off, const void *src, uint64_t bytes) {
+        if (bytes % 4 || dst_off % 4) throw NativeError(-1, "upload must be word aligned");
+        const uint8_t *s = static_cast<const uint8_t *>(src);
+        while (bytes) {
+            const uint64_t chunk = std::min<uint64_t>(bytes, kStagingBytes);
+            std::memcpy(staging.mapped, s, chunk);
+            const uint32_t words = (uint32_t)(chunk / 4);
+            dev.begin();
+            dispatch("ew", {staging.uav, 0, 0, staging.uav, 0, 0, dst.uav, (uint32_t)(dst_off / 4), 0, words, 1, 5},
+                     (words + 255) / 256);
+            dev.wait(dev.submit());
+            s += chunk;
+            dst_off += chunk;
+            bytes -= chunk;
+        }
+    }
+
+    void fill_zero(const Buffer &dst) {
+        const uint32_t words = (uint32_t)(dst.bytes / 4);
+        uint32_t done = 0;
+        dev.begin();
+        while (done < words) {
+            const uint32_t n = std::min<uint32_t>(words - done, 1u << 16);
+            // y = a + b over a zero host row: the zero-filled staging buffer head.
+            dispatch("ew", {zeros.uav, 0, 0, zeros.uav, 0, 0, dst.uav, done, 0, n, 1, 5}, (n + 255) / 256);
+            done += n;
+        }
+        dev.wait(dev.submit());
+    }
+
+    void create(const std::string &kernel_dir, uint32_t adapter, uint32_t tokens_per_call) {
+        max_tok = tokens_per_call;
+        dev.init(adapter);
+        load_kernels(kernel_dir);
+        staging = dev.buffer(kStagingBytes, Kind::host);
+        zeros = dev.buffer(1u << 18, Kind::host);  // stays zero: the source of fills
+        codebook = dev.buffer(8192, Kind::device);
+        std::vector<uint8_t> book = read_file(kernel_dir + "/../../data/gyro_codebook.f16");
+        if (book.size() != 8192) throw NativeError(-1, "codebook must hold 8192 bytes");
+        upload(codebook, 0, book.data(), 8192);
+    }
+
+    void allocate_activations() {
+        const uint64_t T = max_tok, f = 4;
+        x_in = dev.buffer(T * E * f, Kind::device);
+        router_out = dev.buffer(T * NE * f, Kind::device);
+        ids = dev.buffer(T * U * 4, Kind::device);
+        weights = dev.buffer(T * U * f, Kind::device);
+        table = dev.buffer(T * U * 24, Kind::device);
+        xh = dev.buffer(T * E * f, Kind::device);
+        gu = dev.buffer(T * U * 2 * F * f, Kind::device);
+        parts = E / 1024 ? E / 1024 : 1;
+        gu_part = dev.buffer(parts * T * U * 2 * F * f, Kind::device);
+        act = dev.buffer(T * U * F * f, Kind::device);
+        down = dev.buffer(T * U * E * f, Kind::device);
+        out = dev.buffer(T * E * f, Kind::device);
+        // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
+        Buffer z = dev.buffer(T * E * f, Kind::device);
+        fill_zero(z);
+        sh_zero = z;
+    }
+    Buffer sh_zero;
+
+    uint32_t add_layer(const gm_layer_desc &d) {
+        if (layers.empty()) {
+            E = d.E; F = d.F; NE = d.n_expert; U = d.n_used;
+            if (!E || !F || E % 128 || F % 128 || NE == 0 || NE > 512 || U == 0 || U > 16 || U > NE)
+                throw NativeError(-1, "unsupported layer shape");
+            allocate_activations();
+        } else if (d.E != E || d.F != F || d.n_expert != NE || d.n_used != U) {
+            throw NativeError(-1, "layers of one engine must share their shape");
+        }
+        const uint32_t il = (uint32_t)layers.size();
+        Layer L;
+        L.scale = d.expert_weights_scale;
+        // Per-expert projection sizes and the slot stride (256-byte aligned bundles).
+        std::vector<uint64_t> gb(NE), ub(NE), db(NE);
+        uint64_t max_bundle = 0;
+        bool uniform = true;
+        for (uint32_t e = 0; e < NE; ++e) {
+            const uint32_t tg = d.types[e * 3], tu = d.types[e * 3 + 1], td = d.types[e * 3 + 2];
+            if (!block_bytes_of(tg) || !block_bytes_of(tu) || !block_bytes_of(td))
+                throw NativeError(-1, "unsupported Gyro type");
+            gb[e] = (uint64_t)F * (E / 128) * block_bytes_of(tg);
+            ub[e] = (uint64_t)F * (E / 128) * block_bytes_of(tu);
+            db[e] = (uint64_t)E * (F / 128) * block_bytes_of(td);
+            max_bundle = std::max(max_bundle, gb[e] + ub[e] + db[e]);
+            if (tg != d.types[0] || tu != d.types[0] || td != d.types[0]) uniform = false;
+        }
+        L.type_id = uniform ? d.types[0] : 0;
+        L.gate_bytes = uniform ? (uint32_t)gb[0] : 0;
+        if (!slot_stride) {
+            slot_stride = (uint32_t)((max_bundle + 255) & ~uint64_t(255));
+            per_arena = (uint32_t)(kArenaLimit / slot_stride);
+            lookup = dev.buffer((uint64_t)kMaxArenas * per_arena * 4, Kind::host);
+        } else if (max_bundle > slot_stride) {
+            throw NativeError(-1, "expert bundle exceeds the slot stride of the first layer");
+        }
+        // A layer's bundles are contiguous in one arena, so kernels can address expert e as
+        // base + e * slot_stride.
+        if (used_slots % per_arena + NE > per_arena) used_slots += per_arena - used_slots % per_arena;
+        std::vector<ExpertDesc> desc(NE);
+        for (uint32_t e = 0; e < NE; ++e) {
+            const uint32_t slot = used_slots++;
+            const uint32_t ai = slot / per_arena;
+            if (ai >= kMaxArenas) throw NativeError(-1, "too many arenas");
+            while (arenas.size() <= ai)
+                // 256 bytes of slack: decoders read whole words past a row's last block.
+                arenas.push_back(dev.buffer((uint64_t)per_arena * slot_stride + 256, Kind::device));
+            const uint64_t off = (uint64_t)(slot % per_arena) * slot_stride;
+            const Buffer &arena = arenas[ai];
+            upload(arena, off, d.gate[e], gb[e]);
+            upload(arena, off + gb[e], d.up[e], ub[e]);
+            upload(arena, off + gb[e] + ub[e], d.down[e], db[e]);
+            lookup.words()[il * NE + e] = slot;
+            desc[e].gate = arena.gpu + off;
+            desc[e].up = arena.gpu + off + gb[e];
+            desc[e].down = arena.gpu + off + gb[e] + ub[e];
+            desc[e].types = d.types[e * 3] | (d.types[e * 3 + 1] << 8) | (d.types[e * 3 + 2] << 16);
+            desc[e].pad = 0;
+            if (e == 0) L.base = desc[0].gate;
+        }
+        L.xtab = dev.buffer(NE * sizeof(ExpertDesc), Kind::device);
+        upload(L.xtab, 0, desc.data(), NE * sizeof(ExpertDesc));
+        L.router = dev.buffer((uint64_t)NE * E * 4, Kind::device);
+        upload(L.router, 0, d.router, (uint64_t)NE * E * 4);
+        if (d.router_bias) {
+            L.has_bias = true;
+            L.bias = dev.buffer(NE * 4, Kind::device);
+            upload(L.bias, 0, d.router_bias, NE * 4);
+        }
+        std::vector<float> signs(E + F, 1.0f);
+        if (d.gate_signs) {
+            L.has_gate_signs = true;
+            std::memcpy(signs.data(), d.gate_signs, E * 4);
+        }
+        if (d.down_signs) {
+            L.has_down_signs = true;
+            std::memcpy(signs.data() + E, d.down_signs, F * 4);
+        }
+        L.signs = dev.buffer((E + F) * 4, Kind::device);
+        upload(L.signs, 0, signs.data(), (E + F) * 4);
+        layers.push_back(L);
+        return il;
+    }
+
+    // Reference dispatch sequence, src/gpu_engine.zig:1052-1119 (routed experts; no shared
+    // expert in these layers, so moe_combine adds sigmoid(0) * 0).
+    void ffn_reference(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
+                       uint32_t out_off) {
+        const Layer &L = layers.at(il);
+        if (!L.type_id) throw NativeError(-1, "the reference path needs one Gyro type per layer");
+        const uint32_t bb = block_bytes_of(L.type_id);
+        // Router logits, in chunks of 8 tokens (src/gpu_engine.zig:838-864); a bias is
+        // preloaded and accumulated (mode 1).
+        if (L.has_bias)
+            dispatch("ew", {L.bias.uav, 0, 0, L.bias.uav, 0, 0, router_out.uav, 0, NE, NE, n, 5},
+                     (NE * n + 255) / 256);
+        uint32_t rpw = 1;
+        while (NE / (8 * rpw * 2) >= 1024) rpw *= 2;
+        const uint32_t groups = (NE + 8 * rpw - 1) / (8 * rpw);
+        for (uint32_t done = 0; done < n; done += 8) {
+            const uint32_t m = std::min(n - done, 8u);
+            dispatch("mv_f32", {L.router.srv, 0, NE, E, x_uav, x_off + done * E, E, m, router_out.uav, done * NE,
+                                NE, L.has_bias ? 1u : 0u, 0, bits(1.0f), E * 4, rpw},
+                     groups);
+        }
+        if (L.has_gate_signs)
+            dispatch("rotate128", {x_uav, x_off, xh.uav, 0, L.signs.srv, 0, E, E}, E / 128, n);
+        else
+            dispatch("ew", {x_uav, x_off, E, x_uav, x_off, E, xh.uav, 0, E, E, n, 3}, (E * n + 255) / 256);
+        dev.barrier();
+        dispatch("moe_route", {router_out.uav, 0, NE, U, ids.uav, 0, weights.uav, 0, kNone, 0, bits(L.scale), n}, n);
+        dev.barrier();
+        const uint32_t n_slots = n * U;
+        std::vector<uint32_t> rs = {ids.uav, 0, n_slots, table.uav, lookup.uav, il * NE, per_arena, slot_stride,
+                                    L.gate_bytes, (uint32_t)arenas.size(), 0, 0};
+        for (uint32_t i = 0; i < 8; ++i) rs.push_back(i < arenas.size() ? arenas[i].srv : 0);
+        dispatch("moe_resolve", rs, (n_slots + 63) / 64);
+        dev.barrier();
+        dispatch("moe_gyro", {table.uav, codebook.srv, xh.uav, 0, E, gu.uav, 0, F, E, L.type_id, bb, 0, U, 0, 0, 0},
+                 (F + 31) / 32, n_slots, 2);
+        dev.barrier();
+        dispatch("moe_act", {gu.uav, 0, act.uav, 0, L.signs.srv, E, F, L.has_down_signs ? 1u : 0u}, n_slots);
+        dev.barrier();
+        dispatch("moe_gyro", {table.uav, codebook.srv, act.uav, 0, F, down.uav, 0, E, F, L.type_id, bb, 2, U, 1, 0, 0},
+                 (E + 31) / 32, n_slots, 1);
+        dev.barrier();
+        dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh_zero.uav, 0, sh_zero.uav, 0},
+                 (E + 255) / 256, n);
+        dev.barrier();
+    }
+
+    bool decode_supported(const Layer &L, uint32_t n) const {
+        return L.type_id == 144 && E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
+    }
+
+    // MI355X decode path: router + rotation, routed gate/up, down + combine.
+    void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
+                    int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
+        const Layer &L = layers.at(il);
+        if (!decode_supported(L, n))
+            throw NativeError(-1, "decode path needs TQ2_T, E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8");
+        const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
+        auto mark = [&](int which) {
+            if (bracket == which && marks) marks->push_back(dev.timestamp());
+        };
+        mark(1);
+        dispatch("moe_router", {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
+                                router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
+                 std::max(NE, E / 128));
+        mark(1);
+        mark(2);
+        dispatch("moe_decode_gu", {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
+                                   base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
+                 F / 64, 2 * parts, n * U);
+        mark(2);
+        mark(3);
+        dispatch("moe_decode_down", {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
+                                     2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E,
+                                     out_uav, out_off, E, F, U, n, parts, NE},
+                 E / 8, n);
+        mark(3);
+    }
+
+    void ffn(uint32_t path, uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
+             uint32_t out_off, int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
+        if (path == GM_PATH_REFERENCE)
+            ffn_reference(il, n, x_uav, x_off, out_uav, out_off);
+        else if (path == GM_PATH_DECODE)
+            ffn_decode(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
+        else
+            throw NativeError(-1, "path not available");
+    }
+
+    void forward(uint32_t il, uint32_t path, const float *x, uint32_t n, float *y) {
+        if (n == 0 || n > max_tok) throw NativeError(-1, "token count exceeds max_tok");
+        upload(x_in, 0, x, (uint64_t)n * E * 4);
+        dev.begin();
+        ffn(path, il, n, x_in.uav, 0, out.uav, 0);
+        dev.wait(dev.submit());
+        check(gd_readback(dev.ctx, out.handle, 0, n * E * 4, y, kTimeoutMs), "gd_readback");
+    }
+};
+
+}  // namespace gyro
+
+using gyro::Engine;
+
+struct gm_engine {
+    Engine e;
+};
+
+template <typename Fn>
+static int guarded(gm_engine *g, Fn fn) {
+    if (!g) return -1;
+    try {
+        fn();
+        return 0;
+    } catch (const gyro::NativeError &err) {
+        g->e.error = err.what();
+        return err.code < 0 ? err.code : -1;
+    } catch (const std::exception &err) {
+        g->e.error = err.what();
+        return -1;
+    }
+}
+
+extern "C" int gm_create(const char *kernel_dir, uint32_t adapter, uint32_t max_tok, gm_engine **out) {
+    if (!kernel_dir || !out || !max_tok) return -1;
+    auto g = std::make_unique<gm_engine>();
+    int rc = guarded(g.get(), [&] { g->e.create(kernel_dir, adapter, max_tok); });
+    if (rc) {
+        std::fprintf(stderr, "gm_create: %s\n", g->e.error.c_str());
+        return rc;
+    }
+    *out = g.release();
+    return 0;
+}
+
+extern "C" void gm_destroy(gm_engine *g) {
+    if (!g) return;
+    g->e.dev.deinit();
+    delete g;
+}
+
+extern "C" const char *gm_last_error(gm_engine *g) { return g ? g->e.error.c_str() : "no engine"; }
+
+extern "C" int gm_add_layer(gm_engine *g, const gm_layer_desc *d, uint32_t *out_index) {
+    if (!d || !out_index) return -1;
+    return guarded(g, [&] { *out_index = g->e.add_layer(*d); });
+}
+
+extern "C" int gm_forward(gm_engine *g, uint32_t layer, uint32_t path, const float *x, uint32_t n, float *y) {
+    if (!x || !y) return -1;
+    return guarded(g, [&] { g->e.forward(layer, path, x, n, y); });
+}
+
+extern "C" int gm_last_routes(gm_engine *g, uint32_t n, uint32_t *ids, float *weights) {
+    if (!ids || !weights) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        gyro::check(gd_readback(e.dev.ctx, e.ids.handle, 0, n * e.U * 4, ids, gyro::kTimeoutMs), "gd_readback");
+        gyro::check(gd_readback(e.dev.ctx, e.weights.handle, 0, n * e.U * 4, weights, gyro::kTimeoutMs),
+                    "gd_readback");
+    });
+}
+
+extern "C" int gm_dequant(gm_engine *g, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
+                          uint32_t rows, float *out) {
+    if (!out) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        const gyro::Layer &L = e.layers.at(layer);
+        if (L.type_id != 144) throw gyro::NativeError(-1, "dequant check covers TQ2_T layers");
+        const uint32_t cols = proj == 2 ? e.F : e.E, total_rows = proj == 2 ? e.E : e.F;
+        if (expert >= e.NE || proj > 2 || row0 + rows > total_rows) throw gyro::NativeError(-1, "range");
+        gyro::Buffer o = e.dev.buffer((uint64_t)rows * cols * 4, gyro::Kind::device);
+        const uint32_t units = rows * (cols / 128);
+        e.dev.begin();
+        e.dispatch("moe_dequant", {L.xtab.srv, expert, proj, row0, rows, cols, e.codebook.srv, o.uav, 0},
+                   (units + 255) / 256);
+        e.dev.wait(e.dev.submit());
+        gyro::check(gd_readback(e.dev.ctx, o.handle, 0, rows * cols * 4, out, gyro::kTimeoutMs), "gd_readback");
+        e.dev.release(o);
+    });
+}
+
+extern "C" int gm_set_tokens(gm_engine *g, const float *x, uint32_t n_total) {
+    if (!x || !n_total) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        if (e.tokens.handle) e.dev.release(e.tokens);
+        if (e.outputs.handle) e.dev.release(e.outputs);
+        e.tokens = e.dev.buffer((uint64_t)n_total * e.E * 4, gyro::Kind::device);
+        e.outputs = e.dev.buffer((uint64_t)n_total * e.E * 4, gyro::Kind::device);
+        e.upload(e.tokens, 0, x, (uint64_t)n_total * e.E * 4);
+        e.n_tokens = n_total;
+    });
+}
+
+extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls,
+                                const uint32_t *layer_list, uint32_t n_layers, uint32_t bracket, double *device_ms,
+                                double *wall_ms, double *bracket_us) {
+    if (!layer_list || !n_layers || !device_ms || !wall_ms) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        if (!e.n_tokens || !batch || batch > e.max_tok || (uint64_t)batch * calls > e.n_tokens)
+            throw gyro::NativeError(-1, "run exceeds the uploaded tokens or max_tok");
+        const uint32_t per_submit = bracket ? 1000u : 4000u;
+        double dev = 0, br = 0;
+        uint64_t br_n = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint32_t first = 0; first < calls; first += per_submit) {
+            const uint32_t last = std::min(calls, first + per_submit);
+            std::vector<uint32_t> marks;
+            e.dev.begin();
+            marks.push_back(e.dev.timestamp());
+            for (uint32_t i = first; i < last; ++i) {
+                const uint32_t off = i * batch * e.E;
+                e.ffn(path, layer_list[i % n_layers], batch, e.tokens.uav, off, e.outputs.uav, off, (int)bracket,
+                      &marks);
+            }
+            marks.push_back(e.dev.timestamp());
+            e.dev.wait(e.dev.submit());
+            std::vector<uint64_t> ticks(marks.size());
+            const uint64_t freq = e.dev.timestamps(ticks.data(), (uint32_t)ticks.size());
+            dev += (double)(ticks.back() - ticks.front()) * 1e3 / (double)freq;
+            for (size_t j = 1; j + 2 < marks.size(); j += 2) {
+                br += (double)(ticks[j + 1] - ticks[j]) * 1e6 / (double)freq;
+                ++br_n;
+            }
+        }
+        *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        *device_ms = dev;
+        if (bracket_us) *bracket_us = br_n ? br / (double)br_n : 0.0;
+    });
+}
+
+extern "C" int gm_run(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, const uint32_t *layer_list,
+                      uint32_t n_layers, double *device_ms, double *wall_ms) {
+    return gm_run_bracketed(g, path, batch, calls, layer_list, n_layers, 0, device_ms, wall_ms, nullptr);
+}
+
+extern "C" int gm_read_outputs(gm_engine *g, float *y, uint32_t n_total) {
+    if (!y) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        if (n_total > e.n_tokens) throw gyro::NativeError(-1, "more outputs than tokens");
+        gyro::check(gd_readback(e.dev.ctx, e.outputs.handle, 0, (uint32_t)((uint64_t)n_total * e.E * 4), y,
+                                gyro::kTimeoutMs),
+                    "gd_readback");
+    });
+}

@@ -1,0 +1,84 @@
+/*
+ * gyro_moe: the host-side MoE layer engine above the gyro_native C ABI.
+ *
+ * The reference's host side is Zig (src/gpu.zig Device, src/gpu_engine.zig Engine.ffn); no Zig
+ * toolchain exists for this build, so the same dispatch logic is restated in C++ and exposed
+ * here for tests and benchmarks. Every GPU operation goes through gd_* calls.
+ *
+ * Paths (gm_forward, gm_run):
+ *   GM_PATH_REFERENCE  the reference dispatch sequence of src/gpu_engine.zig:1052-1119
+ *                      (mv_f32 router, rotate128, moe_route, moe_resolve, moe_gyro gate/up,
+ *                      moe_act, moe_gyro down, moe_combine), in passes of max_tok tokens.
+ *   GM_PATH_DECODE     the MI355X decode path: moe_router, moe_decode_gu, moe_decode_down.
+ *   GM_PATH_PREFILL    the MI355X grouped-GEMM path: moe_router, moe_sort, moe_ggemm_gu,
+ *                      moe_ggemm_down, moe_gather.
+ * All return 0 or a negative code; gm_last_error describes the failure.
+ */
+#ifndef GYRO_MOE_H
+#define GYRO_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define GM_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gm_engine gm_engine;
+
+enum { GM_PATH_REFERENCE = 0, GM_PATH_DECODE = 1, GM_PATH_PREFILL = 2 };
+
+/* One MoE layer in the reference's tensor layout (src/model.zig:115-123): per expert, gate and
+ * up hold F rows of E columns and down holds E rows of F columns, each row a run of Gyro blocks.
+ * types[e*3 + p] is the Gyro type id of expert e, projection p (0 gate, 1 up, 2 down). */
+typedef struct gm_layer_desc {
+    uint32_t E, F, n_expert, n_used;
+    float expert_weights_scale;
+    const float *router;      /* [n_expert][E] */
+    const float *router_bias; /* [n_expert] or NULL */
+    const float *gate_signs;  /* [E] or NULL */
+    const float *down_signs;  /* [F] or NULL */
+    const uint8_t *const *gate;
+    const uint8_t *const *up;
+    const uint8_t *const *down;
+    const uint32_t *types;
+} gm_layer_desc;
+
+/* Creates an engine on device `adapter`, loading every <name>.co pipeline in kernel_dir.
+ * max_tok bounds the tokens of one gm_forward/gm_run call (the reference uses passes of 64). */
+GM_API int gm_create(const char *kernel_dir, uint32_t adapter, uint32_t max_tok, gm_engine **out);
+GM_API void gm_destroy(gm_engine *e);
+GM_API const char *gm_last_error(gm_engine *e);
+/* Uploads a layer and returns its index. Layers of one engine share E, F, n_expert, n_used. */
+GM_API int gm_add_layer(gm_engine *e, const gm_layer_desc *desc, uint32_t *out_index);
+/* Runs n tokens (n <= max_tok) of x[n][E] through one layer on a path; writes out[n][E]. */
+GM_API int gm_forward(gm_engine *e, uint32_t layer, uint32_t path, const float *x, uint32_t n, float *out);
+/* Reads the routing of the last gm_forward: ids[n][n_used], weights[n][n_used]. */
+GM_API int gm_last_routes(gm_engine *e, uint32_t n, uint32_t *ids, float *weights);
+/* Decodes rows [row0, row0 + rows) of one expert projection to fp32 with the fast path's
+ * device decoder (bit-exact check of the in-kernel dequantisation). */
+GM_API int gm_dequant(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
+                      uint32_t rows, float *out);
+
+/* Benchmark harness: tokens[n_total][E] are uploaded once; gm_run then processes them in calls
+ * of `batch` tokens, call i using layer layers[i % n_layers], with every input already in device
+ * memory. Returns the device time between the first and last dispatch (ms), measured with
+ * events on the compute stream, and the host wall time of the loop (ms). */
+GM_API int gm_set_tokens(gm_engine *e, const float *tokens, uint32_t n_total);
+GM_API int gm_run(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, const uint32_t *layers,
+                  uint32_t n_layers, double *device_ms, double *wall_ms);
+/* As gm_run, and also brackets every launch of one kernel of the path with timestamps on the
+ * compute stream (bracket: 1 router, 2 gate/up, 3 down, 0 none); *bracket_us receives the mean
+ * time of one bracketed launch in microseconds. */
+GM_API int gm_run_bracketed(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls,
+                            const uint32_t *layers, uint32_t n_layers, uint32_t bracket,
+                            double *device_ms, double *wall_ms, double *bracket_us);
+/* Reads outputs[n_total][E] written by gm_run. */
+GM_API int gm_read_outputs(gm_engine *e, float *out, uint32_t n_total);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

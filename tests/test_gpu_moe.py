@@ -1,0 +1,151 @@
+"""GPU parity of the MoE layer paths against the CPU oracle, through the C ABI.
+
+Bar: dequantised weights and top-k expert ids bit-exact; layer outputs
+within relative RMS 2e-3 and cosine 0.9999 of the CPU path's fp32 results on the same seeded
+inputs. Top-k ids are compared for every token whose 8th/9th fp64 router probabilities are
+separated by more than 1e-5 relative (a near-tie can legitimately flip under a different fp32
+summation order); the test reports how many tokens that excludes (expected: none).
+"""
+import numpy as np
+import pytest
+
+from gyrodx import synth
+from gyrodx.engine import PATH_DECODE, PATH_REFERENCE, Engine
+
+pytestmark = pytest.mark.gpu
+REL_RMS = 2e-3
+COSINE = 0.9999
+
+
+@pytest.fixture(scope="module")
+def full_layer():
+    return synth.make_layer(101)  # hidden 2048, 256 experts, top-8, F 512, TQ2_T, signs
+
+
+@pytest.fixture(scope="module")
+def engine(full_layer):
+    eng = Engine(max_tok=64)
+    assert eng.add_layer(full_layer) == 0
+    yield eng
+    eng.close()
+
+
+@pytest.fixture(scope="module")
+def oracle_layer(full_layer, oracle_mod):
+    return oracle_mod.OracleLayer(full_layer)
+
+
+@pytest.fixture(scope="module")
+def tokens():
+    return synth.make_tokens(102, 16)
+
+
+@pytest.fixture(scope="module")
+def reference(oracle_layer, tokens):
+    return oracle_layer.forward(tokens, trace=True)
+
+
+def separable(oracle_layer, x, U, margin=1e-5):
+    logits = oracle_layer.router_f64(x)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    s = -np.sort(-p, axis=1)
+    return (s[:, U - 1] - s[:, U]) > margin * s[:, U - 1]
+
+
+def assert_close(oracle_mod, ref, out, what):
+    r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
+    print(f"{what}: rel_rms={r:.3e} cosine={c:.8f}")
+    assert r <= REL_RMS, (what, r)
+    assert c >= COSINE, (what, c)
+
+
+def test_fast_dequant_bit_exact(engine, full_layer, oracle_mod):
+    L = full_layer
+    for e, proj, row0, rows in [(0, 0, 0, 8), (17, 1, 100, 4), (255, 2, 2040, 8), (128, 2, 0, 16), (3, 0, 511, 1)]:
+        mats, cols = (L.gate, L.E) if proj == 0 else (L.up, L.E) if proj == 1 else (L.down, L.F)
+        got = engine.dequant(0, e, proj, row0, rows, cols)
+        for r in range(rows):
+            rc, ref = oracle_mod.decode_row(144, mats[e][row0 + r], cols)
+            assert rc == 0
+            np.testing.assert_array_equal(got[r].view(np.uint32), ref.view(np.uint32), err_msg=f"e{e} p{proj} r{row0 + r}")
+
+
+@pytest.mark.parametrize("path", [PATH_DECODE, PATH_REFERENCE])
+def test_single_token_parity(engine, full_layer, oracle_layer, tokens, reference, oracle_mod, path):
+    ref, tr = reference
+    ok = separable(oracle_layer, tokens, full_layer.n_used)
+    print("tokens excluded from the id check by the margin guard:", int((~ok).sum()))
+    for i in range(8):
+        out = engine.forward(0, tokens[i:i + 1], path)
+        ids, w = engine.last_routes(1)
+        if ok[i]:
+            np.testing.assert_array_equal(ids[0], tr["route_ids"][i])
+        np.testing.assert_allclose(w[0], tr["route_w"][i], rtol=1e-5, atol=1e-7)
+        assert_close(oracle_mod, ref[i], out[0], f"path {path} token {i}")
+
+
+def test_decode_batch_parity(engine, tokens, reference, oracle_mod):
+    ref, tr = reference
+    out = engine.forward(0, tokens[:4], PATH_DECODE)
+    ids, _ = engine.last_routes(4)
+    np.testing.assert_array_equal(ids, tr["route_ids"][:4])
+    assert_close(oracle_mod, ref[:4], out, "decode batch 4")
+
+
+def test_reference_path_batch_parity(engine, tokens, reference, oracle_mod):
+    ref, tr = reference
+    out = engine.forward(0, tokens, PATH_REFERENCE)
+    ids, _ = engine.last_routes(16)
+    np.testing.assert_array_equal(ids, tr["route_ids"])
+    assert_close(oracle_mod, ref, out, "reference path 16 tokens")
+
+
+def test_against_fp64_dense(engine, oracle_layer, tokens, reference, oracle_mod):
+    """The GPU output also meets the bar against the fp64 dense reference on the same routes."""
+    ref, tr = reference
+    d64 = oracle_layer.dense_f64(tokens[:4], tr["route_ids"][:4], tr["route_w"][:4])
+    out = engine.forward(0, tokens[:4], PATH_DECODE)
+    assert_close(oracle_mod, d64, out, "decode vs fp64")
+    assert_close(oracle_mod, d64, ref[:4], "oracle vs fp64")
+
+
+def test_run_harness_matches_forward(engine, tokens):
+    """gm_run over device-resident tokens reproduces gm_forward bit for bit."""
+    engine.set_tokens(tokens)
+    dev_ms, wall_ms, _ = engine.run(PATH_DECODE, 1, 16, [0])
+    outs = engine.read_outputs(16)
+    for i in (0, 7, 15):
+        one = engine.forward(0, tokens[i:i + 1], PATH_DECODE)
+        np.testing.assert_array_equal(outs[i].view(np.uint32), one[0].view(np.uint32))
+    assert dev_ms > 0 and wall_ms > 0
+
+
+def test_reference_path_other_types(oracle_mod):
+    """The reference dispatch sequence decodes every Gyro type (one type per layer)."""
+    for type_id in (147, 151):
+        L = synth.make_layer(300 + type_id, E=1024, F=256, n_expert=32, n_used=4, type_id=type_id)
+        eng = Engine(max_tok=8)
+        eng.add_layer(L)
+        x = synth.make_tokens(7, 5, L.E)
+        ref, tr = oracle_mod.OracleLayer(L).forward(x, trace=True)
+        out = eng.forward(0, x, PATH_REFERENCE)
+        ids, _ = eng.last_routes(5)
+        np.testing.assert_array_equal(ids, tr["route_ids"])
+        assert_close(oracle_mod, ref, out, f"type {type_id}")
+        eng.close()
+
+
+def test_zipf_bias_routing(oracle_mod):
+    """A router-logit bias (the skewed prefill workload) reaches both paths."""
+    L = synth.make_layer(55, E=1024, F=512, n_expert=64, n_used=8, zipf=1.1)
+    eng = Engine(max_tok=8)
+    eng.add_layer(L)
+    x = synth.make_tokens(56, 4, L.E)
+    ref, tr = oracle_mod.OracleLayer(L).forward(x, trace=True)
+    for path in (PATH_DECODE, PATH_REFERENCE):
+        out = eng.forward(0, x, path)
+        ids, _ = eng.last_routes(4)
+        np.testing.assert_array_equal(ids, tr["route_ids"])
+        assert_close(oracle_mod, ref, out, f"zipf path {path}")
+    eng.close()
