@@ -4,7 +4,7 @@
 // Constants (EwC): a_uav a_off a_stride b_uav b_off b_stride y_uav y_off y_stride n rows op.
 #include "gd_kernel.h"
 
-GD_PIPELINE(256) {
+GD_PIPELINE_NAMED(ew, 256) {
     const uint32_t n = a.c[9], rows = a.c[10], op = a.c[11];
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= n * rows) return;

@@ -14,9 +14,13 @@ struct GdArgs {
     uint32_t c[60];
 };
 
-#define GD_PIPELINE(WG)                                                   \
+// Defines the pipeline's kernel `NAME`, its workgroup size and the `gd_entry` string through
+// which gd_create_pipeline finds the kernel (so profilers show each pipeline by name).
+#define GD_PIPELINE_NAMED(NAME, WG)                                        \
     extern "C" __constant__ uint32_t gd_workgroup[3] = {WG, 1, 1};        \
-    extern "C" __global__ __launch_bounds__(WG) void gd_main(const GdArgs a)
+    extern "C" __constant__ char gd_entry[32] = #NAME;                     \
+    extern "C" __global__ __launch_bounds__(WG) void NAME(const GdArgs a)
+#define GD_PIPELINE(WG) GD_PIPELINE_NAMED(gd_main, WG)
 
 template <typename T>
 __device__ __forceinline__ T *gd_buf(const GdArgs &a, uint32_t index) {

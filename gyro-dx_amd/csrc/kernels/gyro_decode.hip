@@ -6,7 +6,7 @@
 // Invalid ids or spans produce no writes (the host validates before dispatch).
 #include "gd_kernel.h"
 
-GD_PIPELINE(64) {
+GD_PIPELINE_NAMED(gyro_decode, 64) {
     const uint32_t in_off = a.c[0], block_count = a.c[1], type_id = a.c[2], out_off = a.c[3];
     const uint8_t *input = gd_buf<const uint8_t>(a, a.c[4]);
     const uint16_t *book = gd_buf<const uint16_t>(a, a.c[5]);

@@ -52,7 +52,12 @@ __device__ __forceinline__ float fma_hi(uint32_t w, float x, float acc) {
 // become scalar loads (the scalar cache is invalidated at every dispatch). Only for buffers
 // that no wave writes during the dispatch.
 typedef const __attribute__((address_space(4))) float cfloat;
+typedef const __attribute__((address_space(4))) uint32_t cuint;
 __device__ __forceinline__ cfloat *as_const(const float *p) { return (cfloat *)(uintptr_t)p; }
+__device__ __forceinline__ cuint *as_const(const uint32_t *p) { return (cuint *)(uintptr_t)p; }
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
 // Dot of one TQ2_T block's 32 steps with 128 activations, given the 8 stream words; returns
 // the unscaled sum of codebook * x. X is either a uniform cfloat* (scalar loads) or an LDS
@@ -76,6 +81,30 @@ __device__ __forceinline__ float tq2_block_dot(const uint32_t q[8], const uint32
             acc1 = fma_hi(w0, xs[1], acc1);
             acc0 = fma_lo(w1, xs[2], acc0);
             acc1 = fma_hi(w1, xs[3], acc1);
+        }
+    }
+    return acc0 + acc1;
+}
+
+// As tq2_block_dot with activations as 64 packed binary16 pairs held in scalar registers
+// (xs[2t] = x[4t], x[4t+1]; xs[2t+1] = x[4t+2], x[4t+3]): two v_dot2_f32_f16 per step, fp32
+// accumulation of exact fp16 products.
+__device__ __forceinline__ float tq2_block_dot_h(const uint32_t q[8], const uint32_t *book, const uint32_t xs[64]) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t qp = q[(i + 7) & 7];
+        const uint32_t p01 = tq2_pair01(q[i], qp), p23 = tq2_pair23(q[i]);
+        const uint32_t s[4] = {p01 & 0x7fffu, __builtin_amdgcn_ubfe(p01, 16, 15), p23 & 0x7fffu,
+                               __builtin_amdgcn_ubfe(p23, 16, 15)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t a0, a1;
+            cb_addr(s[j], a0, a1);
+            const uint32_t w0 = lds_word(book, a0), w1 = lds_word(book, a1);
+            const int st = i * 4 + j;
+            acc0 = __builtin_amdgcn_fdot2(as_half2(w0), as_half2(xs[2 * st]), acc0, false);
+            acc1 = __builtin_amdgcn_fdot2(as_half2(w1), as_half2(xs[2 * st + 1]), acc1, false);
         }
     }
     return acc0 + acc1;

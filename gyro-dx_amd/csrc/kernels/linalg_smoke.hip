@@ -6,7 +6,7 @@
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-GD_PIPELINE(64) {
+GD_PIPELINE_NAMED(linalg_smoke, 64) {
     const _Float16 *A = gd_buf<const _Float16>(a, a.c[0]);
     const _Float16 *B = gd_buf<const _Float16>(a, a.c[1]);
     float *Cm = gd_buf<float>(a, a.c[2]);

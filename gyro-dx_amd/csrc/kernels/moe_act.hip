@@ -6,7 +6,7 @@
 // gate/up input layout: [slot][2][ff]; output [slot][ff].
 #include "fwht.h"
 
-GD_PIPELINE(128) {
+GD_PIPELINE_NAMED(moe_act, 128) {
     const float *GU = gd_buf<const float>(a, a.c[0]);
     float *O = gd_buf<float>(a, a.c[2]);
     const float *S = gd_buf<const float>(a, a.c[4]);

@@ -5,7 +5,7 @@
 // 7 dim 8 sh_uav 9 sh_off 10 shg_uav 11 shg_off.
 #include "gd_kernel.h"
 
-GD_PIPELINE(256) {
+GD_PIPELINE_NAMED(moe_combine, 256) {
     const uint32_t t = blockIdx.y, i = blockIdx.x * 256u + threadIdx.x, U = a.c[6], dim = a.c[7];
     if (i >= dim) return;
     const float *D = gd_buf<const float>(a, a.c[0]);

@@ -5,7 +5,7 @@
 // 6 codebook_srv 7 out_uav 8 out_off. TQ2_T only.
 #include "gyro_fast.h"
 
-GD_PIPELINE(256) {
+GD_PIPELINE_NAMED(moe_dequant, 256) {
     __shared__ uint32_t book[2048];
     const uint32_t *cb = gd_buf<const uint32_t>(a, a.c[6]);
     for (uint32_t i = threadIdx.x; i < 2048u; i += 256u) book[i] = cb[i];

@@ -11,7 +11,7 @@
 
 #define GYRO_MAX_COLS 8192
 
-GD_PIPELINE(256) {
+GD_PIPELINE_NAMED(moe_gyro, 256) {
     __shared__ uint32_t book[2048];
     __shared__ float xs[GYRO_MAX_COLS];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;

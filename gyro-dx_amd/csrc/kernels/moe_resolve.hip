@@ -6,7 +6,7 @@
 // 6 per_arena 7 slot_stride 8 gate_bytes 9 n_arenas 10-11 pad 12-19 arena srv indices.
 #include "gd_kernel.h"
 
-GD_PIPELINE(64) {
+GD_PIPELINE_NAMED(moe_resolve, 64) {
     const uint32_t k = blockIdx.x * 64u + threadIdx.x;
     if (k >= a.c[2]) return;
     const uint32_t e = gd_buf<const uint32_t>(a, a.c[0])[a.c[1] + k];

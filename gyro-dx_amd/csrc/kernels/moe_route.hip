@@ -14,7 +14,7 @@ __device__ __forceinline__ void arg_better(float v, uint32_t i, float &bv, uint3
     }
 }
 
-GD_PIPELINE(256) {
+GD_PIPELINE_NAMED(moe_route, 256) {
     __shared__ float p[512];
     __shared__ float red[4];
     __shared__ uint32_t redi[4];

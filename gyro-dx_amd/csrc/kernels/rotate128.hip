@@ -3,7 +3,7 @@
 // Constants (RotC): 0 x_uav 1 x_off 2 y_uav 3 y_off 4 signs_srv 5 signs_off 6 n 7 stride.
 #include "fwht.h"
 
-GD_PIPELINE(64) {
+GD_PIPELINE_NAMED(rotate128, 64) {
     const float *X = gd_buf<const float>(a, a.c[0]);
     float *Y = gd_buf<float>(a, a.c[2]);
     const float *S = gd_buf<const float>(a, a.c[4]);

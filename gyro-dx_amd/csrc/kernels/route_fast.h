@@ -11,7 +11,6 @@
 #pragma once
 #include "gd_kernel.h"
 
-#define RF_MAX_USED 16
 
 __device__ __forceinline__ uint32_t rf_order(float f) {
     const uint32_t u = gd_f32_bits(f);
@@ -22,73 +21,80 @@ __device__ __forceinline__ float rf_unorder(uint32_t k) {
 }
 
 template <int CTRL, int ROWS>
-__device__ __forceinline__ void rf_step(uint32_t &hi, uint32_t &lo) {
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, ROWS, 0xf, true);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, ROWS, 0xf, true);
-    const bool take = ohi > hi || (ohi == hi && olo > lo);
-    hi = take ? ohi : hi;
-    lo = take ? olo : lo;
+__device__ __forceinline__ uint64_t rf_step(uint64_t key) {
+    const uint32_t hi = (uint32_t)(key >> 32), lo = (uint32_t)key;
+    const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, ROWS, 0xf, true) << 32) |
+                       (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, ROWS, 0xf, true);
+    return o > key ? o : key;
 }
 
-// Wave maximum of 64-bit keys; every lane receives it (as scalars).
-__device__ __forceinline__ void rf_wave_max(uint32_t hi, uint32_t lo, uint32_t &mhi, uint32_t &mlo) {
-    rf_step<0x111, 0xf>(hi, lo);  // row_shr:1
-    rf_step<0x112, 0xf>(hi, lo);  // row_shr:2
-    rf_step<0x114, 0xf>(hi, lo);  // row_shr:4
-    rf_step<0x118, 0xf>(hi, lo);  // row_shr:8  -> lane 15 of each row holds the row maximum
-    rf_step<0x142, 0xa>(hi, lo);  // row_bcast:15 into rows 1 and 3
-    rf_step<0x143, 0xc>(hi, lo);  // row_bcast:31 into rows 2 and 3 -> lane 63 holds the maximum
-    mhi = __builtin_amdgcn_readlane(hi, 63);
-    mlo = __builtin_amdgcn_readlane(lo, 63);
+// Wave maximum of 64-bit keys; every lane receives it (as a scalar).
+__device__ __forceinline__ uint64_t rf_wave_max(uint64_t key) {
+    key = rf_step<0x111, 0xf>(key);  // row_shr:1
+    key = rf_step<0x112, 0xf>(key);  // row_shr:2
+    key = rf_step<0x114, 0xf>(key);  // row_shr:4
+    key = rf_step<0x118, 0xf>(key);  // row_shr:8  -> lane 15 of each row holds the row maximum
+    key = rf_step<0x142, 0xa>(key);  // row_bcast:15 into rows 1 and 3
+    key = rf_step<0x143, 0xc>(key);  // row_bcast:31 into rows 2 and 3 -> lane 63 holds the maximum
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), 63) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, 63);
 }
 
-// logits: the token's n_expert (<= 256 * PER / 4 ... <= 64 * PER) values. Returns ids and
-// weights (uniform across the wave).
+// Loads the lane's PER logits (n_expert <= 64 * PER) without branches; invalid slots get the
+// key 0, below every real key.
 template <int PER>
-__device__ __forceinline__ void wave_route_fast(const float *__restrict__ logits, uint32_t NE, uint32_t U, float scale,
-                                                uint32_t ids[RF_MAX_USED], float wts[RF_MAX_USED]) {
+__device__ __forceinline__ void rf_load(const float *__restrict__ logits, uint32_t NE, float v[PER]) {
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t khi[PER], klo[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const uint32_t i = lane + 64u * j;
-        khi[j] = i < NE ? rf_order(logits[i]) : 0u;
-        klo[j] = i < NE ? ~i : 0u;
+        v[j] = logits[i < NE ? i : NE - 1u];
+    }
+}
+
+// Top-U of the logits loaded by rf_load. Returns ids and weights (uniform across the wave).
+// U is a compile-time count (the number of experts used per token).
+template <int PER, int U>
+__device__ __forceinline__ void wave_route_fast(const float v[PER], uint32_t NE, float scale, uint32_t ids[U],
+                                                float wts[U]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const uint32_t i = lane + 64u * j;
+        key[j] = i < NE ? ((uint64_t)rf_order(v[j]) << 32) | (uint32_t)~i : 0ull;
     }
     // Sort the lane's candidates in descending key order (insertion network).
 #pragma unroll
     for (int a = 1; a < PER; ++a)
 #pragma unroll
         for (int b = a; b > 0; --b) {
-            const bool sw = khi[b] > khi[b - 1] || (khi[b] == khi[b - 1] && klo[b] > klo[b - 1]);
-            const uint32_t th = khi[b], tl = klo[b];
-            khi[b] = sw ? khi[b - 1] : khi[b];
-            klo[b] = sw ? klo[b - 1] : klo[b];
-            khi[b - 1] = sw ? th : khi[b - 1];
-            klo[b - 1] = sw ? tl : klo[b - 1];
+            const uint64_t hi = key[b] > key[b - 1] ? key[b] : key[b - 1];
+            const uint64_t lo = key[b] > key[b - 1] ? key[b - 1] : key[b];
+            key[b - 1] = hi;
+            key[b] = lo;
         }
-    float top[RF_MAX_USED];
-    for (uint32_t k = 0; k < U; ++k) {
-        uint32_t mhi, mlo;
-        rf_wave_max(khi[0], klo[0], mhi, mlo);
-        ids[k] = ~mlo;
-        top[k] = rf_unorder(mhi);
-        const bool mine = khi[0] == mhi && klo[0] == mlo;
+    float top[U];
 #pragma unroll
-        for (int j = 0; j + 1 < PER; ++j) {
-            khi[j] = mine ? khi[j + 1] : khi[j];
-            klo[j] = mine ? klo[j + 1] : klo[j];
-        }
-        khi[PER - 1] = mine ? 0u : khi[PER - 1];
-        klo[PER - 1] = mine ? 0u : klo[PER - 1];
+    for (int k = 0; k < U; ++k) {
+        const uint64_t m = rf_wave_max(key[0]);
+        ids[k] = ~(uint32_t)m;
+        top[k] = rf_unorder((uint32_t)(m >> 32));
+        const bool mine = key[0] == m;
+#pragma unroll
+        for (int j = 0; j + 1 < PER; ++j) key[j] = mine ? key[j + 1] : key[j];
+        key[PER - 1] = mine ? 0ull : key[PER - 1];
     }
     float total = 0.f;
-    for (uint32_t k = 0; k < U; ++k) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
         wts[k] = expf(top[k] - top[0]);
         total += wts[k];
     }
-    for (uint32_t k = 0; k < U; ++k) {
-        float w = wts[k] / total;
+    const float inv = 1.0f / total;
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        float w = wts[k] * inv;
         if (scale != 0.f && scale != 1.f) w *= scale;
         wts[k] = w;
     }

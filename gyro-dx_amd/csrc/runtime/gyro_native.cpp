@@ -474,7 +474,15 @@ static gd_result load_pipeline(gd_context *c, const void *code, size_t bytes, gd
     if (!elf && !bundle) return kInvalidArg;
     GD_HIP(hipSetDevice(c->device));
     GD_HIP(hipModuleLoadData(&p->module, code));
-    hipError_t e = hipModuleGetFunction(&p->function, p->module, "gd_main");
+    // The kernel is named by the module's gd_entry string (gd_main when absent).
+    char entry[33] = "gd_main";
+    hipDeviceptr_t name_ptr = nullptr;
+    size_t name_bytes = 0;
+    if (hipModuleGetGlobal(&name_ptr, &name_bytes, p->module, "gd_entry") == hipSuccess && name_bytes == 32) {
+        if (hipMemcpyDtoH(entry, name_ptr, 32) != hipSuccess) entry[0] = 0;
+        entry[32] = 0;
+    }
+    hipError_t e = hipModuleGetFunction(&p->function, p->module, entry);
     if (e != hipSuccess) {
         hipModuleUnload(p->module);
         p->module = nullptr;

@@ -10,8 +10,9 @@
  *  - Resources are device memory (hipMalloc) or pinned, mapped host memory (hipHostMalloc).
  *    Each receives two indices (SRV and UAV) into a device-resident table of 65,536 base
  *    pointers; both indices name the same memory.
- *  - A pipeline is a gfx950 code object exporting `gd_main(GdArgs)` and a `gd_workgroup[3]`
- *    constant; GdArgs is {const uint64_t *table; uint32_t constants[60];}.
+ *  - A pipeline is a gfx950 code object exporting one kernel taking GdArgs, a `gd_workgroup[3]`
+ *    constant and a `gd_entry` string naming the kernel (default `gd_main`); GdArgs is
+ *    {const uint64_t *table; uint32_t constants[60];}.
  *  - gd_dispatch launches immediately on the compute stream; gd_barrier is a no-op because
  *    the stream is in order; gd_submit records an event and returns its ticket.
  *  - File reads use pread into pinned staging and asynchronous copies on the copy stream.
@@ -121,7 +122,7 @@ GD_API gd_result gd_validate_gyro(gd_context *context, const void *code, size_t 
 GD_API gd_result gd_create_resource(gd_context *context, uint64_t bytes, uint32_t kind,
     gd_buffer **out_buffer, gd_buffer_info *out_info);
 /* Replaces gd_create_pipeline (:849-864): code is a gfx950 code object (ELF or offload
- * bundle) exporting gd_main and gd_workgroup. */
+ * bundle) exporting its kernel, gd_entry and gd_workgroup. */
 GD_API gd_result gd_create_pipeline(gd_context *context, const void *code, size_t code_bytes,
     gd_pipeline **out_pipeline);
 /* Replaces gd_release_pipeline (:866-872). */
