@@ -6,6 +6,7 @@
 // SRV/UAV indices kernels receive in their constants, and hipEvents as fence tickets.
 #include "gyro_native.h"
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <fcntl.h>
@@ -526,7 +527,8 @@ extern "C" gd_result gd_release_pipeline(gd_context *c, gd_pipeline *p, uint32_t
 }
 
 static gd_result launch(gd_context *c, gd_pipeline *p, const uint64_t *table, const uint32_t *constants,
-                        uint32_t count, uint32_t x, uint32_t y, uint32_t z, hipStream_t stream) {
+                        uint32_t count, uint32_t x, uint32_t y, uint32_t z, hipStream_t stream,
+                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr) {
     GdArgs args;
     args.table = table;
     std::memset(args.c, 0, sizeof(args.c));
@@ -534,6 +536,11 @@ static gd_result launch(gd_context *c, gd_pipeline *p, const uint64_t *table, co
     size_t size = sizeof(args);
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
                       HIP_LAUNCH_PARAM_END};
+    if (start) {
+        GD_HIP(hipExtModuleLaunchKernel(p->function, x * p->block[0], y * p->block[1], z * p->block[2], p->block[0],
+                                        p->block[1], p->block[2], 0, stream, nullptr, config, start, stop, 0));
+        return kOk;
+    }
     GD_HIP(hipModuleLaunchKernel(p->function, x, y, z, p->block[0], p->block[1], p->block[2], 0,
                                  stream, nullptr, config));
     return kOk;
@@ -732,6 +739,32 @@ extern "C" gd_result gd_dispatch(gd_context *c, gd_pipeline *p, const uint32_t *
     return launch(c, p, c->table, constants, count, x, y, z, c->compute);
 }
 
+// Reserves the next timestamp slot of the recording (events of a completed submission only).
+static gd_result take_timestamp(gd_context *c, uint32_t *index) {
+    if (c->ts_count >= kMaxTimestamps) return kOutOfMemory;
+    while (c->ts_pool.size() <= c->ts_count) {
+        hipEvent_t e = nullptr;
+        GD_HIP(hipEventCreate(&e));
+        c->ts_pool.push_back(e);
+    }
+    if (c->ts_ticket) GD_TRY(c->wait_compute(c->ts_ticket, kInfinite));
+    c->ts_ticket = 0;
+    *index = c->ts_count++;
+    return kOk;
+}
+
+extern "C" gd_result gd_dispatch_timed(gd_context *c, gd_pipeline *p, const uint32_t *constants, uint32_t count,
+                                       uint32_t x, uint32_t y, uint32_t z, uint32_t *out_index) {
+    if (!c || !p || p->owner != c || !c->recording || count > kMaxConstants || (count && !constants) || !x ||
+        !y || !z || x > 65535 || y > 65535 || z > 65535 || !out_index)
+        return kInvalidArg;
+    uint32_t first = 0, second = 0;
+    GD_TRY(take_timestamp(c, &first));
+    GD_TRY(take_timestamp(c, &second));
+    *out_index = first;
+    return launch(c, p, c->table, constants, count, x, y, z, c->compute, c->ts_pool[first], c->ts_pool[second]);
+}
+
 extern "C" gd_result gd_barrier(gd_context *c) {
     if (!c || !c->recording) return kInvalidArg;
     return kOk;  // the compute stream executes dispatches in order
@@ -739,17 +772,9 @@ extern "C" gd_result gd_barrier(gd_context *c) {
 
 extern "C" gd_result gd_timestamp(gd_context *c, uint32_t *out_index) {
     if (!c || !out_index || !c->recording) return kInvalidArg;
-    if (c->ts_count >= kMaxTimestamps) return kOutOfMemory;
-    while (c->ts_pool.size() <= c->ts_count) {
-        hipEvent_t e = nullptr;
-        GD_HIP(hipEventCreate(&e));
-        c->ts_pool.push_back(e);
-    }
     // Events of the previous submission are reused only once it completed.
-    if (c->ts_ticket) GD_TRY(c->wait_compute(c->ts_ticket, kInfinite));
-    c->ts_ticket = 0;
-    *out_index = c->ts_count;
-    GD_HIP(hipEventRecord(c->ts_pool[c->ts_count++], c->compute));
+    GD_TRY(take_timestamp(c, out_index));
+    GD_HIP(hipEventRecord(c->ts_pool[*out_index], c->compute));
     return kOk;
 }
 

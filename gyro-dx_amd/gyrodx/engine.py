@@ -39,8 +39,9 @@ def lib() -> C.CDLL:
         L.gm_last_routes.argtypes = [vp, u32, C.POINTER(u32), f32p]
         L.gm_dequant.argtypes = [vp, u32, u32, u32, u32, u32, f32p]
         L.gm_set_tokens.argtypes = [vp, f32p, u32]
-        L.gm_run.argtypes = [vp, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double), C.POINTER(C.c_double)]
-        L.gm_run_bracketed.argtypes = [vp, u32, u32, u32, C.POINTER(u32), u32, u32, C.POINTER(C.c_double),
+        L.gm_run.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
+                             C.POINTER(C.c_double)]
+        L.gm_run_bracketed.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, u32, C.POINTER(C.c_double),
                                        C.POINTER(C.c_double), C.POINTER(C.c_double)]
         L.gm_read_outputs.argtypes = [vp, f32p, u32]
         _lib = L
@@ -127,11 +128,13 @@ class Engine:
         self._check(lib().gm_set_tokens(self._h, _f32p(x), x.shape[0]), "gm_set_tokens")
         self.n_tokens = x.shape[0]
 
-    def run(self, path: int, batch: int, calls: int, layers, bracket: int = 0):
+    def run(self, path: int, batch: int, calls: int, layers, bracket: int = 0, first: int = 0):
+        """Processes `calls` calls of `batch` device-resident tokens from token `first`; returns
+        (device ms, wall ms, mean duration in us of the bracketed kernel's launches)."""
         arr = (C.c_uint32 * len(layers))(*layers)
         dev, wall, br = C.c_double(), C.c_double(), C.c_double()
-        self._check(lib().gm_run_bracketed(self._h, path, batch, calls, arr, len(layers), bracket, C.byref(dev),
-                                           C.byref(wall), C.byref(br)), "gm_run")
+        self._check(lib().gm_run_bracketed(self._h, path, batch, calls, first, arr, len(layers), bracket,
+                                           C.byref(dev), C.byref(wall), C.byref(br)), "gm_run")
         return dev.value, wall.value, br.value
 
     def read_outputs(self, n: int) -> np.ndarray:

@@ -19,6 +19,8 @@ SYMBOLS = [
     "gd_create_resource", "gd_create_pipeline", "gd_release_pipeline", "gd_begin", "gd_dispatch",
     "gd_barrier", "gd_timestamp", "gd_submit", "gd_wait_compute", "gd_read_timestamps",
     "gd_queue_wait_storage", "gd_read_ranges_after", "gd_release_buffer", "gd_release_file", "gd_destroy",
+    # Extension without a counterpart in the reference ABI (timed dispatch for profiling).
+    "gd_dispatch_timed",
 ]
 
 
@@ -84,6 +86,7 @@ def lib() -> C.CDLL:
             "gd_release_buffer": [vp, vp, u32],
             "gd_release_file": [vp, vp, u32],
             "gd_destroy": [vp, u32],
+            "gd_dispatch_timed": [vp, vp, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(u32)],
         }
         for name, args in sig.items():
             f = getattr(L, name)

@@ -65,6 +65,13 @@ void Device::dispatch(gd_pipeline *p, const uint32_t *constants, uint32_t count,
     check(gd_dispatch(ctx, p, constants, count, x, y, z), "gd_dispatch");
 }
 
+uint32_t Device::dispatch_timed(gd_pipeline *p, const uint32_t *constants, uint32_t count, uint32_t x, uint32_t y,
+                                uint32_t z) {
+    uint32_t index = 0;
+    check(gd_dispatch_timed(ctx, p, constants, count, x, y, z, &index), "gd_dispatch_timed");
+    return index;
+}
+
 void Device::barrier() { check(gd_barrier(ctx), "gd_barrier"); }
 
 uint32_t Device::timestamp() {

@@ -48,6 +48,9 @@ class Device {
     void begin();
     void dispatch(gd_pipeline *p, const uint32_t *constants, uint32_t count, uint32_t x, uint32_t y,
                   uint32_t z);
+    // Dispatch whose own start and end become timestamps (returns the first index).
+    uint32_t dispatch_timed(gd_pipeline *p, const uint32_t *constants, uint32_t count, uint32_t x, uint32_t y,
+                            uint32_t z);
     void barrier();
     uint32_t timestamp();
     uint64_t submit();

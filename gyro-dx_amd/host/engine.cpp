@@ -98,6 +98,19 @@ class Engine {
         dev.dispatch(pipe(name), c.data(), (uint32_t)c.size(), x, y, z);
     }
 
+    // Dispatch that records its own start and end timestamps when `timed` is set (their
+    // indices are appended to marks).
+    void dispatch_maybe_timed(bool timed, std::vector<uint32_t> *marks, const char *name,
+                              const std::vector<uint32_t> &c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
+        if (timed && marks) {
+            const uint32_t first = dev.dispatch_timed(pipe(name), c.data(), (uint32_t)c.size(), x, y, z);
+            marks->push_back(first);
+            marks->push_back(first + 1);
+        } else {
+            dispatch(name, c, x, y, z);
+        }
+    }
+
     void load_kernels(const std::string &dir) {
         DIR *d = opendir(dir.c_str());
         if (!d) throw NativeError(-1, "kernel directory not found: " + dir);
@@ -318,25 +331,19 @@ class Engine {
         if (!decode_supported(L, n))
             throw NativeError(-1, "decode path needs TQ2_T, E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
-        auto mark = [&](int which) {
-            if (bracket == which && marks) marks->push_back(dev.timestamp());
-        };
-        mark(1);
-        dispatch("moe_router", {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
-                                router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
-                 std::max(NE, E / 128));
-        mark(1);
-        mark(2);
-        dispatch("moe_decode_gu", {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
-                                   base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
-                 F / 64, 2 * parts, n * U);
-        mark(2);
-        mark(3);
-        dispatch("moe_decode_down", {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
-                                     2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E,
-                                     out_uav, out_off, E, F, U, n, parts, NE},
-                 E / 8, n);
-        mark(3);
+        dispatch_maybe_timed(bracket == 1, marks, "moe_router",
+                             {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
+                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
+                             std::max(NE, E / 128));
+        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
+                             {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0, base_lo,
+                              base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
+                             F / 64, 2 * parts, n * U);
+        dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
+                             {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
+                              2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
+                              out_off, E, F, U, n, parts, NE},
+                             E / 8, n);
     }
 
     void ffn(uint32_t path, uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
@@ -455,13 +462,13 @@ extern "C" int gm_set_tokens(gm_engine *g, const float *x, uint32_t n_total) {
     });
 }
 
-extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls,
+extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first_token,
                                 const uint32_t *layer_list, uint32_t n_layers, uint32_t bracket, double *device_ms,
                                 double *wall_ms, double *bracket_us) {
     if (!layer_list || !n_layers || !device_ms || !wall_ms) return -1;
     return guarded(g, [&] {
         Engine &e = g->e;
-        if (!e.n_tokens || !batch || batch > e.max_tok || (uint64_t)batch * calls > e.n_tokens)
+        if (!e.n_tokens || !batch || batch > e.max_tok || (uint64_t)first_token + (uint64_t)batch * calls > e.n_tokens)
             throw gyro::NativeError(-1, "run exceeds the uploaded tokens or max_tok");
         const uint32_t per_submit = bracket ? 1000u : 4000u;
         double dev = 0, br = 0;
@@ -473,7 +480,7 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
             e.dev.begin();
             marks.push_back(e.dev.timestamp());
             for (uint32_t i = first; i < last; ++i) {
-                const uint32_t off = i * batch * e.E;
+                const uint32_t off = (first_token + i * batch) * e.E;
                 e.ffn(path, layer_list[i % n_layers], batch, e.tokens.uav, off, e.outputs.uav, off, (int)bracket,
                       &marks);
             }
@@ -493,9 +500,9 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
     });
 }
 
-extern "C" int gm_run(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, const uint32_t *layer_list,
-                      uint32_t n_layers, double *device_ms, double *wall_ms) {
-    return gm_run_bracketed(g, path, batch, calls, layer_list, n_layers, 0, device_ms, wall_ms, nullptr);
+extern "C" int gm_run(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first_token,
+                      const uint32_t *layer_list, uint32_t n_layers, double *device_ms, double *wall_ms) {
+    return gm_run_bracketed(g, path, batch, calls, first_token, layer_list, n_layers, 0, device_ms, wall_ms, nullptr);
 }
 
 extern "C" int gm_read_outputs(gm_engine *g, float *y, uint32_t n_total) {

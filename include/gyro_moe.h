@@ -62,17 +62,18 @@ GM_API int gm_last_routes(gm_engine *e, uint32_t n, uint32_t *ids, float *weight
 GM_API int gm_dequant(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
                       uint32_t rows, float *out);
 
-/* Benchmark harness: tokens[n_total][E] are uploaded once; gm_run then processes them in calls
- * of `batch` tokens, call i using layer layers[i % n_layers], with every input already in device
- * memory. Returns the device time between the first and last dispatch (ms), measured with
- * events on the compute stream, and the host wall time of the loop (ms). */
+/* Benchmark harness: tokens[n_total][E] are uploaded once; gm_run then processes `calls` calls
+ * of `batch` tokens starting at token `first`, call i using layer layers[i % n_layers], with
+ * every input already in device memory. Returns the device time between the first and last
+ * dispatch (ms), measured with events on the compute stream, and the host wall time of the loop
+ * including the final wait (ms). */
 GM_API int gm_set_tokens(gm_engine *e, const float *tokens, uint32_t n_total);
-GM_API int gm_run(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, const uint32_t *layers,
-                  uint32_t n_layers, double *device_ms, double *wall_ms);
-/* As gm_run, and also brackets every launch of one kernel of the path with timestamps on the
- * compute stream (bracket: 1 router, 2 gate/up, 3 down, 0 none); *bracket_us receives the mean
- * time of one bracketed launch in microseconds. */
-GM_API int gm_run_bracketed(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls,
+GM_API int gm_run(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first,
+                  const uint32_t *layers, uint32_t n_layers, double *device_ms, double *wall_ms);
+/* As gm_run, and also times every launch of one kernel of the path by its own start and end
+ * (gd_dispatch_timed; bracket: 1 router, 2 gate/up, 3 down, 0 none); *bracket_us receives the
+ * mean duration of one launch in microseconds. */
+GM_API int gm_run_bracketed(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first,
                             const uint32_t *layers, uint32_t n_layers, uint32_t bracket,
                             double *device_ms, double *wall_ms, double *bracket_us);
 /* Reads outputs[n_total][E] written by gm_run. */

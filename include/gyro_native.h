@@ -156,6 +156,13 @@ GD_API gd_result gd_release_file(gd_context *context, gd_file *file, uint32_t ti
 /* Replaces gd_destroy (:752-759). */
 GD_API gd_result gd_destroy(gd_context *context, uint32_t timeout_ms);
 
+/* Extension with no counterpart in the reference ABI, for profilers and benchmarks: as
+ * gd_dispatch, and records the dispatch's own start and end as timestamps *out_index and
+ * *out_index + 1 of the recording (read with gd_read_timestamps), without adding packets
+ * between dispatches. */
+GD_API gd_result gd_dispatch_timed(gd_context *context, gd_pipeline *pipeline, const uint32_t *constants,
+    uint32_t constant_count, uint32_t groups_x, uint32_t groups_y, uint32_t groups_z, uint32_t *out_index);
+
 #ifdef __cplusplus
 }
 #endif

@@ -421,6 +421,24 @@ static void pool_run(pool *p, size_t count, size_t chunk, void *ctx, pool_fn fn)
     pthread_mutex_unlock(&p->mu);
 }
 
+/* The pool persists across calls (src/runtime.zig:135 creates one pool per runtime); it is
+ * rebuilt only when the requested thread count changes. */
+static pool g_pool;
+static uint32_t g_pool_threads = 0;
+static pthread_mutex_t g_pool_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static pool *pool_get(uint32_t threads) {
+    if (g_pool_threads != threads) {
+        if (g_pool_threads) pool_deinit(&g_pool);
+        if (pool_init(&g_pool, threads)) {
+            g_pool_threads = 0;
+            return NULL;
+        }
+        g_pool_threads = threads;
+    }
+    return &g_pool;
+}
+
 /* src/pool.zig:117-120. */
 static size_t chunk_for(const pool *p, size_t count, size_t min_chunk) {
     size_t target = count / ((p->workers + 1) * 4);
@@ -548,8 +566,13 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
     if (rc) return rc;
     if (n == 0) return GO_OK;
     const size_t E = l->E, F = l->F, U = l->n_used, NE = l->n_expert;
-    pool p;
-    if (pool_init(&p, threads ? threads : 1)) return GO_INVALID_SOURCE_LENGTH;
+    pthread_mutex_lock(&g_pool_mu);
+    pool *pp = pool_get(threads ? threads : 1);
+    if (!pp) {
+        pthread_mutex_unlock(&g_pool_mu);
+        return GO_INVALID_SOURCE_LENGTH;
+    }
+    pool *const pool_ptr = pp;
     float *logits = (float *)malloc(n * NE * sizeof(float));
     uint32_t *ids = (uint32_t *)malloc(n * U * sizeof(uint32_t));
     float *wts = (float *)malloc(n * U * sizeof(float));
@@ -562,7 +585,7 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
                  .down = down, .route_order = order};
 
     /* Router (src/engine.zig:526): matmul with chunkFor(rows, 8). */
-    pool_run(&p, NE, chunk_for(&p, NE, 8), &c, router_range);
+    pool_run(pool_ptr, NE, chunk_for(pool_ptr, NE, 8), &c, router_range);
     if (trace && trace->logits) memcpy(trace->logits, logits, n * NE * sizeof(float));
     /* Softmax, top-k, renormalisation (src/engine.zig:527-540). */
     for (size_t t = 0; t < n; ++t) {
@@ -593,7 +616,7 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
     for (size_t i = 0; i < n * U; ++i) order[fill[ids[i]]++] = (uint32_t)i;
     c.starts = starts;
     /* Phase 1 (src/engine.zig:567-602). */
-    pool_run(&p, NE * F, 16, &c, phase1);
+    pool_run(pool_ptr, NE * F, 16, &c, phase1);
     /* SwiGLU and the down-input rotation (src/engine.zig:603-607). */
     for (size_t slot = 0; slot < n * U; ++slot) {
         float *a = act + slot * F;
@@ -602,7 +625,7 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
         if (l->down_signs) go_rotate_f32signs(a, F, 128, l->down_signs);
     }
     /* Phase 2 (src/engine.zig:608-633). */
-    pool_run(&p, NE * E, 64, &c, phase2);
+    pool_run(pool_ptr, NE * E, 64, &c, phase2);
     /* Combine in k order (src/engine.zig:634-641). */
     for (size_t t = 0; t < n; ++t)
         for (size_t k = 0; k < U; ++k) {
@@ -631,17 +654,17 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
         c.mat_rows = SF;
         c.mat = l->sh_gate;
         c.y_out = sg;
-        pool_run(&p, SF, chunk_for(&p, SF, 8), &c, bf16_range);
+        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, bf16_range);
         c.mat = l->sh_up;
         c.y_out = su;
-        pool_run(&p, SF, chunk_for(&p, SF, 8), &c, bf16_range);
+        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, bf16_range);
         for (size_t i = 0; i < n * SF; ++i) sg[i] = go_silu(sg[i]) * su[i];
         c.y_in = sg;
         c.mat_cols = SF;
         c.mat_rows = E;
         c.mat = l->sh_down;
         c.y_out = sd;
-        pool_run(&p, E, chunk_for(&p, E, 8), &c, bf16_range);
+        pool_run(pool_ptr, E, chunk_for(pool_ptr, E, 8), &c, bf16_range);
         for (size_t t = 0; t < n; ++t) {
             float gate = l->sh_gate_inp ? go_sigmoid(go_dot_dense(l->sh_gate_inp, x + t * E, E))
                                         : l->sh_gate_const;
@@ -659,7 +682,7 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
     free(act);
     free(act_up);
     free(down);
-    pool_deinit(&p);
+    pthread_mutex_unlock(&g_pool_mu);
     return GO_OK;
 }
 
