@@ -25,6 +25,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -41,7 +42,48 @@ E, F, N_EXPERT, TOP_K = 2048, 512, 256, 8
 PROJ_BYTES = F * (E // 128) * 34  # 278,528 packed bytes per expert projection
 EXPERT_BYTES_PER_TOKEN = TOP_K * 3 * PROJ_BYTES  # 6,684,672
 GU_BYTES_PER_LAUNCH = TOP_K * 2 * PROJ_BYTES  # 4,456,448
-TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
+COPY_WORDS = 8 << 20  # calibration copy of the traffic probe: 32 MiB read, 32 MiB written
+
+
+def read_traffic():
+    """HBM bytes per moe_decode_gu launch from the committed counter summary (its
+    `bytes_per_launch:` line), or None when no summary is present."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    m = re.search(r"^bytes_per_launch:\s*(\d+)", TRAFFIC_FILE.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(reps: int) -> None:
+    """Launches the bit-exact 32-bit copy (ew op 5) over COPY_WORDS words `reps` times, device to
+    device, so that a counter pass sees FETCH_SIZE and WRITE_SIZE of a kernel of known traffic."""
+    import ctypes as C
+    from gyrodx import KERNEL_DIR, native
+    L = native.lib()
+    opts = native.Options(0, 0, 0, 32 << 20, 1024)
+    ctx = C.c_void_p()
+    native.check(L.gd_create(C.byref(opts), C.byref(ctx)), "gd_create")
+    code = (KERNEL_DIR / "ew.co").read_bytes()
+    pipe = C.c_void_p()
+    native.check(L.gd_create_pipeline(ctx, code, len(code), C.byref(pipe)), "gd_create_pipeline")
+    bufs = []
+    for _ in range(2):
+        h, info = C.c_void_p(), native.BufferInfo()
+        native.check(L.gd_create_resource(ctx, COPY_WORDS * 4, 0, C.byref(h), C.byref(info)), "gd_create_resource")
+        bufs.append((h, info))
+    (_, src), (_, dst) = bufs
+    cst = (C.c_uint32 * 12)(src.uav_index, 0, 0, src.uav_index, 0, 0, dst.uav_index, 0, 0, COPY_WORDS, 1, 5)
+    native.check(L.gd_begin(ctx, 60000), "gd_begin")
+    for _ in range(reps):
+        native.check(L.gd_dispatch(ctx, pipe, cst, 12, COPY_WORDS // 256, 1, 1), "gd_dispatch")
+    ticket = C.c_uint64()
+    native.check(L.gd_submit(ctx, C.byref(ticket)), "gd_submit")
+    native.check(L.gd_wait_compute(ctx, ticket, 60000), "gd_wait_compute")
+    for h, _ in bufs:
+        native.check(L.gd_release_buffer(ctx, h, 60000), "gd_release_buffer")
+    native.check(L.gd_release_pipeline(ctx, pipe, 60000), "gd_release_pipeline")
+    native.check(L.gd_destroy(ctx, 60000), "gd_destroy")
 
 
 def cpu_threads() -> int:
@@ -86,6 +128,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
+                         "copies of 32 MiB; prints the probe's shape and no benchmark line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -105,6 +150,14 @@ def main() -> int:
     # Warm-up on the first W tokens, then exactly K timed steps on the next K tokens; gm_run
     # returns after the device finished (synchronised on both sides).
     eng.run(PATH_DECODE, 1, args.warmup, layers, first=0)
+    if args.traffic_probe:
+        eng.run(PATH_DECODE, 1, args.steps, layers, first=args.warmup)
+        eng.close()
+        copy_calibration(20)
+        print(json.dumps({"probe": "traffic", "decode_tokens": n_tok, "gu_bytes_per_launch": GU_BYTES_PER_LAUNCH,
+                          "copy_bytes_read": COPY_WORDS * 4, "copy_bytes_written": COPY_WORDS * 4,
+                          "copy_launches": 20}), flush=True)
+        return 0
     dev_ms, wall_ms, _ = eng.run(PATH_DECODE, 1, args.steps, layers, first=args.warmup)
     gpu_out = eng.read_outputs(n_tok)[args.warmup:]
     # Roofline pass: the same steps, the dominant kernel timed by its own dispatch start and end.
@@ -114,9 +167,7 @@ def main() -> int:
 
     value = args.steps / (wall_ms / 1e3)
     achieved = GU_BYTES_PER_LAUNCH / (gu_us * 1e-6) / 1e9
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+    traffic = read_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 1),
