@@ -5,8 +5,32 @@
  * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it, and only as the
  * checker or the timed CPU baseline. The product (gyro-dx_amd/) never links or calls it.
  *
- * Every function cites the reference file:line it restates. Pinning of each function
- * (what fixes its output independently of this restatement) is listed in oracle/README.md.
+ * Every function cites the reference file:line it restates. What pins each function, that is
+ * what fixes its output independently of this restatement (tests named are under tests/):
+ *   go_init              codebook SHA-256 of src/gyro.zig:197-202 (test_codebook_hash).
+ *   go_type_info,        type table and sizes through the golden fixture's 8 types and
+ *   go_row_bytes         src/gyro.zig:204-214 (test_golden_decode_all_bits, test_fail_closed).
+ *   go_fp16_to_fp32      src/gyro.zig:216-224 edge bits and numpy's exact binary16 conversion
+ *                        (test_fp16_edges).
+ *   go_trellis_state,    all 65,536 value bits of tests/gyro_vectors.bin (512 blocks, 8 types,
+ *   go_decode_row        edge scales), the SPEC.md section 10 worked examples, and the vendored
+ *                        C decoder third_party/agention-gyro/src/tq_ref.c built into oracle/_ref
+ *                        (test_golden_decode_all_bits, test_spec_worked_examples,
+ *                        test_against_vendored_reference_decoder).
+ *   go_rotate,           rotation bit patterns of tests/gyro_vectors.bin, the closed form
+ *   go_unrotate,         H[r][c] = (-1)^popcount(r&c)/sqrt(b), H.H = I and dot invariance
+ *   go_rotate_f32signs   (test_golden_rotation_bits, test_rotation_closed_forms).
+ *   go_softmax, go_topk  brute-force fp64 sort with lower-index ties (test_topk_ties_and_brute_force).
+ *   go_dot_row,          fp64 dot of the strictly decoded row, to fp32 reduction tolerance
+ *   go_decode_row_fast,  (test_fused_dot_matches_strict_decoder); their exact bits follow the
+ *   go_dot_f32           reference's fast-math reductions and are parity unpinned bit-for-bit.
+ *   go_silu, go_sigmoid, an independent fp64 numpy model of the layer with planted-mistake
+ *   go_moe_ffn           checks (test_layer_matches_numpy_fp64, test_mixed_types_and_bias,
+ *                        test_counting_sort_invariants, test_layer_thread_count_invariant).
+ *   go_moe_dense_f64,    the same fp64 numpy model and numpy's x.W^T for the router logits
+ *   go_router_f64        (test_layer_matches_numpy_fp64).
+ *   go_dot_bf16,         parity unpinned: the shared bf16 expert and RMSNorm are not yet
+ *   go_rms_norm          checked by any test.
  */
 #ifndef GYRO_ORACLE_H
 #define GYRO_ORACLE_H

@@ -91,6 +91,9 @@ def test_layer_matches_numpy_fp64(oracle_mod, small_layer):
     # The oracle's own fp64 dense path agrees with numpy to rounding.
     d64 = ol.dense_f64(x, tr["route_ids"], tr["route_w"])
     assert oracle_mod.rel_rms(ref, d64) < 1e-6
+    # The fp64 router logits (the margin guard's input) match numpy's x.W^T.
+    r64 = ol.router_f64(x)
+    np.testing.assert_allclose(r64, x.astype(np.float64) @ L.router.astype(np.float64).T, rtol=1e-12, atol=1e-12)
     # Planted mistakes fail.
     bad, _, _ = numpy_layer(oracle_mod, L, x, drop_down_rotation=True)
     assert oracle_mod.rel_rms(bad, out) > 0.1
