@@ -1,0 +1,30 @@
+// Prefill path, step 2: top-8 routing of every token, one wave per token.
+// Softmax, top-k with ties to the lower index, and the renormalised weights of
+// src/engine.zig:527-540 and :670-687, computed on the logits as route_fast.h describes.
+// Grid: ceil(n / 4); 256 threads (four tokens per group). Requires n_expert <= 256, top-8.
+// Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_tok 4 scale (fp32 bits) 5 ids_uav
+// 6 ids_off 7 weights_uav 8 weights_off.
+#include "route_fast.h"
+
+GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t NE = a.c[2], n = a.c[3];
+    const uint32_t t = blockIdx.x * 4u + wave;
+    if (t >= n) return;
+    float v[4];
+    rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * NE, NE, v);
+    uint32_t ids[8];
+    float wts[8];
+    wave_route_fast<4, 8>(v, NE, gd_bits_f32(a.c[4]), ids, wts);
+    if (lane < 8u) {
+        uint32_t id = ids[0];
+        float w = wts[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            id = lane == (uint32_t)j ? ids[j] : id;
+            w = lane == (uint32_t)j ? wts[j] : w;
+        }
+        gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * 8u + lane] = id;
+        gd_buf<float>(a, a.c[7])[a.c[8] + t * 8u + lane] = w;
+    }
+}

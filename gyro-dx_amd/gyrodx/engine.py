@@ -37,6 +37,7 @@ def lib() -> C.CDLL:
         L.gm_add_layer.argtypes = [vp, C.POINTER(LayerDesc), C.POINTER(u32)]
         L.gm_forward.argtypes = [vp, u32, u32, f32p, u32, f32p]
         L.gm_last_routes.argtypes = [vp, u32, C.POINTER(u32), f32p]
+        L.gm_last_sort.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(u32)]
         L.gm_dequant.argtypes = [vp, u32, u32, u32, u32, u32, f32p]
         L.gm_set_tokens.argtypes = [vp, f32p, u32]
         L.gm_run.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
@@ -102,7 +103,7 @@ class Engine:
                       types=ptr(np.ascontiguousarray(layer.types, np.uint32).reshape(-1)))
         idx = C.c_uint32()
         self._check(lib().gm_add_layer(self._h, C.byref(d), C.byref(idx)), "gm_add_layer")
-        self.E, self.U = layer.E, layer.n_used
+        self.E, self.U, self.n_expert = layer.E, layer.n_used, layer.n_expert
         return idx.value
 
     def forward(self, layer: int, x: np.ndarray, path: int = PATH_DECODE) -> np.ndarray:
@@ -117,6 +118,14 @@ class Engine:
         self._check(lib().gm_last_routes(self._h, n, ids.ctypes.data_as(C.POINTER(C.c_uint32)), _f32p(w)),
                     "gm_last_routes")
         return ids, w
+
+    def last_sort(self, n: int):
+        """Counting sort of the last prefill forward: (route_order[n * n_used], order_start[n_expert + 1])."""
+        order = np.empty(n * self.U, np.uint32)
+        start = np.empty(self.n_expert + 1, np.uint32)
+        p = lambda a: a.ctypes.data_as(C.POINTER(C.c_uint32))
+        self._check(lib().gm_last_sort(self._h, n, p(order), p(start)), "gm_last_sort")
+        return order, start
 
     def dequant(self, layer: int, expert: int, proj: int, row0: int, rows: int, cols: int) -> np.ndarray:
         out = np.empty((rows, cols), np.float32)

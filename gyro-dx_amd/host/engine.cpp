@@ -60,7 +60,35 @@ struct Layer {
     uint32_t type_id = 0;     // uniform Gyro type, 0 when projections mix types
     uint32_t gate_bytes = 0;  // per projection, uniform types only
     uint64_t base = 0;        // device address of expert 0's bundle; expert e at base + e * stride
+    float max_scale = 0;      // largest |block scale| over the layer's experts
 };
+
+// binary16 -> float for host-side range checks.
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 31u, man = h & 1023u;
+    uint32_t u;
+    if (exp == 31u) u = sign | 0x7f800000u | (man << 13);
+    else if (exp) u = sign | ((exp + 112u) << 23) | (man << 13);
+    else {
+        float f = std::ldexp((float)man, -24);
+        return sign ? -f : f;
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Largest |scale| of the TQ2_T blocks in `bytes` bytes of packed rows (34-byte blocks).
+float max_block_scale(const uint8_t *p, uint64_t bytes) {
+    float m = 0;
+    for (uint64_t off = 0; off + 34 <= bytes; off += 34) {
+        uint16_t h;
+        std::memcpy(&h, p + off, 2);
+        const float v = std::fabs(half_to_float(h));
+        if (!(v <= m)) m = v;  // NaN propagates as "too large"
+    }
+    return m;
+}
 
 std::vector<uint8_t> read_file(const std::string &path) {
     std::ifstream f(path, std::ios::binary);
@@ -84,9 +112,12 @@ class Engine {
     // Shared buffers.
     Buffer staging, codebook, zeros;
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
+    Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
     Buffer tokens, outputs;
     uint32_t n_tokens = 0;
     uint32_t parts = 0;
+    float max_codebook = 0;  // largest |codebook value|
+    static constexpr uint32_t kTileRows = 128;
 
     gd_pipeline *pipe(const char *name) {
         auto it = pipes.find(name);
@@ -167,6 +198,11 @@ class Engine {
         std::vector<uint8_t> book = read_file(kernel_dir + "/../../data/gyro_codebook.f16");
         if (book.size() != 8192) throw NativeError(-1, "codebook must hold 8192 bytes");
         upload(codebook, 0, book.data(), 8192);
+        for (uint32_t i = 0; i < 4096; ++i) {
+            uint16_t h;
+            std::memcpy(&h, book.data() + 2 * i, 2);
+            max_codebook = std::max(max_codebook, std::fabs(half_to_float(h)));
+        }
     }
 
     void allocate_activations() {
@@ -183,12 +219,20 @@ class Engine {
         act = dev.buffer(T * U * F * f, Kind::device);
         down = dev.buffer(T * U * E * f, Kind::device);
         out = dev.buffer(T * E * f, Kind::device);
+        order = dev.buffer(T * U * 4, Kind::device);
+        meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
         // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
         Buffer z = dev.buffer(T * E * f, Kind::device);
         fill_zero(z);
         sh_zero = z;
     }
     Buffer sh_zero;
+
+    // Upper bound of the sort's tile count for n tokens: every non-empty expert segment
+    // adds at most one partial tile.
+    uint32_t max_tiles(uint32_t n) const {
+        return (n * U + kTileRows - 1) / kTileRows + std::min(NE, n * U);
+    }
 
     uint32_t add_layer(const gm_layer_desc &d) {
         if (layers.empty()) {
@@ -241,6 +285,9 @@ class Engine {
             upload(arena, off, d.gate[e], gb[e]);
             upload(arena, off + gb[e], d.up[e], ub[e]);
             upload(arena, off + gb[e] + ub[e], d.down[e], db[e]);
+            if (uniform && d.types[0] == 144)
+                L.max_scale = std::max({L.max_scale, max_block_scale(d.gate[e], gb[e]), max_block_scale(d.up[e], ub[e]),
+                                        max_block_scale(d.down[e], db[e])});
             lookup.words()[il * NE + e] = slot;
             desc[e].gate = arena.gpu + off;
             desc[e].up = arena.gpu + off + gb[e];
@@ -346,12 +393,51 @@ class Engine {
                              E / 8, n);
     }
 
+    // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;
+    // every such product must be finite in binary16.
+    bool prefill_supported(const Layer &L) const {
+        return L.type_id == 144 && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
+               L.max_scale * max_codebook < 65504.0f;
+    }
+
+    // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
+    // down GEMMs, combine. bracket: 1 router, 2 gate/up, 3 down, 4 top-k, 5 sort, 6 combine.
+    void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
+                     int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
+        const Layer &L = layers.at(il);
+        if (!prefill_supported(L))
+            throw NativeError(-1, "prefill path needs TQ2_T, E and F multiples of 256, top-8 of <= 256 experts "
+                                  "and binary16-finite scale x codebook products");
+        const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
+        const uint32_t tiles = max_tiles(n);
+        dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
+                             {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
+                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
+                             (n + 31) / 32, (NE + 31) / 32);
+        dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
+                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0}, (n + 3) / 4);
+        dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
+                             {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows}, 1);
+        dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
+                             {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
+                              codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, act.uav, 0, E, F, U},
+                             tiles, F / 128);
+        dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down",
+                             {meta.uav, order.uav, 0, act.uav, 0, base_lo, base_hi, slot_stride, 2 * L.gate_bytes,
+                              codebook.srv, down.uav, 0, E, F},
+                             tiles, E / 128);
+        dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
+                             {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U}, (E + 1023) / 1024, n);
+    }
+
     void ffn(uint32_t path, uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
              uint32_t out_off, int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
         if (path == GM_PATH_REFERENCE)
             ffn_reference(il, n, x_uav, x_off, out_uav, out_off);
         else if (path == GM_PATH_DECODE)
             ffn_decode(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
+        else if (path == GM_PATH_PREFILL)
+            ffn_prefill(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
         else
             throw NativeError(-1, "path not available");
     }
@@ -425,6 +511,17 @@ extern "C" int gm_last_routes(gm_engine *g, uint32_t n, uint32_t *ids, float *we
         Engine &e = g->e;
         gyro::check(gd_readback(e.dev.ctx, e.ids.handle, 0, n * e.U * 4, ids, gyro::kTimeoutMs), "gd_readback");
         gyro::check(gd_readback(e.dev.ctx, e.weights.handle, 0, n * e.U * 4, weights, gyro::kTimeoutMs),
+                    "gd_readback");
+    });
+}
+
+extern "C" int gm_last_sort(gm_engine *g, uint32_t n, uint32_t *order, uint32_t *order_start) {
+    if (!order || !order_start) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        if (n == 0 || n > e.max_tok) throw gyro::NativeError(-1, "token count exceeds max_tok");
+        gyro::check(gd_readback(e.dev.ctx, e.order.handle, 0, n * e.U * 4, order, gyro::kTimeoutMs), "gd_readback");
+        gyro::check(gd_readback(e.dev.ctx, e.meta.handle, 0, (e.NE + 1) * 4, order_start, gyro::kTimeoutMs),
                     "gd_readback");
     });
 }

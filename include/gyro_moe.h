@@ -10,8 +10,8 @@
  *                      (mv_f32 router, rotate128, moe_route, moe_resolve, moe_gyro gate/up,
  *                      moe_act, moe_gyro down, moe_combine), in passes of max_tok tokens.
  *   GM_PATH_DECODE     the MI355X decode path: moe_router, moe_decode_gu, moe_decode_down.
- *   GM_PATH_PREFILL    the MI355X grouped-GEMM path: moe_router, moe_sort, moe_ggemm_gu,
- *                      moe_ggemm_down, moe_gather.
+ *   GM_PATH_PREFILL    the MI355X grouped-GEMM path: moe_prefill_router, moe_prefill_topk,
+ *                      moe_prefill_sort, moe_prefill_gu, moe_prefill_down, moe_prefill_combine.
  * All return 0 or a negative code; gm_last_error describes the failure.
  */
 #ifndef GYRO_MOE_H
@@ -57,6 +57,10 @@ GM_API int gm_add_layer(gm_engine *e, const gm_layer_desc *desc, uint32_t *out_i
 GM_API int gm_forward(gm_engine *e, uint32_t layer, uint32_t path, const float *x, uint32_t n, float *out);
 /* Reads the routing of the last gm_forward: ids[n][n_used], weights[n][n_used]. */
 GM_API int gm_last_routes(gm_engine *e, uint32_t n, uint32_t *ids, float *weights);
+/* Reads the counting sort of the last GM_PATH_PREFILL gm_forward of n tokens (src/engine.zig:
+ * 553-564): order[n * n_used] lists the slots t * n_used + k grouped by expert, stable in slot
+ * order; order_start[n_expert + 1] is the exclusive prefix of the expert counts. */
+GM_API int gm_last_sort(gm_engine *e, uint32_t n, uint32_t *order, uint32_t *order_start);
 /* Decodes rows [row0, row0 + rows) of one expert projection to fp32 with the fast path's
  * device decoder (bit-exact check of the in-kernel dequantisation). */
 GM_API int gm_dequant(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,

@@ -1,0 +1,95 @@
+"""GPU parity of the grouped-GEMM prefill path against the CPU oracle, through the C ABI.
+
+Bar: top-k expert ids identical (tokens whose 8th/9th fp64 router probabilities lie within
+1e-5 relative are reported and excluded); the counting sort (route_order, order_start)
+identical to the oracle's whenever every token is separable; layer outputs within relative
+RMS 2e-3 and cosine 0.9999 of the oracle's fp32 results. Shapes cover the full layer with the
+Zipf-skewed router, a single token, ragged tile rows, an expert whose segment spans several
+128-row tiles, and a layer without rotations.
+"""
+import numpy as np
+import pytest
+
+from gyrodx import synth
+from gyrodx.engine import PATH_PREFILL, Engine
+
+pytestmark = pytest.mark.gpu
+REL_RMS = 2e-3
+COSINE = 0.9999
+
+
+def separable(oracle_layer, x, U, margin=1e-5):
+    logits = oracle_layer.router_f64(x)
+    if oracle_layer.layer.router_bias is not None:
+        logits = logits + oracle_layer.layer.router_bias.astype(np.float64)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    s = -np.sort(-p, axis=1)
+    return (s[:, U - 1] - s[:, U]) > margin * s[:, U - 1]
+
+
+def run_case(oracle_mod, layer, x, max_tok, what):
+    eng = Engine(max_tok=max_tok)
+    try:
+        eng.add_layer(layer)
+        n = x.shape[0]
+        ol = oracle_mod.OracleLayer(layer)
+        ref, tr = ol.forward(x, trace=True)
+        print(f"{what}: n={n} E={layer.E} F={layer.F} experts={layer.n_expert}", flush=True)
+        out = eng.forward(0, x, PATH_PREFILL)
+        ids, w = eng.last_routes(n)
+        sep = separable(ol, x, layer.n_used)
+        print(f"{what}: {int((~sep).sum())} near-tie tokens excluded", flush=True)
+        np.testing.assert_array_equal(ids[sep], tr["route_ids"][sep])
+        np.testing.assert_allclose(w[sep], tr["route_w"][sep], rtol=2e-5, atol=1e-7)
+        if sep.all():
+            order, start = eng.last_sort(n)
+            np.testing.assert_array_equal(start, tr["order_start"])
+            np.testing.assert_array_equal(order, tr["route_order"])
+        r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
+        print(f"{what}: rel_rms={r:.3e} cosine={c:.8f}", flush=True)
+        assert r <= REL_RMS and c >= COSINE, (what, r, c)
+        return eng.last_sort(n)
+    finally:
+        eng.close()
+
+
+def test_prefill_full_layer_zipf(oracle_mod):
+    """The prefill workload's layer (hidden 2048, 256 experts, top-8, F 512, Zipf(1.1) bias)."""
+    layer = synth.make_layer(20261201, zipf=1.1)
+    x = synth.make_tokens(20261202, 256, bf16=True)
+    order, start = run_case(oracle_mod, layer, x, 256, "full zipf")
+    counts = np.diff(start.astype(np.int64))
+    assert counts.max() > 128  # at least one expert spans several tiles
+
+
+def test_prefill_single_and_ragged(oracle_mod):
+    layer = synth.make_layer(31, E=1024, F=256, n_expert=64, n_used=8)
+    for n in (1, 37):
+        run_case(oracle_mod, layer, synth.make_tokens(32 + n, n, layer.E, bf16=True), 64, f"ragged n={n}")
+
+
+def test_prefill_hot_experts_span_tiles(oracle_mod):
+    """A steep bias sends every token to the same few experts: segments of 300 rows."""
+    layer = synth.make_layer(41, E=1024, F=256, n_expert=32, n_used=8, zipf=1.1, zipf_factor=6.0)
+    x = synth.make_tokens(42, 300, layer.E, bf16=True)
+    order, start = run_case(oracle_mod, layer, x, 300, "hot experts")
+    assert np.diff(start.astype(np.int64)).max() == 300
+
+
+def test_prefill_without_rotations(oracle_mod):
+    layer = synth.make_layer(51, E=1024, F=512, n_expert=64, n_used=8, signs=False)
+    run_case(oracle_mod, layer, synth.make_tokens(52, 70, layer.E), 128, "no signs")
+
+
+def test_prefill_refuses_fp16_overflowing_scales():
+    """Blocks whose scale x codebook product overflows binary16 are refused, not computed."""
+    layer = synth.make_layer(61, E=1024, F=256, n_expert=16, n_used=8)
+    layer.gate[3][5, 0:2] = np.frombuffer(np.float16(60000.0).tobytes(), np.uint8)
+    eng = Engine(max_tok=8)
+    try:
+        eng.add_layer(layer)
+        with pytest.raises(RuntimeError, match="binary16-finite"):
+            eng.forward(0, synth.make_tokens(62, 4, layer.E), PATH_PREFILL)
+    finally:
+        eng.close()
