@@ -17,8 +17,11 @@ Reported beside the throughput:
   cpu_baseline  the CPU oracle (a C restatement of src/engine.zig ffn and its thread pool) on a
                 bounded sample of the same tokens, on this host's cores.
   parity        rel-RMS and cosine of the GPU outputs against that CPU sample.
-  prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias, when the
-                grouped-GEMM pipelines are built.
+  prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (four cycled
+                copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
+                and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
+                16-bit MFMA peak, for the grouped GEMMs alone and for the whole layer; the CPU
+                oracle times one of the calls and checks its outputs.
 """
 from __future__ import annotations
 
@@ -43,6 +46,12 @@ PROJ_BYTES = F * (E // 128) * 34  # 278,528 packed bytes per expert projection
 EXPERT_BYTES_PER_TOKEN = TOP_K * 3 * PROJ_BYTES  # 6,684,672
 GU_BYTES_PER_LAUNCH = TOP_K * 2 * PROJ_BYTES  # 4,456,448
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
+PREFILL_TOKENS = 1024
+# Routed-expert FLOPs of one prefill call: tokens x top-8 x (gate, up, down) x 2 x E x F.
+PREFILL_GU_FLOPS = PREFILL_TOKENS * TOP_K * 2 * 2 * E * F       # 34,359,738,368
+PREFILL_DOWN_FLOPS = PREFILL_TOKENS * TOP_K * 2 * E * F         # 17,179,869,184
+PREFILL_FLOPS = PREFILL_GU_FLOPS + PREFILL_DOWN_FLOPS           # 51,539,607,552
+BUNDLE_BYTES = 3 * PROJ_BYTES                                   # 835,584 per expert
 COPY_WORDS = 8 << 20  # calibration copy of the traffic probe: 32 MiB read, 32 MiB written
 
 
@@ -119,6 +128,61 @@ def cpu_baseline(layer, tokens, gpu_out, budget_s: float):
     return base, parity
 
 
+def prefill_bench(eng, layer, args):
+    """1024-token prefill of the layer with a Zipf(1.1) router bias over four cycled copies;
+    `args.prefill_calls` timed calls on distinct bf16 token batches already in HBM."""
+    import dataclasses
+    from gyrodx import synth
+    from gyrodx.engine import PATH_PREFILL
+    zl = dataclasses.replace(layer, router_bias=synth.zipf_bias(args.seed, N_EXPERT, 1.1))
+    layers = [eng.add_layer(zl) for _ in range(args.copies)]
+    batches = args.prefill_calls
+    x = synth.make_tokens(args.seed + 3, PREFILL_TOKENS * batches, bf16=True)
+    eng.set_tokens(x)
+    eng.run(PATH_PREFILL, PREFILL_TOKENS, min(batches, 4), layers, first=0)  # warm-up
+    dev_ms, wall_ms, _ = eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, first=0)
+    us = {}
+    for name, br in (("moe_prefill_router", 1), ("moe_prefill_topk", 4), ("moe_prefill_sort", 5),
+                     ("moe_prefill_gu", 2), ("moe_prefill_down", 3), ("moe_prefill_combine", 6)):
+        us[name] = round(eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, bracket=br, first=0)[2], 3)
+    out0 = eng.read_outputs(PREFILL_TOKENS)
+    # Distinct experts of the first batch (product path routes, read back after a forward).
+    eng.forward(layers[0], x[:PREFILL_TOKENS], PATH_PREFILL)
+    ids, _ = eng.last_routes(PREFILL_TOKENS)
+    distinct = int(np.unique(ids).size)
+    t_call = wall_ms / batches * 1e-3
+    t_dev = dev_ms / batches * 1e-3
+    gemm_s = (us["moe_prefill_gu"] + us["moe_prefill_down"]) * 1e-6
+    res = {
+        "workload": "single MoE layer, 1024-token prefill, Zipf(1.1) router bias, bf16 N(0,1) tokens",
+        "tokens_per_call": PREFILL_TOKENS, "calls": batches, "layer_copies": args.copies,
+        "tok_s": round(PREFILL_TOKENS / t_call, 1),
+        "us_per_call": round(t_call * 1e6, 2), "device_us_per_call": round(t_dev * 1e6, 2),
+        "kernel_us": us,
+        "flops_per_call": PREFILL_FLOPS,
+        "mfma_peak_tflops": MFMA_PEAK_TFLOPS, "mfma_dtype": "fp16 (same dense peak as bf16)",
+        "layer_tflops": round(PREFILL_FLOPS / t_dev / 1e12, 1),
+        "layer_frac_of_peak": round(PREFILL_FLOPS / t_dev / 1e12 / MFMA_PEAK_TFLOPS, 4),
+        "grouped_gemm_tflops": round(PREFILL_FLOPS / gemm_s / 1e12, 1),
+        "grouped_gemm_frac_of_peak": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
+        "distinct_experts": distinct, "expert_bytes": distinct * BUNDLE_BYTES,
+    }
+    return res, x[:PREFILL_TOKENS], out0, zl
+
+
+def prefill_cpu(layer, x, gpu_out):
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    threads = cpu_threads()
+    ol = oracle.OracleLayer(layer)
+    t0 = time.perf_counter()
+    ref = ol.forward(x, threads=threads)
+    dt = time.perf_counter() - t0
+    return ({"value": round(x.shape[0] / dt, 1), "unit": "tok/s", "cores": threads, "kind": "port",
+             "sample": f"one {x.shape[0]}-token call (the first timed batch), {dt:.1f} s on {threads} threads"},
+            {"rel_rms": oracle.rel_rms(ref, gpu_out), "cosine": oracle.cosine(ref, gpu_out)})
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +192,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-calls", type=int, default=16, help="timed 1024-token prefill calls (0: skip)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="for profiling passes: only the prefill measurement, printed as its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
                          "copies of 32 MiB; prints the probe's shape and no benchmark line")
@@ -141,9 +208,15 @@ def main() -> int:
     from gyrodx.engine import PATH_DECODE, Engine
 
     layer = synth.make_layer(args.seed)
+    if args.prefill_only:
+        eng = Engine(max_tok=PREFILL_TOKENS)
+        pre, _, _, _ = prefill_bench(eng, layer, args)
+        eng.close()
+        print(json.dumps({"prefill": pre}), flush=True)
+        return 0
     n_tok = args.warmup + args.steps
     tokens = synth.make_tokens(args.seed + 1, n_tok)
-    eng = Engine(max_tok=64)
+    eng = Engine(max_tok=PREFILL_TOKENS)
     layers = [eng.add_layer(layer) for _ in range(args.copies)]
     eng.set_tokens(tokens)
 
@@ -194,6 +267,11 @@ def main() -> int:
     }
     if not args.no_cpu:
         line["cpu_baseline"], line["parity"] = cpu_baseline(layer, tokens[args.warmup:], gpu_out, args.cpu_budget)
+    if args.prefill_calls > 0:
+        pre, px, pout, zl = prefill_bench(eng, layer, args)
+        if not args.no_cpu:
+            pre["cpu_baseline"], pre["parity"] = prefill_cpu(zl, px, pout)
+        line["prefill"] = pre
     eng.close()
     print(json.dumps(line), flush=True)
     return 0

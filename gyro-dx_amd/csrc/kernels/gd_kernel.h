@@ -1,6 +1,7 @@
 // Device-side conventions shared by every gyro_native pipeline (gfx950, wave64).
 //
-// A pipeline is one code object exporting `gd_main(GdArgs)` and `gd_workgroup[3]`. GdArgs
+// A pipeline is one code object exporting one kernel that takes GdArgs, the `gd_entry` string
+// naming that kernel and `gd_workgroup[3]` (GD_PIPELINE_NAMED below). GdArgs
 // carries the device table of buffer base pointers and up to 60 32-bit constants, the same
 // constant layouts the reference's HLSL kernels read from root constants
 // (shaders/engine/common.hlsli:9-14): buffers are named by table index; element offsets count
@@ -21,6 +22,11 @@ struct GdArgs {
     extern "C" __constant__ char gd_entry[32] = #NAME;                     \
     extern "C" __global__ __launch_bounds__(WG) void NAME(const GdArgs a)
 #define GD_PIPELINE(WG) GD_PIPELINE_NAMED(gd_main, WG)
+// As GD_PIPELINE_NAMED, asking the compiler to fit WAVES waves per SIMD (registers included).
+#define GD_PIPELINE_NAMED_OCC(NAME, WG, WAVES)                             \
+    extern "C" __constant__ uint32_t gd_workgroup[3] = {WG, 1, 1};        \
+    extern "C" __constant__ char gd_entry[32] = #NAME;                     \
+    extern "C" __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(const GdArgs a)
 
 template <typename T>
 __device__ __forceinline__ T *gd_buf(const GdArgs &a, uint32_t index) {
@@ -100,6 +106,19 @@ __device__ __forceinline__ float gd_wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+
+// Global-address-space views of table buffers. Loads through them are global_load, counted by
+// vmcnt only (a flat load also counts against lgkmcnt), so an LDS-only wait leaves them in flight.
+typedef uint32_t gd_u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) uint32_t gd_guint;
+typedef const __attribute__((address_space(1))) gd_u32x4 gd_gu32x4;
+__device__ __forceinline__ gd_guint *gd_global(const uint32_t *p) { return (gd_guint *)(uintptr_t)p; }
+__device__ __forceinline__ gd_gu32x4 *gd_global4(const uint32_t *p) { return (gd_gu32x4 *)(uintptr_t)p; }
+
+// Workgroup barrier that waits for this wave's LDS (and scalar) traffic only, so global loads
+// issued before it stay in flight; the memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void gd_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // 1 / sqrt(128) rounded to binary32, the normalisation of a 128-point Walsh-Hadamard block.
 #define GD_INV_SQRT128 0.0883883461356163f
