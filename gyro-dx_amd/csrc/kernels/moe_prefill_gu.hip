@@ -8,50 +8,49 @@
 // weight is decoded twice; each decoded fragment feeds all of the tile's 32-row blocks
 // (v_mfma_f32_32x32x16_f16, fp32 accumulation). K runs over the E / 128 Gyro blocks: the
 // tile's activation rows (binary16 rows of the rotated input, gathered through route_order)
-// arrive in LDS by direct loads issued one block ahead (ggemm.h), and each lane decodes the
-// block of its own weight row (loaded one block ahead into registers) into B operands.
+// and the 256 weight rows' blocks arrive in LDS by direct loads issued two blocks ahead
+// (ggemm.h); each lane decodes the block of its own gate and up rows into B operands.
 // The fp16 products scale x codebook stay finite: the host checks every layer's scales.
-// Epilogue: silu(g) * u times the down signs, through LDS into rows, one 128-point
-// Walsh-Hadamard transform per row and wave, and binary16 rows act16[sorted row][F].
-// Grid: (max tiles, F / 128); 256 threads, two groups per CU; the groups beyond the sort's tile
-// count exit.
+// Epilogue: silu(g) * u times the down signs, rounded to binary16 into LDS rows, the 128-point
+// Walsh-Hadamard transform of every row as one more fp16 MFMA product with H_128 (exact +-1
+// entries, fp32 accumulation, then x 1/sqrt(128)), and binary16 rows act16[sorted row][F].
+// Grid: (max tiles, F / 128); 256 threads, one group per CU (141 KB of LDS); the groups beyond
+// the sort's tile count exit.
 // Requires TQ2_T experts, E % 256 == 0 (rows start at 4-byte boundaries, an even block count),
 // F % 128 == 0, |xh|, |act| < 65504.
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 xh16_uav 4 xh16_off (words) 5 base_lo
 // 6 base_hi 7 slot_stride 8 proj_bytes 9 codebook_srv 10 signs_srv (0xffffffff: none)
 // 11 signs_off 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used.
-#include "fwht.h"
 #include "ggemm.h"
 
-#define GU_ACT_STRIDE 132  // floats per epilogue row
+#define GU_LOADS 11        // global-to-LDS loads per wave and K block: 8 activation + 3 weight
 
 struct GuState {
-    gd_guint *grow, *urow;  // this lane's gate and up rows
-    const void *xbase;      // activation rows (byte offsets in roff)
-    uint32_t roff[8];
-    uint32_t wave, m, h, sel, nrb, nk;
+    const void *xbase, *wbase;  // activation rows; the layer's slot arena (expert bundles)
+    uint32_t roff[8], woff[3];
+    uint32_t wave, m, h, sel, nk;
 };
 
-// Block kb from buffer BUF with weights (gc, uc) for NRB 32-row blocks; prefetches block kb + 1
-// into the other buffer and (gn, un). The current block is unpacked before the prefetch is
-// issued (and the scheduler may not move it past), so waiting for it never waits for the
-// prefetch: loads retire in order.
+// K block kb from buffer BUF for NRB 32-row blocks; stages block kb + 2 into buffer
+// (BUF + 2) % 3, the buffer of block kb - 1, which every wave has left once past the sync.
 template <int BUF, int NRB>
-__device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb, const GgBlk &gc, const GgBlk &uc,
-                                        GgBlk &gn, GgBlk &un, f32x16 (&accg)[NRB], f32x16 (&accu)[NRB]) {
+__device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb, f32x16 (&accg)[NRB],
+                                        f32x16 (&accu)[NRB]) {
+    if (kb + 1u < t.nk) gg_sync<GU_LOADS>();
+    else gg_sync<0>();
+    if (kb + 2u < t.nk) {
+        gg_stage_a(sm, (BUF + 2) % 3, t.wave, t.xbase, t.roff, kb + 2u);
+        gg_stage_w<3>(sm, (BUF + 2) % 3, t.wave, t.wbase, t.woff, kb + 2u);
+    }
+    GgBlk gc, uc;
+    gg_read_w(sm, BUF, t.wave * 32u + t.m, gc);
+    gg_read_w(sm, BUF, 128u + t.wave * 32u + t.m, uc);
     const bool odd = kb & 1u;
     float gs, us;
     uint32_t gq[8], uq[8];
     tq2_unpack(gc.d, odd, gs, gq);
     tq2_unpack(uc.d, odd, us, uq);
     const half2_t gs2 = {(_Float16)gs, (_Float16)gs}, us2 = {(_Float16)us, (_Float16)us};
-    gg_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if (kb + 1u < t.nk) {
-        gg_stage(sm, BUF ^ 1, t.wave, t.xbase, t.roff, kb + 1u);
-        gg_load_blk(t.grow, kb + 1u, gn);
-        gg_load_blk(t.urow, kb + 1u, un);
-    }
     // Software pipeline over the 8 K-steps with an explicit schedule (sched_barrier fences keep
     // the compiler from regrouping it). Everything step s + 1 reads from LDS is issued during
     // step s, between its MFMAs: first the codebook gathers of its decode (one trellis state per
@@ -113,49 +112,78 @@ __device__ __forceinline__ void gu_tile(GgLds &sm, const GuState &t, const GdArg
         accg[r] = (f32x16){};
         accu[r] = (f32x16){};
     }
-    GgBlk g0, u0, g1, u1;
-    gg_load_blk(t.grow, 0, g0);
-    gg_load_blk(t.urow, 0, u0);
-    gg_stage(sm, 0, t.wave, t.xbase, t.roff, 0);
-    // nk is even: blocks alternate between buffer 0 with (g0, u0) and buffer 1 with (g1, u1).
-    for (uint32_t kb = 0; kb < t.nk; kb += 2u) {
-        gu_step<0, NRB>(sm, t, kb, g0, u0, g1, u1, accg, accu);
-        gu_step<1, NRB>(sm, t, kb + 1u, g1, u1, g0, u0, accg, accu);
+    // Blocks rotate through the three buffers: block kb in buffer kb % 3.
+    for (uint32_t kb = 0; kb < t.nk; kb += 3u) {
+        gu_step<0, NRB>(sm, t, kb, accg, accu);
+        if (kb + 1u < t.nk) gu_step<1, NRB>(sm, t, kb + 1u, accg, accu);
+        if (kb + 2u < t.nk) gu_step<2, NRB>(sm, t, kb + 2u, accg, accu);
     }
-    gg_barrier();  // every wave is done with the activation buffers
+    gg_sync<0>();  // every wave is done with the buffers
 
-    // Epilogue: act = down_signs * silu(g) * u into LDS rows (132-float stride, from offset 0).
-    float *act = reinterpret_cast<float *>(&sm);
+    // Epilogue. (1) act = down_signs * silu(g) * u, rounded to binary16, into activation buffer
+    // 0 in the A-operand layout (row i, column c = 32 wave + m of the F block).
     const bool has_signs = a.c[10] != 0xffffffffu;
     const uint32_t col = t.wave * 32u + t.m;
     const float sgn = has_signs ? gd_buf<const float>(a, a.c[10])[a.c[11] + fb * 128u + col] : 1.0f;
+    _Float16 *act = reinterpret_cast<_Float16 *>(&sm.a[0][0]);
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-            act[i * GU_ACT_STRIDE + col] = gd_silu(accg[rb][r]) * accu[rb][r] * sgn;
+            act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
+                (_Float16)(gd_silu(accg[rb][r]) * accu[rb][r] * sgn);
         }
     }
     __syncthreads();
     uint32_t *out = gd_buf<uint32_t>(a, a.c[12]) + a.c[13];
-    for (uint32_t i = t.wave; i < rows; i += 4u) {
-        const float2 v = *reinterpret_cast<const float2 *>(act + i * GU_ACT_STRIDE + 2u * lane);
-        float x0 = v.x, x1 = v.y;
-        if (has_signs) {
-            gd_fwht128_wave(x0, x1);
-            x0 *= GD_INV_SQRT128;
-            x1 *= GD_INV_SQRT128;
+    if (has_signs) {
+        // (2) The 128-point Walsh-Hadamard transform of every row as a GEMM with H_128 (entries
+        // (-1)^popcount(k & j), exact in binary16): wave w computes output columns 32 w .. +31.
+        // The B operand of lane (j, h) at K-step s holds H[16 s + 8 h + e][j] for e = 0..7, which
+        // is the lane's fixed pattern (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j).
+        const uint32_t j = t.wave * 32u + t.m;
+        f16x8 hp, hn;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            hp[e] = (__builtin_popcount((uint32_t)e & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
+            hn[e] = -hp[e];
         }
-        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)x0);
-        const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)x1);
-        out[(size_t)(row0 + i) * (F / 2u) + fb * 64u + lane] = h0 | (h1 << 16);
+        f32x16 rot[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) rot[rb] = (f32x16){};
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * t.h) & j) & 1) ? hn : hp;
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+                rot[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gg_a(sm, 0, rb * 32u + t.m, s8, t.h), hb, rot[rb], 0, 0, 0);
+        }
+        // (3) Scaled rows into activation buffer 1 (same layout), then 16-byte row copies out.
+        _Float16 *res = reinterpret_cast<_Float16 *>(&sm.a[1][0]);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[rb][r] * GD_INV_SQRT128);
+            }
+        }
+        __syncthreads();
+    }
+    // Rows of 128 binary16 values (16 chunks of 16 bytes, swizzled) to act16[row0 + i][fb * 128 ..].
+    const gd_u32x4 *rows_src = has_signs ? &sm.a[1][0] : &sm.a[0][0];
+    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 256u) {
+        const uint32_t i = idx >> 4, c = idx & 15u;
+        *reinterpret_cast<gd_u32x4 *>(out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u) =
+            rows_src[i * 16u + (c ^ (i & 15u))];
     }
 }
 
-GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 2) {
+GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 1) {
     __shared__ GgLds sm;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const uint32_t *meta = gd_buf<const uint32_t>(a, a.c[0]);
     const uint32_t tile = blockIdx.x;
     if (tile >= __builtin_amdgcn_readfirstlane(meta[1023])) return;
@@ -176,7 +204,6 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 2) {
     t.m = lane & 31u;
     t.h = lane >> 5;
     t.sel = gg_sel(t.h);
-    t.nrb = (rows + 31u) >> 5;
     t.nk = E / 128u;
     t.xbase = gd_buf<const uint32_t>(a, a.c[3]) + a.c[4];
 #pragma unroll
@@ -185,13 +212,23 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 2) {
         const uint32_t c = gg_chunk(wave, lane, i, r);
         t.roff[i] = sm.src[r] * (E * 2u) + c;
     }
+    // Weight rows q < 128: gate row fb * 128 + q; q >= 128: up row fb * 128 + q - 128.
     const uint64_t base = ((uint64_t)a.c[6] << 32) | a.c[5];
-    const uint8_t *grow = reinterpret_cast<const uint8_t *>(base + (uint64_t)e * a.c[7]) +
-                          (size_t)(fb * 128u + wave * 32u + t.m) * ((E / 128u) * 34u);
-    t.grow = gd_global(reinterpret_cast<const uint32_t *>(grow));
-    t.urow = gd_global(reinterpret_cast<const uint32_t *>(grow + a.c[8]));
-
-    switch (t.nrb) {
+    t.wbase = reinterpret_cast<const void *>(base);
+    const uint32_t row_bytes = (E / 128u) * 34u, proj_bytes = a.c[8];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        uint32_t q, piece;
+        gg_w_piece<3>(wave, lane, i, q, piece);
+        t.woff[i] = e * a.c[7] + (q >> 7) * proj_bytes + (fb * 128u + (q & 127u)) * row_bytes + piece * 16u;
+    }
+    gg_stage_a(sm, 0, wave, t.xbase, t.roff, 0);
+    gg_stage_w<3>(sm, 0, wave, t.wbase, t.woff, 0);
+    if (t.nk > 1u) {
+        gg_stage_a(sm, 1, wave, t.xbase, t.roff, 1);
+        gg_stage_w<3>(sm, 1, wave, t.wbase, t.woff, 1);
+    }
+    switch ((rows + 31u) >> 5) {
         case 1: gu_tile<1>(sm, t, a, row0, rows, fb, F); break;
         case 2: gu_tile<2>(sm, t, a, row0, rows, fb, F); break;
         case 3: gu_tile<3>(sm, t, a, row0, rows, fb, F); break;
