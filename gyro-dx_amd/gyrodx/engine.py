@@ -8,7 +8,7 @@ import numpy as np
 from . import BUILD_DIR, KERNEL_DIR
 
 LIB_PATH = BUILD_DIR / "libgyro_moe.so"
-PATH_REFERENCE, PATH_DECODE, PATH_PREFILL = 0, 1, 2
+PATH_REFERENCE, PATH_DECODE, PATH_PREFILL, PATH_GENERIC = 0, 1, 2, 3
 
 
 class LayerDesc(C.Structure):
@@ -16,7 +16,8 @@ class LayerDesc(C.Structure):
                 ("expert_weights_scale", C.c_float),
                 ("router", C.c_void_p), ("router_bias", C.c_void_p), ("gate_signs", C.c_void_p),
                 ("down_signs", C.c_void_p), ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
-                ("types", C.c_void_p)]
+                ("types", C.c_void_p), ("SF", C.c_uint32), ("sh_gate", C.c_void_p), ("sh_up", C.c_void_p),
+                ("sh_down", C.c_void_p), ("sh_gate_inp", C.c_void_p)]
 
 
 _lib = None
@@ -100,7 +101,9 @@ class Engine:
                       router_bias=ptr(None if layer.router_bias is None else np.asarray(layer.router_bias, np.float32)),
                       gate_signs=ptr(layer.gate_signs), down_signs=ptr(layer.down_signs),
                       gate=ptrs(layer.gate), up=ptrs(layer.up), down=ptrs(layer.down),
-                      types=ptr(np.ascontiguousarray(layer.types, np.uint32).reshape(-1)))
+                      types=ptr(np.ascontiguousarray(layer.types, np.uint32).reshape(-1)),
+                      SF=layer.SF, sh_gate=ptr(layer.sh_gate), sh_up=ptr(layer.sh_up), sh_down=ptr(layer.sh_down),
+                      sh_gate_inp=ptr(None if layer.sh_gate_inp is None else np.asarray(layer.sh_gate_inp, np.float32)))
         idx = C.c_uint32()
         self._check(lib().gm_add_layer(self._h, C.byref(d), C.byref(idx)), "gm_add_layer")
         self.E, self.U, self.n_expert = layer.E, layer.n_used, layer.n_expert

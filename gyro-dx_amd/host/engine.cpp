@@ -61,6 +61,8 @@ struct Layer {
     uint32_t gate_bytes = 0;  // per projection, uniform types only
     uint64_t base = 0;        // device address of expert 0's bundle; expert e at base + e * stride
     float max_scale = 0;      // largest |block scale| over the layer's experts
+    uint32_t SF = 0;          // shared expert width (0: none)
+    Buffer sh_gu, sh_down, sh_gate;  // bf16 [2 SF][E] (gate rows, then up rows), [E][SF]; fp32 [E]
 };
 
 // binary16 -> float for host-side range checks.
@@ -113,6 +115,8 @@ class Engine {
     Buffer staging, codebook, zeros;
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
     Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
+    Buffer sh_h, sh_a, sh_o, sh_g;  // shared expert: [T][2 SF], [T][SF], [T][E], [T]
+    uint32_t sh_width = 0;          // SF the shared buffers are sized for
     Buffer tokens, outputs;
     uint32_t n_tokens = 0;
     uint32_t parts = 0;
@@ -316,12 +320,35 @@ class Engine {
         }
         L.signs = dev.buffer((E + F) * 4, Kind::device);
         upload(L.signs, 0, signs.data(), (E + F) * 4);
+        if (d.SF) {
+            if (!d.sh_gate || !d.sh_up || !d.sh_down || !d.sh_gate_inp) throw NativeError(-1, "shared expert weights missing");
+            L.SF = d.SF;
+            const uint64_t half = (uint64_t)d.SF * E * 2;
+            if (half % 4) throw NativeError(-1, "shared expert shape must be word aligned");
+            L.sh_gu = dev.buffer(2 * half, Kind::device);
+            upload(L.sh_gu, 0, d.sh_gate, half);
+            upload(L.sh_gu, half, d.sh_up, half);
+            L.sh_down = dev.buffer(half, Kind::device);
+            upload(L.sh_down, 0, d.sh_down, half);
+            L.sh_gate = dev.buffer((uint64_t)E * 4, Kind::device);
+            upload(L.sh_gate, 0, d.sh_gate_inp, (uint64_t)E * 4);
+            if (d.SF > sh_width) {
+                for (Buffer *b : {&sh_h, &sh_a, &sh_o, &sh_g})
+                    if (b->handle) dev.release(*b);
+                const uint64_t T = max_tok;
+                sh_h = dev.buffer(T * 2 * d.SF * 4, Kind::device);
+                sh_a = dev.buffer(T * d.SF * 4, Kind::device);
+                sh_o = dev.buffer(T * E * 4, Kind::device);
+                sh_g = dev.buffer(T * 4, Kind::device);
+                sh_width = d.SF;
+            }
+        }
         layers.push_back(L);
         return il;
     }
 
-    // Reference dispatch sequence, src/gpu_engine.zig:1052-1119 (routed experts; no shared
-    // expert in these layers, so moe_combine adds sigmoid(0) * 0).
+    // Reference dispatch sequence, src/gpu_engine.zig:1052-1119: routed experts of one Gyro type
+    // and the optional shared expert.
     void ffn_reference(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
                        uint32_t out_off) {
         const Layer &L = layers.at(il);
@@ -362,13 +389,79 @@ class Engine {
         dispatch("moe_gyro", {table.uav, codebook.srv, act.uav, 0, F, down.uav, 0, E, F, L.type_id, bb, 2, U, 1, 0, 0},
                  (E + 31) / 32, n_slots, 1);
         dev.barrier();
-        dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh_zero.uav, 0, sh_zero.uav, 0},
-                 (E + 255) / 256, n);
+        uint32_t sh = sh_zero.uav, shg = sh_zero.uav;  // no shared expert: sigmoid(0) * 0
+        if (L.SF) {
+            shared_expert(L, n, x_uav, x_off);
+            sh = sh_o.uav;
+            shg = sh_g.uav;
+        }
+        dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
         dev.barrier();
     }
 
+    // Rows per wave of the reference's matrix-vector grid (src/gpu_engine.zig:851-853).
+    static uint32_t mv_rpw(uint32_t rows) {
+        uint32_t rpw = 1;
+        while (rows / (8 * rpw * 2) >= 1024) rpw *= 2;
+        return rpw;
+    }
+    void mv(const char *kernel, uint32_t w_srv, uint32_t rows, uint32_t cols, uint32_t row_bytes, uint32_t x_uav,
+            uint32_t x_off, uint32_t x_stride, uint32_t n, uint32_t y_uav, uint32_t y_off, uint32_t y_stride) {
+        const uint32_t rpw = mv_rpw(rows), groups = (rows + 8 * rpw - 1) / (8 * rpw);
+        for (uint32_t done = 0; done < n; done += 8) {
+            const uint32_t m = std::min(n - done, 8u);
+            dispatch(kernel, {w_srv, 0, rows, cols, x_uav, x_off + done * x_stride, x_stride, m, y_uav,
+                              y_off + done * y_stride, y_stride, 0, 0, bits(1.0f), row_bytes, rpw},
+                     groups);
+        }
+    }
+
+    // Shared expert of src/engine.zig:644-653 on the unrotated input (sh_o = W_d (silu(W_g x) *
+    // W_u x), sh_g = g . x), in the reference's kernels: mv_bf16, ew SwiGLU, mv_bf16, mv_f32.
+    void shared_expert(const Layer &L, uint32_t n, uint32_t x_uav, uint32_t x_off) {
+        const uint32_t SF = L.SF;
+        mv("mv_bf16", L.sh_gu.srv, 2 * SF, E, E * 2, x_uav, x_off, E, n, sh_h.uav, 0, 2 * SF);
+        dispatch("ew", {sh_h.uav, 0, 2 * SF, sh_h.uav, SF, 2 * SF, sh_a.uav, 0, SF, SF, n, 0}, (SF * n + 255) / 256);
+        mv("mv_bf16", L.sh_down.srv, E, SF, SF * 2, sh_a.uav, 0, SF, n, sh_o.uav, 0, E);
+        mv("mv_f32", L.sh_gate.srv, 1, E, E * 4, x_uav, x_off, E, n, sh_g.uav, 0, 1);
+    }
+
+    // Any layer (mixed Gyro types, optional shared expert), in the reference's dispatch style:
+    // router, rotation, route, moe_gyro_x gate/up, moe_act, moe_gyro_x down, shared expert,
+    // combine.
+    void ffn_generic(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off) {
+        const Layer &L = layers.at(il);
+        if (L.has_bias)
+            dispatch("ew", {L.bias.uav, 0, 0, L.bias.uav, 0, 0, router_out.uav, 0, NE, NE, n, 5}, (NE * n + 255) / 256);
+        const uint32_t rpw = mv_rpw(NE), groups = (NE + 8 * rpw - 1) / (8 * rpw);
+        for (uint32_t done = 0; done < n; done += 8) {
+            const uint32_t m = std::min(n - done, 8u);
+            dispatch("mv_f32", {L.router.srv, 0, NE, E, x_uav, x_off + done * E, E, m, router_out.uav, done * NE,
+                                NE, L.has_bias ? 1u : 0u, 0, bits(1.0f), E * 4, rpw},
+                     groups);
+        }
+        if (L.has_gate_signs)
+            dispatch("rotate128", {x_uav, x_off, xh.uav, 0, L.signs.srv, 0, E, E}, E / 128, n);
+        else
+            dispatch("ew", {x_uav, x_off, E, x_uav, x_off, E, xh.uav, 0, E, E, n, 3}, (E * n + 255) / 256);
+        dispatch("moe_route", {router_out.uav, 0, NE, U, ids.uav, 0, weights.uav, 0, kNone, 0, bits(L.scale), n}, n);
+        const uint32_t n_slots = n * U;
+        dispatch("moe_gyro_x", {ids.uav, 0, L.xtab.srv, codebook.srv, xh.uav, 0, E, gu.uav, 0, F, E, 0, U, 0, NE},
+                 (F + 31) / 32, n_slots, 2);
+        dispatch("moe_act", {gu.uav, 0, act.uav, 0, L.signs.srv, E, F, L.has_down_signs ? 1u : 0u}, n_slots);
+        dispatch("moe_gyro_x", {ids.uav, 0, L.xtab.srv, codebook.srv, act.uav, 0, F, down.uav, 0, E, F, 2, U, 1, NE},
+                 (E + 31) / 32, n_slots, 1);
+        uint32_t sh = sh_zero.uav, shg = sh_zero.uav;
+        if (L.SF) {
+            shared_expert(L, n, x_uav, x_off);
+            sh = sh_o.uav;
+            shg = sh_g.uav;
+        }
+        dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
+    }
+
     bool decode_supported(const Layer &L, uint32_t n) const {
-        return L.type_id == 144 && E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
+        return L.type_id == 144 && !L.SF && E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
     }
 
     // MI355X decode path: router + rotation, routed gate/up, down + combine.
@@ -376,7 +469,8 @@ class Engine {
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
-            throw NativeError(-1, "decode path needs TQ2_T, E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8");
+            throw NativeError(-1, "decode path needs TQ2_T, no shared expert, E % 1024 == 0, F == 512, top-8 of <= 256 "
+                                  "experts, n <= 8");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
@@ -396,7 +490,7 @@ class Engine {
     // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;
     // every such product must be finite in binary16.
     bool prefill_supported(const Layer &L) const {
-        return L.type_id == 144 && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
+        return L.type_id == 144 && !L.SF && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
                L.max_scale * max_codebook < 65504.0f;
     }
 
@@ -406,8 +500,8 @@ class Engine {
                      int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
-            throw NativeError(-1, "prefill path needs TQ2_T, E and F multiples of 256, top-8 of <= 256 experts "
-                                  "and binary16-finite scale x codebook products");
+            throw NativeError(-1, "prefill path needs TQ2_T, no shared expert, E and F multiples of 256, top-8 of "
+                                  "<= 256 experts and binary16-finite scale x codebook products");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
@@ -438,6 +532,8 @@ class Engine {
             ffn_decode(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
         else if (path == GM_PATH_PREFILL)
             ffn_prefill(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
+        else if (path == GM_PATH_GENERIC)
+            ffn_generic(il, n, x_uav, x_off, out_uav, out_off);
         else
             throw NativeError(-1, "path not available");
     }

@@ -12,6 +12,10 @@
  *   GM_PATH_DECODE     the MI355X decode path: moe_router, moe_decode_gu, moe_decode_down.
  *   GM_PATH_PREFILL    the MI355X grouped-GEMM path: moe_prefill_router, moe_prefill_topk,
  *                      moe_prefill_sort, moe_prefill_gu, moe_prefill_down, moe_prefill_combine.
+ *   GM_PATH_GENERIC    any layer: Gyro types mixed per expert and projection (moe_gyro_x reads
+ *                      each expert's projections and types from the layer's descriptor table)
+ *                      and the optional bf16 shared expert (mv_bf16, ew, mv_f32 gate, combine),
+ *                      in the reference's dispatch style; passes of max_tok tokens.
  * All return 0 or a negative code; gm_last_error describes the failure.
  */
 #ifndef GYRO_MOE_H
@@ -28,7 +32,7 @@ extern "C" {
 
 typedef struct gm_engine gm_engine;
 
-enum { GM_PATH_REFERENCE = 0, GM_PATH_DECODE = 1, GM_PATH_PREFILL = 2 };
+enum { GM_PATH_REFERENCE = 0, GM_PATH_DECODE = 1, GM_PATH_PREFILL = 2, GM_PATH_GENERIC = 3 };
 
 /* One MoE layer in the reference's tensor layout (src/model.zig:115-123): per expert, gate and
  * up hold F rows of E columns and down holds E rows of F columns, each row a run of Gyro blocks.
@@ -44,6 +48,14 @@ typedef struct gm_layer_desc {
     const uint8_t *const *up;
     const uint8_t *const *down;
     const uint32_t *types;
+    /* Optional shared SwiGLU expert (src/engine.zig:644-653), SF = 0 for none: bf16 gate and up
+     * [SF][E], down [E][SF], and the fp32 gate input [E]: out += sigmoid(g . x) * W_d (silu(W_g x)
+     * * W_u x) on the unrotated input x. */
+    uint32_t SF;
+    const uint16_t *sh_gate;
+    const uint16_t *sh_up;
+    const uint16_t *sh_down;
+    const float *sh_gate_inp;
 } gm_layer_desc;
 
 /* Creates an engine on device `adapter`, loading every <name>.co pipeline in kernel_dir.

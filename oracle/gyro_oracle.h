@@ -29,8 +29,9 @@
  *                        test_counting_sort_invariants, test_layer_thread_count_invariant).
  *   go_moe_dense_f64,    the same fp64 numpy model and numpy's x.W^T for the router logits
  *   go_router_f64        (test_layer_matches_numpy_fp64).
- *   go_dot_bf16,         parity unpinned: the shared bf16 expert and RMSNorm are not yet
- *   go_rms_norm          checked by any test.
+ *   go_dot_bf16          the bf16 shared expert against an fp64 numpy model of its algebra
+ *                        (test_shared_expert_matches_numpy).
+ *   go_rms_norm          parity unpinned: RMSNorm is not yet checked by any test.
  */
 #ifndef GYRO_ORACLE_H
 #define GYRO_ORACLE_H

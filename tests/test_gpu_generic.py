@@ -1,0 +1,58 @@
+"""GPU parity of the generic path (mixed Gyro types per expert and projection, bf16 shared
+expert) and of the reference path with a shared expert, against the CPU oracle, through the C
+ABI. Bar as in test_gpu_moe.py: top-k ids identical for separable tokens, rel-RMS <= 2e-3,
+cosine >= 0.9999."""
+import numpy as np
+import pytest
+
+from gyrodx import synth
+from gyrodx.engine import PATH_GENERIC, PATH_REFERENCE, Engine
+
+pytestmark = pytest.mark.gpu
+
+
+def separable(oracle_layer, x, U, margin=1e-5):
+    logits = oracle_layer.router_f64(x)
+    if oracle_layer.layer.router_bias is not None:
+        logits = logits + oracle_layer.layer.router_bias.astype(np.float64)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    s = -np.sort(-p, axis=1)
+    return (s[:, U - 1] - s[:, U]) > margin * s[:, U - 1]
+
+
+def check(oracle_mod, layer, x, path, what, max_tok=16):
+    eng = Engine(max_tok=max_tok)
+    try:
+        eng.add_layer(layer)
+        ol = oracle_mod.OracleLayer(layer)
+        ref, tr = ol.forward(x, trace=True)
+        print(f"{what}: n={x.shape[0]} types={sorted(set(layer.types.ravel().tolist()))} SF={layer.SF}", flush=True)
+        out = eng.forward(0, x, path)
+        ids, _ = eng.last_routes(x.shape[0])
+        sep = separable(ol, x, layer.n_used)
+        np.testing.assert_array_equal(ids[sep], tr["route_ids"][sep])
+        r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
+        print(f"{what}: rel_rms={r:.3e} cosine={c:.8f} excluded={int((~sep).sum())}", flush=True)
+        assert r <= 2e-3 and c >= 0.9999, (what, r, c)
+    finally:
+        eng.close()
+
+
+def test_generic_mixed_types_small(oracle_mod):
+    layer = synth.make_layer(81, E=1024, F=256, n_expert=32, n_used=8, mixed_types=True)
+    assert len(np.unique(layer.types)) == 8
+    check(oracle_mod, layer, synth.make_tokens(82, 11, layer.E), PATH_GENERIC, "mixed small")
+
+
+def test_generic_mixed_quant_layer_with_shared_expert(oracle_mod):
+    """The mixed-quant configuration: hidden 2048, 256 experts, top-8, F 512, all eight Gyro types
+    assigned by seed per expert and projection, a bf16 shared expert of width 1024, rotations."""
+    layer = synth.make_layer(91, mixed_types=True, SF=1024)
+    check(oracle_mod, layer, synth.make_tokens(92, 4, layer.E), PATH_GENERIC, "mixed quant + shared")
+
+
+def test_reference_path_with_shared_expert(oracle_mod):
+    layer = synth.make_layer(101, E=1024, F=256, n_expert=32, n_used=8, SF=256)
+    check(oracle_mod, layer, synth.make_tokens(102, 9, layer.E), PATH_REFERENCE, "reference + shared")
+    check(oracle_mod, layer, synth.make_tokens(103, 9, layer.E), PATH_GENERIC, "generic + shared")

@@ -168,3 +168,29 @@ def test_scale_zero_blocks_give_zero_output(oracle_mod):
             v[:, :, 1] = 0
     out = oracle_mod.OracleLayer(L).forward(synth.make_tokens(32, 3, L.E), threads=2)
     assert np.all(out == 0)
+
+
+def bf16_to_f64(bits):
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_shared_expert_matches_numpy(oracle_mod):
+    """The bf16 shared expert (src/engine.zig:644-653, dotHalf of src/kernels.zig:86-105): the
+    difference the shared expert makes to the oracle's output equals an fp64 numpy model of
+    sigmoid(g . x) * W_d (silu(W_g x) * W_u x) on the unrotated input."""
+    L = synth.make_layer(71, E=256, F=128, n_expert=16, n_used=4, SF=64)
+    x = synth.make_tokens(72, 5, L.E)
+    with_sh = oracle_mod.OracleLayer(L).forward(x, threads=2)
+    L0 = synth.make_layer(71, E=256, F=128, n_expert=16, n_used=4)
+    without = oracle_mod.OracleLayer(L0).forward(x, threads=2)
+    x64 = x.astype(np.float64)
+    g = x64 @ bf16_to_f64(L.sh_gate).T
+    u = x64 @ bf16_to_f64(L.sh_up).T
+    a = g / (1 + np.exp(-g)) * u
+    sh = a @ bf16_to_f64(L.sh_down).T
+    gate = 1 / (1 + np.exp(-(x64 @ L.sh_gate_inp.astype(np.float64))))
+    ref = gate[:, None] * sh
+    got = with_sh.astype(np.float64) - without.astype(np.float64)
+    assert oracle_mod.rel_rms(ref, got) < 1e-4
+    # A planted mistake (gate = 1, the "always on" reading) fails.
+    assert oracle_mod.rel_rms(sh, got) > 1e-2
