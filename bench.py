@@ -17,6 +17,11 @@ Reported beside the throughput:
   cpu_baseline  the CPU oracle (a C restatement of src/engine.zig ffn and its thread pool) on a
                 bounded sample of the same tokens, on this host's cores.
   parity        rel-RMS and cosine of the GPU outputs against that CPU sample.
+  --stack       (its own JSON line) the residual stack x <- x + MoE_l(RMSNorm_l(x)) of 48 distinct
+                seeded layers resident in HBM: batch 1, 8 (decode path), 32, 64 (prefill path) and
+                a 4096-token prefill, each with tok/s and the fraction of its binding roofline
+                (HBM: measured distinct experts' packed bytes plus the router matrices per step;
+                MFMA: routed-expert FLOPs), and the CPU oracle on a sample of 8 tokens.
   prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (four cycled
                 copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
                 and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
@@ -183,6 +188,99 @@ def prefill_cpu(layer, x, gpu_out):
             {"rel_rms": oracle.rel_rms(ref, gpu_out), "cosine": oracle.cosine(ref, gpu_out)})
 
 
+ROUTER_BYTES = N_EXPERT * E * 4  # fp32 router matrix read per layer and step
+LAYER_FLOPS_PER_TOKEN = TOP_K * 3 * 2 * E * F  # 50,331,648
+
+
+def stack_bench(args):
+    """The 48-layer residual stack: batch sweep and 4096-token prefill (see the module doc)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from gyrodx import synth
+    from gyrodx.engine import PATH_DECODE, PATH_PREFILL, Engine
+
+    n_layers = args.stack_layers
+    eng = Engine(max_tok=4096)
+    sample = synth.make_tokens(args.seed + 7, 8)
+    xo = sample.copy()  # the oracle's own (free-running) stack
+    xg = sample.copy()  # the GPU's stack after the layers so far
+    threads = cpu_threads()
+    cpu_s = 0.0
+    ids, layer_err, excluded = [], [], 0
+    t0 = time.perf_counter()
+    for l in range(n_layers):
+        L = synth.make_stack(args.seed + 100 + l, 1)[0]
+        ids.append(eng.add_layer(L))
+        ol = oracle.OracleLayer(L)
+        # Teacher-forced check of layer l: the oracle's step from the GPU's own stack state
+        # against the GPU's step (tokens with a near-tie at this layer's top-8 excluded).
+        xg_next = eng.forward_stack(ids, sample, PATH_DECODE)
+        h = oracle.rms_norm(xg, L.norm_weight, L.norm_eps)
+        t1 = time.perf_counter()
+        y = ol.forward(h, threads=threads)
+        cpu_s += time.perf_counter() - t1
+        p = ol.router_f64(h)
+        p = -np.sort(-np.exp(p - p.max(axis=1, keepdims=True)), axis=1)
+        sep = (p[:, TOP_K - 1] - p[:, TOP_K]) > 1e-5 * p[:, TOP_K - 1]
+        excluded += int((~sep).sum())
+        layer_err.append(oracle.rel_rms(y[sep], (xg_next - xg)[sep]) if sep.any() else 0.0)
+        xg = xg_next
+        xo = xo + ol.forward(oracle.rms_norm(xo, L.norm_weight, L.norm_eps), threads=threads)
+        del L, ol
+        if l % 8 == 7:
+            print(f"stack: {l + 1} of {n_layers} layers resident ({time.perf_counter() - t0:.0f} s)",
+                  file=sys.stderr, flush=True)
+    bundle_all = n_layers * N_EXPERT * BUNDLE_BYTES
+    points = []
+    for batch, path, calls in ((1, PATH_DECODE, 200), (8, PATH_DECODE, 100), (32, PATH_PREFILL, 50),
+                               (64, PATH_PREFILL, 50), (4096, PATH_PREFILL, 4)):
+        x = synth.make_tokens(args.seed + 200 + batch, batch * calls, bf16=path == PATH_PREFILL)
+        eng.set_tokens(x)
+        eng.run_stack(path, batch, 1, ids)  # warm-up
+        dev_ms, wall_ms = eng.run_stack(path, batch, calls, ids)
+        # Measured distinct experts per layer on the first batch: the stack's prefix up to each
+        # layer, then that layer's routes.
+        distinct = []
+        if batch <= 64:
+            for l in range(n_layers):
+                eng.forward_stack(ids[:l + 1], x[:batch], path)
+                r, _ = eng.last_routes(batch)
+                distinct.append(int(np.unique(r).size))
+        else:
+            distinct = [N_EXPERT] * n_layers  # every expert at 4096 tokens
+        step_s = wall_ms / calls * 1e-3
+        step_bytes = sum(distinct) * BUNDLE_BYTES + n_layers * ROUTER_BYTES
+        flops = batch * n_layers * LAYER_FLOPS_PER_TOKEN
+        hbm_gbs = step_bytes / step_s / 1e9
+        tflops = flops / step_s / 1e12
+        bound = "hbm" if step_bytes / (HBM_PEAK_GBS * 1e9) > flops / (MFMA_PEAK_TFLOPS * 1e12) else "mfma"
+        frac = hbm_gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / MFMA_PEAK_TFLOPS
+        points.append({"batch": batch, "path": "decode" if path == PATH_DECODE else "prefill", "calls": calls,
+                       "tok_s": round(batch / step_s, 1), "ms_per_step": round(step_s * 1e3, 4),
+                       "device_ms_per_step": round(dev_ms / calls, 4),
+                       "distinct_experts_per_layer": round(sum(distinct) / n_layers, 1),
+                       "bytes_per_step": step_bytes, "flops_per_step": flops,
+                       "hbm_gbs": round(hbm_gbs, 1), "tflops": round(tflops, 2),
+                       "roofline": {"bound": bound, "frac": round(frac, 4)}})
+        print(f"stack: batch {batch}: {points[-1]['tok_s']} tok/s", file=sys.stderr, flush=True)
+    eng.close()
+    return {
+        "workload": f"{n_layers}-layer residual MoE stack (RMSNorm -> MoE -> residual), hidden {E}, "
+                    f"{N_EXPERT} TQ2_T experts per layer, top-{TOP_K}, F {F}",
+        "layers": n_layers, "resident_expert_bytes": bundle_all,
+        "hbm_peak_gbs": HBM_PEAK_GBS, "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
+        "points": points,
+        "cpu_baseline": {"value": round(8 / cpu_s, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+                         "sample": f"8 decode tokens through all {n_layers} layers, {cpu_s:.1f} s on {threads} threads"},
+        "parity": {"teacher_forced_max_layer_rel_rms": round(max(layer_err), 7),
+                   "teacher_forced_mean_layer_rel_rms": round(float(np.mean(layer_err)), 7),
+                   "near_tie_token_layers_excluded": excluded,
+                   "free_running_per_token_rel_rms": [round(oracle.rel_rms(xo[t], xg[t]), 6) for t in range(8)],
+                   "note": "per layer: the oracle's MoE output from the GPU's stack state vs the GPU's; free "
+                           "running: 48 layers each way, where one routing flip changes a token's path"},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,6 +293,9 @@ def main() -> int:
     ap.add_argument("--prefill-calls", type=int, default=16, help="timed 1024-token prefill calls (0: skip)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="for profiling passes: only the prefill measurement, printed as its own JSON line")
+    ap.add_argument("--stack", action="store_true",
+                    help="the 48-layer stack batch sweep and 4096-token prefill, printed as its own JSON line")
+    ap.add_argument("--stack-layers", type=int, default=48)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
                          "copies of 32 MiB; prints the probe's shape and no benchmark line")
@@ -207,6 +308,9 @@ def main() -> int:
     from gyrodx import synth
     from gyrodx.engine import PATH_DECODE, Engine
 
+    if args.stack:
+        print(json.dumps({"stack": stack_bench(args)}), flush=True)
+        return 0
     layer = synth.make_layer(args.seed)
     if args.prefill_only:
         eng = Engine(max_tok=PREFILL_TOKENS)

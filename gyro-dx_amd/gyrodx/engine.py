@@ -17,7 +17,8 @@ class LayerDesc(C.Structure):
                 ("router", C.c_void_p), ("router_bias", C.c_void_p), ("gate_signs", C.c_void_p),
                 ("down_signs", C.c_void_p), ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
                 ("types", C.c_void_p), ("SF", C.c_uint32), ("sh_gate", C.c_void_p), ("sh_up", C.c_void_p),
-                ("sh_down", C.c_void_p), ("sh_gate_inp", C.c_void_p)]
+                ("sh_down", C.c_void_p), ("sh_gate_inp", C.c_void_p), ("norm_weight", C.c_void_p),
+                ("norm_eps", C.c_float)]
 
 
 _lib = None
@@ -46,6 +47,9 @@ def lib() -> C.CDLL:
         L.gm_run_bracketed.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, u32, C.POINTER(C.c_double),
                                        C.POINTER(C.c_double), C.POINTER(C.c_double)]
         L.gm_read_outputs.argtypes = [vp, f32p, u32]
+        L.gm_forward_stack.argtypes = [vp, C.POINTER(u32), u32, u32, f32p, u32, f32p]
+        L.gm_run_stack.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_double)]
         _lib = L
     return _lib
 
@@ -103,7 +107,9 @@ class Engine:
                       gate=ptrs(layer.gate), up=ptrs(layer.up), down=ptrs(layer.down),
                       types=ptr(np.ascontiguousarray(layer.types, np.uint32).reshape(-1)),
                       SF=layer.SF, sh_gate=ptr(layer.sh_gate), sh_up=ptr(layer.sh_up), sh_down=ptr(layer.sh_down),
-                      sh_gate_inp=ptr(None if layer.sh_gate_inp is None else np.asarray(layer.sh_gate_inp, np.float32)))
+                      sh_gate_inp=ptr(None if layer.sh_gate_inp is None else np.asarray(layer.sh_gate_inp, np.float32)),
+                      norm_weight=ptr(None if layer.norm_weight is None else np.asarray(layer.norm_weight, np.float32)),
+                      norm_eps=layer.norm_eps)
         idx = C.c_uint32()
         self._check(lib().gm_add_layer(self._h, C.byref(d), C.byref(idx)), "gm_add_layer")
         self.E, self.U, self.n_expert = layer.E, layer.n_used, layer.n_expert
@@ -148,6 +154,23 @@ class Engine:
         self._check(lib().gm_run_bracketed(self._h, path, batch, calls, first, arr, len(layers), bracket,
                                            C.byref(dev), C.byref(wall), C.byref(br)), "gm_run")
         return dev.value, wall.value, br.value
+
+    def forward_stack(self, layers, x: np.ndarray, path: int = PATH_DECODE) -> np.ndarray:
+        """x <- x + MoE_l(RMSNorm_l(x)) over the given layer indices."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        arr = (C.c_uint32 * len(layers))(*layers)
+        self._check(lib().gm_forward_stack(self._h, arr, len(layers), path, _f32p(x), x.shape[0], _f32p(out)),
+                    "gm_forward_stack")
+        return out
+
+    def run_stack(self, path: int, batch: int, calls: int, layers, first: int = 0):
+        """Timed stack passes over device-resident tokens; returns (device ms, wall ms)."""
+        arr = (C.c_uint32 * len(layers))(*layers)
+        dev, wall = C.c_double(), C.c_double()
+        self._check(lib().gm_run_stack(self._h, path, batch, calls, first, arr, len(layers), C.byref(dev),
+                                       C.byref(wall)), "gm_run_stack")
+        return dev.value, wall.value
 
     def read_outputs(self, n: int) -> np.ndarray:
         out = np.empty((n, self.E), np.float32)

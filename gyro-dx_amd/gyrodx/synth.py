@@ -26,7 +26,7 @@ TQ2_T = 144
 
 # Independent streams per quantity.
 STREAM_GATE, STREAM_UP, STREAM_DOWN, STREAM_ROUTER = 1, 2, 3, 4
-STREAM_SIGNS, STREAM_X, STREAM_ZIPF, STREAM_TYPES, STREAM_SHARED = 5, 6, 7, 8, 9
+STREAM_SIGNS, STREAM_X, STREAM_ZIPF, STREAM_TYPES, STREAM_SHARED, STREAM_NORM = 5, 6, 7, 8, 9, 10
 
 
 def row_bytes(type_id: int, cols: int) -> int:
@@ -78,6 +78,8 @@ class Layer:
     sh_up: np.ndarray | None = None
     sh_down: np.ndarray | None = None  # [E, SF] bf16 bits
     sh_gate_inp: np.ndarray | None = None  # [E] fp32
+    norm_weight: np.ndarray | None = None  # [E] fp32, RMSNorm of the layer's input in a stack
+    norm_eps: float = 1e-6
 
     def uniform_type(self) -> int | None:
         t = np.unique(self.types)
@@ -142,6 +144,16 @@ def make_layer(seed: int, E: int = 2048, F: int = 512, n_expert: int = 256, n_us
         layer.sh_down = bf16(sh.standard_normal((E, SF)) * 0.02)
         layer.sh_gate_inp = (sh.standard_normal(E) * 0.02).astype(np.float32)
     return layer
+
+
+def make_stack(seed: int, n_layers: int, **kw) -> list:
+    """n_layers layers seeded seed, seed + 1, ...; each with RMSNorm weights 1 + 0.1 N(0, 1)."""
+    layers = []
+    for l in range(n_layers):
+        L = make_layer(seed + l, **kw)
+        L.norm_weight = (1.0 + 0.1 * rng(seed + l, STREAM_NORM).standard_normal(L.E)).astype(np.float32)
+        layers.append(L)
+    return layers
 
 
 def make_tokens(seed: int, n: int, E: int = 2048, bf16: bool = False, stream: int = STREAM_X) -> np.ndarray:

@@ -63,6 +63,9 @@ struct Layer {
     float max_scale = 0;      // largest |block scale| over the layer's experts
     uint32_t SF = 0;          // shared expert width (0: none)
     Buffer sh_gu, sh_down, sh_gate;  // bf16 [2 SF][E] (gate rows, then up rows), [E][SF]; fp32 [E]
+    Buffer norm;                     // fp32 [E] RMSNorm weight of the layer's input in a stack
+    bool has_norm = false;
+    float norm_eps = 0;
 };
 
 // binary16 -> float for host-side range checks.
@@ -118,6 +121,7 @@ class Engine {
     Buffer sh_h, sh_a, sh_o, sh_g;  // shared expert: [T][2 SF], [T][SF], [T][E], [T]
     uint32_t sh_width = 0;          // SF the shared buffers are sized for
     Buffer tokens, outputs;
+    Buffer hn;  // stack: the normalised input of the current layer [T][E]
     uint32_t n_tokens = 0;
     uint32_t parts = 0;
     float max_codebook = 0;  // largest |codebook value|
@@ -223,6 +227,7 @@ class Engine {
         act = dev.buffer(T * U * F * f, Kind::device);
         down = dev.buffer(T * U * E * f, Kind::device);
         out = dev.buffer(T * E * f, Kind::device);
+        hn = dev.buffer(T * E * f, Kind::device);
         order = dev.buffer(T * U * 4, Kind::device);
         meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
         // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
@@ -267,7 +272,16 @@ class Engine {
         L.type_id = uniform ? d.types[0] : 0;
         L.gate_bytes = uniform ? (uint32_t)gb[0] : 0;
         if (!slot_stride) {
-            slot_stride = (uint32_t)((max_bundle + 255) & ~uint64_t(255));
+            // A first layer that mixes Gyro types reserves the bundle of the largest type, so
+            // that later mixed layers fit the same slots; a uniform first layer fixes the stride
+            // at its own bundle.
+            uint64_t stride = max_bundle;
+            if (!uniform) {
+                uint32_t widest = 0;
+                for (uint32_t t = 144; t <= 151; ++t) widest = std::max(widest, block_bytes_of(t));
+                stride = ((uint64_t)F * (E / 128) * 2 + (uint64_t)E * (F / 128)) * widest;
+            }
+            slot_stride = (uint32_t)((stride + 255) & ~uint64_t(255));
             per_arena = (uint32_t)(kArenaLimit / slot_stride);
             lookup = dev.buffer((uint64_t)kMaxArenas * per_arena * 4, Kind::host);
         } else if (max_bundle > slot_stride) {
@@ -320,6 +334,13 @@ class Engine {
         }
         L.signs = dev.buffer((E + F) * 4, Kind::device);
         upload(L.signs, 0, signs.data(), (E + F) * 4);
+        if (d.norm_weight) {
+            L.has_norm = true;
+            L.norm = dev.buffer((uint64_t)E * 4, Kind::device);
+            upload(L.norm, 0, d.norm_weight, (uint64_t)E * 4);
+        }
+        if (!(d.norm_eps >= 0.0f)) throw NativeError(-1, "norm_eps must be a non-negative number");
+        L.norm_eps = d.norm_eps;
         if (d.SF) {
             if (!d.sh_gate || !d.sh_up || !d.sh_down || !d.sh_gate_inp) throw NativeError(-1, "shared expert weights missing");
             L.SF = d.SF;
@@ -538,6 +559,41 @@ class Engine {
             throw NativeError(-1, "path not available");
     }
 
+    // One stack pass over n tokens whose residual stream starts at x (x_uav, x_off) and ends in
+    // (y_uav, y_off): per layer, the residual add of the previous layer's output and the layer's
+    // RMSNorm (moe_stack_norm, which also writes the stream to y), the MoE layer into `out`; the
+    // last layer's output is added by ew. y may be x.
+    void stack(const uint32_t *list, uint32_t n_layers, uint32_t path, uint32_t n, uint32_t x_uav, uint32_t x_off,
+               uint32_t y_uav, uint32_t y_off) {
+        if (E > 4096) throw NativeError(-1, "stack RMSNorm covers E <= 4096");
+        for (uint32_t l = 0; l < n_layers; ++l) {
+            const Layer &L = layers.at(list[l]);
+            const bool first = l == 0;
+            dispatch("moe_stack_norm", {first ? x_uav : y_uav, first ? x_off : y_off, first ? kNone : out.uav, 0,
+                                        L.has_norm ? L.norm.srv : kNone, 0, hn.uav, 0, E, bits(L.norm_eps), y_uav,
+                                        y_off},
+                     n);
+            ffn(path, list[l], n, hn.uav, 0, out.uav, 0);
+        }
+        dispatch("ew", {y_uav, y_off, E, out.uav, 0, E, y_uav, y_off, E, E, n, 2}, (E * n + 255) / 256);
+    }
+
+    void check_stack(const uint32_t *list, uint32_t n_layers) const {
+        if (!list || !n_layers) throw NativeError(-1, "empty layer list");
+        for (uint32_t l = 0; l < n_layers; ++l)
+            if (list[l] >= layers.size()) throw NativeError(-1, "layer index out of range");
+    }
+
+    void forward_stack(const uint32_t *list, uint32_t n_layers, uint32_t path, const float *x, uint32_t n, float *y) {
+        if (n == 0 || n > max_tok) throw NativeError(-1, "token count exceeds max_tok");
+        check_stack(list, n_layers);
+        upload(x_in, 0, x, (uint64_t)n * E * 4);
+        dev.begin();
+        stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
+        dev.wait(dev.submit());
+        check(gd_readback(dev.ctx, x_in.handle, 0, n * E * 4, y, kTimeoutMs), "gd_readback");
+    }
+
     void forward(uint32_t il, uint32_t path, const float *x, uint32_t n, float *y) {
         if (n == 0 || n > max_tok) throw NativeError(-1, "token count exceeds max_tok");
         upload(x_in, 0, x, (uint64_t)n * E * 4);
@@ -599,6 +655,12 @@ extern "C" int gm_add_layer(gm_engine *g, const gm_layer_desc *d, uint32_t *out_
 extern "C" int gm_forward(gm_engine *g, uint32_t layer, uint32_t path, const float *x, uint32_t n, float *y) {
     if (!x || !y) return -1;
     return guarded(g, [&] { g->e.forward(layer, path, x, n, y); });
+}
+
+extern "C" int gm_forward_stack(gm_engine *g, const uint32_t *layers, uint32_t n_layers, uint32_t path,
+                                const float *x, uint32_t n, float *out) {
+    if (!x || !out) return -1;
+    return guarded(g, [&] { g->e.forward_stack(layers, n_layers, path, x, n, out); });
 }
 
 extern "C" int gm_last_routes(gm_engine *g, uint32_t n, uint32_t *ids, float *weights) {
@@ -696,6 +758,37 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
 extern "C" int gm_run(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first_token,
                       const uint32_t *layer_list, uint32_t n_layers, double *device_ms, double *wall_ms) {
     return gm_run_bracketed(g, path, batch, calls, first_token, layer_list, n_layers, 0, device_ms, wall_ms, nullptr);
+}
+
+extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first_token,
+                            const uint32_t *layer_list, uint32_t n_layers, double *device_ms, double *wall_ms) {
+    if (!device_ms || !wall_ms) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        e.check_stack(layer_list, n_layers);
+        if (!e.n_tokens || !batch || batch > e.max_tok || (uint64_t)first_token + (uint64_t)batch * calls > e.n_tokens)
+            throw gyro::NativeError(-1, "run exceeds the uploaded tokens or max_tok");
+        // About 4000 dispatches per submission.
+        const uint32_t per_submit = std::max(1u, 4000u / (n_layers * 8u));
+        double dev = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint32_t first = 0; first < calls; first += per_submit) {
+            const uint32_t last = std::min(calls, first + per_submit);
+            e.dev.begin();
+            const uint32_t t_start = e.dev.timestamp();
+            for (uint32_t i = first; i < last; ++i) {
+                const uint32_t off = (first_token + i * batch) * e.E;
+                e.stack(layer_list, n_layers, path, batch, e.tokens.uav, off, e.outputs.uav, off);
+            }
+            const uint32_t t_end = e.dev.timestamp();
+            e.dev.wait(e.dev.submit());
+            std::vector<uint64_t> ticks(t_end + 1);
+            const uint64_t freq = e.dev.timestamps(ticks.data(), (uint32_t)ticks.size());
+            dev += (double)(ticks[t_end] - ticks[t_start]) * 1e3 / (double)freq;
+        }
+        *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        *device_ms = dev;
+    });
 }
 
 extern "C" int gm_read_outputs(gm_engine *g, float *y, uint32_t n_total) {

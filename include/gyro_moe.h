@@ -56,6 +56,10 @@ typedef struct gm_layer_desc {
     const uint16_t *sh_up;
     const uint16_t *sh_down;
     const float *sh_gate_inp;
+    /* RMSNorm applied to this layer's input inside a stack (gm_forward_stack, gm_run_stack): fp32
+     * weight [E] or NULL (no weight), and eps (src/kernels.zig:281-291). */
+    const float *norm_weight;
+    float norm_eps;
 } gm_layer_desc;
 
 /* Creates an engine on device `adapter`, loading every <name>.co pipeline in kernel_dir.
@@ -63,7 +67,10 @@ typedef struct gm_layer_desc {
 GM_API int gm_create(const char *kernel_dir, uint32_t adapter, uint32_t max_tok, gm_engine **out);
 GM_API void gm_destroy(gm_engine *e);
 GM_API const char *gm_last_error(gm_engine *e);
-/* Uploads a layer and returns its index. Layers of one engine share E, F, n_expert, n_used. */
+/* Uploads a layer and returns its index. Layers of one engine share E, F, n_expert, n_used.
+ * Every expert occupies one slot of a fixed stride set by the first layer: its own bundle when
+ * its experts share one Gyro type, the widest type's bundle when they mix types; a later layer
+ * whose bundle exceeds the stride is refused. */
 GM_API int gm_add_layer(gm_engine *e, const gm_layer_desc *desc, uint32_t *out_index);
 /* Runs n tokens (n <= max_tok) of x[n][E] through one layer on a path; writes out[n][E]. */
 GM_API int gm_forward(gm_engine *e, uint32_t layer, uint32_t path, const float *x, uint32_t n, float *out);
@@ -92,7 +99,15 @@ GM_API int gm_run(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, u
 GM_API int gm_run_bracketed(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first,
                             const uint32_t *layers, uint32_t n_layers, uint32_t bracket,
                             double *device_ms, double *wall_ms, double *bracket_us);
-/* Reads outputs[n_total][E] written by gm_run. */
+/* A stack of layers: x <- x + MoE_l(RMSNorm_l(x)) for l = layers[0..n_layers), on n <= max_tok
+ * tokens of x[n][E]; writes the final x to out[n][E]. */
+GM_API int gm_forward_stack(gm_engine *e, const uint32_t *layers, uint32_t n_layers, uint32_t path, const float *x,
+                            uint32_t n, float *out);
+/* As gm_run for a stack: each of `calls` calls takes `batch` device-resident tokens (from token
+ * `first`, as gm_run) through every layer of the stack, writing the results to the outputs. */
+GM_API int gm_run_stack(gm_engine *e, uint32_t path, uint32_t batch, uint32_t calls, uint32_t first,
+                        const uint32_t *layers, uint32_t n_layers, double *device_ms, double *wall_ms);
+/* Reads outputs[n_total][E] written by gm_run or gm_run_stack. */
 GM_API int gm_read_outputs(gm_engine *e, float *out, uint32_t n_total);
 
 #ifdef __cplusplus

@@ -31,7 +31,11 @@
  *   go_router_f64        (test_layer_matches_numpy_fp64).
  *   go_dot_bf16          the bf16 shared expert against an fp64 numpy model of its algebra
  *                        (test_shared_expert_matches_numpy).
- *   go_rms_norm          parity unpinned: RMSNorm is not yet checked by any test.
+ *   go_rms_norm          closed forms (a constant row c gives sign(c) / sqrt(1 + eps / c^2) * w;
+ *                        unit mean square at eps = 0; scale invariance) and an fp64 numpy model,
+ *                        with planted mistakes (sum for mean, a dropped weight) that must fail
+ *                        (test_rms_norm_closed_forms); the stack of layers is pinned through it
+ *                        and the layer (test_stack_matches_numpy).
  */
 #ifndef GYRO_ORACLE_H
 #define GYRO_ORACLE_H

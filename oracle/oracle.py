@@ -51,6 +51,7 @@ def lib():
     L.go_moe_ffn.argtypes = [C.c_void_p, f32p, C.c_size_t, f32p, C.c_void_p, C.c_uint32]
     L.go_moe_dense_f64.argtypes = [C.c_void_p, f32p, C.c_size_t, u32p, f32p, C.POINTER(C.c_double)]
     L.go_router_f64.argtypes = [C.c_void_p, f32p, C.c_size_t, C.POINTER(C.c_double)]
+    L.go_rms_norm.argtypes = [f32p, f32p, f32p, C.c_size_t, C.c_float]
     cb = np.frombuffer(CODEBOOK.read_bytes(), dtype=np.uint8)
     rc = L.go_init(cb.ctypes.data_as(u8p), cb.size)
     if rc != 0:
@@ -199,6 +200,27 @@ class OracleLayer:
         out = np.empty((x.shape[0], self.layer.n_expert), dtype=np.float64)
         lib().go_router_f64(C.byref(self.struct), _p(x, C.c_float), x.shape[0], _p(out, C.c_double))
         return out
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+    """go_rms_norm (src/kernels.zig:281-291) on each row of x."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(rows)
+    wp = None if w is None else _p(np.ascontiguousarray(w, dtype=np.float32), C.c_float)
+    for i in range(rows.shape[0]):
+        lib().go_rms_norm(_p(out[i], C.c_float), _p(rows[i], C.c_float), wp, rows.shape[1], eps)
+    return out.reshape(x.shape)
+
+
+def stack_forward(layers, x: np.ndarray, threads: int | None = None) -> np.ndarray:
+    """The residual MoE stack x <- x + MoE_l(RMSNorm_l(x)) over synth layers (rmsNorm of
+    src/kernels.zig:281-291, the MoE layer of src/engine.zig:520-687, a plain residual add)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    for L in layers:
+        h = rms_norm(x, L.norm_weight, L.norm_eps)
+        x = x + OracleLayer(L).forward(h, threads=threads)
+    return x
 
 
 def rel_rms(ref, cand) -> float:

@@ -24,7 +24,7 @@ def exported(lib):
 
 @pytest.mark.parametrize("lib,header,prefix,count", [
     ("libgyro_native.so", "gyro_native.h", "gd_", 27),
-    ("libgyro_moe.so", "gyro_moe.h", "gm_", 12),
+    ("libgyro_moe.so", "gyro_moe.h", "gm_", 14),
 ])
 def test_exports(lib, header, prefix, count):
     path = BUILD / lib
@@ -56,5 +56,6 @@ def test_kernels_built():
     reference = {"mv_f32", "mv_bf16", "moe_route", "moe_resolve", "moe_gyro", "moe_act", "rotate128",
                  "moe_combine", "ew", "gyro_decode", "linalg_smoke", "moe_gyro_x"}
     fast = {"moe_router", "moe_decode_gu", "moe_decode_down", "moe_dequant", "moe_prefill_router",
-            "moe_prefill_topk", "moe_prefill_sort", "moe_prefill_gu", "moe_prefill_down", "moe_prefill_combine"}
+            "moe_prefill_topk", "moe_prefill_sort", "moe_prefill_gu", "moe_prefill_down", "moe_prefill_combine",
+            "moe_stack_norm"}
     assert reference | fast <= kernels, (reference | fast) - kernels

@@ -194,3 +194,49 @@ def test_shared_expert_matches_numpy(oracle_mod):
     assert oracle_mod.rel_rms(ref, got) < 1e-4
     # A planted mistake (gate = 1, the "always on" reading) fails.
     assert oracle_mod.rel_rms(sh, got) > 1e-2
+
+
+def test_rms_norm_closed_forms(oracle_mod):
+    """rmsNorm, src/kernels.zig:281-291: out = x / sqrt(mean(x^2) + eps) * w."""
+    g = np.random.default_rng(81)
+    n = 2048
+    # A constant row c: mean square c^2, so out = sign(c) / sqrt(1 + eps / c^2) * w.
+    for c, eps in ((3.0, 1e-6), (-0.25, 1e-2), (1e-3, 1e-6)):
+        w = g.standard_normal(n).astype(np.float32)
+        out = oracle_mod.rms_norm(np.full((1, n), c, np.float32), w, eps)[0]
+        expect = np.sign(c) / np.sqrt(1 + eps / c ** 2) * w.astype(np.float64)
+        np.testing.assert_allclose(out, expect, rtol=2e-6, atol=1e-7)
+    # Unit mean square without weight at eps = 0, and invariance to a positive scale.
+    x = g.standard_normal((4, n)).astype(np.float32)
+    out = oracle_mod.rms_norm(x, None, 0.0)
+    np.testing.assert_allclose(np.mean(out.astype(np.float64) ** 2, axis=1), 1.0, rtol=1e-5)
+    np.testing.assert_allclose(oracle_mod.rms_norm(x * 8.0, None, 0.0), out, rtol=1e-5, atol=1e-6)
+    # An fp64 numpy model with weight and eps.
+    w = (1 + 0.1 * g.standard_normal(n)).astype(np.float32)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 ** 2, axis=1, keepdims=True) + 1e-6) * w
+    got = oracle_mod.rms_norm(x, w, 1e-6)
+    assert oracle_mod.rel_rms(ref, got) < 1e-6
+    # Planted mistakes fail: the sum in place of the mean, and a dropped weight.
+    bad = x64 / np.sqrt(np.sum(x64 ** 2, axis=1, keepdims=True) + 1e-6) * w
+    assert oracle_mod.rel_rms(bad, got) > 0.5
+    bad = x64 / np.sqrt(np.mean(x64 ** 2, axis=1, keepdims=True) + 1e-6)
+    assert oracle_mod.rel_rms(bad, got) > 0.05
+
+
+def test_stack_matches_numpy(oracle_mod):
+    """The residual stack x <- x + MoE_l(RMSNorm_l(x)) over three layers against the fp64 numpy
+    model of each step; dropping the residual or the norm weight fails."""
+    layers = synth.make_stack(91, 3, E=256, F=128, n_expert=16, n_used=4)
+    x = synth.make_tokens(92, 3, 256)
+    got = oracle_mod.stack_forward(layers, x, threads=2)
+    ref = x.astype(np.float64)
+    no_res = None
+    for L in layers:
+        h = ref / np.sqrt(np.mean(ref ** 2, axis=1, keepdims=True) + L.norm_eps) * L.norm_weight
+        y, _, _ = numpy_layer(oracle_mod, L, h.astype(np.float32))
+        if no_res is None:
+            no_res = y
+        ref = ref + y
+    assert oracle_mod.rel_rms(ref, got) < 1e-5
+    assert oracle_mod.rel_rms(no_res, got) > 0.1
