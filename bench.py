@@ -232,8 +232,10 @@ def stack_bench(args):
                   file=sys.stderr, flush=True)
     bundle_all = n_layers * N_EXPERT * BUNDLE_BYTES
     points = []
-    for batch, path, calls in ((1, PATH_DECODE, 200), (8, PATH_DECODE, 100), (32, PATH_PREFILL, 50),
-                               (64, PATH_PREFILL, 50), (4096, PATH_PREFILL, 4)):
+    sweep = ((1, PATH_DECODE, 200), (8, PATH_DECODE, 100), (32, PATH_PREFILL, 50), (64, PATH_PREFILL, 50),
+             (4096, PATH_PREFILL, 4))
+    wanted = {int(b) for b in args.stack_batches.split(",")}
+    for batch, path, calls in (p for p in sweep if p[0] in wanted):
         x = synth.make_tokens(args.seed + 200 + batch, batch * calls, bf16=path == PATH_PREFILL)
         eng.set_tokens(x)
         eng.run_stack(path, batch, 1, ids)  # warm-up
@@ -296,6 +298,7 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true",
                     help="the 48-layer stack batch sweep and 4096-token prefill, printed as its own JSON line")
     ap.add_argument("--stack-layers", type=int, default=48)
+    ap.add_argument("--stack-batches", default="1,8,32,64,4096", help="sweep points of --stack (of 1,8,32,64,4096)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
                          "copies of 32 MiB; prints the probe's shape and no benchmark line")

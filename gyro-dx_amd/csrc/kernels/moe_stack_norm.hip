@@ -4,8 +4,8 @@
 //   xo[t] = v                            (when given: the residual stream after the add)
 //   h[t]  = v / sqrt(mean(v^2) + eps) * w
 // One group per token, 256 threads, up to 16 values per thread (E <= 4096). The sum of squares
-// is reduced per wave with shuffles, then over the four waves in order. xo may alias x (each
-// thread reads its own elements before it writes them).
+// is reduced per wave with shuffles, then over the four waves in order. xo may alias x: every
+// load of a thread comes before its first store, so the loads need not wait for the stores.
 // Grid: n tokens; 256 threads.
 // Constants: 0 x_uav 1 x_off 2 add_uav (0xffffffff: none) 3 add_off 4 w_srv (0xffffffff: none)
 // 5 w_off 6 h_uav 7 h_off 8 E 9 eps (fp32 bits) 10 xo_uav (0xffffffff: none) 11 xo_off.
@@ -28,12 +28,15 @@ GD_PIPELINE_NAMED(moe_stack_norm, 256) {
     for (int j = 0; j < SN_PER; ++j) {
         const uint32_t i = tid + 256u * j;
         v[j] = 0.f;
-        if (i < E) {
-            float x = X[i];
-            if (add) x += A[i];
-            if (keep) XO[i] = x;
-            v[j] = x;
-            ss += x * x;
+        if (i < E) v[j] = add ? X[i] + A[i] : X[i];
+    }
+#pragma unroll
+    for (int j = 0; j < SN_PER; ++j) ss += v[j] * v[j];
+    if (keep) {
+#pragma unroll
+        for (int j = 0; j < SN_PER; ++j) {
+            const uint32_t i = tid + 256u * j;
+            if (i < E) XO[i] = v[j];
         }
     }
     ss = gd_wave_sum(ss);

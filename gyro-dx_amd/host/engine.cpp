@@ -102,6 +102,13 @@ std::vector<uint8_t> read_file(const std::string &path) {
 
 }  // namespace
 
+// Residual stream of a stack step: the layer input is normalised by the layer's RMSNorm inside
+// the path's first kernel, and the path's last kernel adds res to its output.
+struct StackStep {
+    bool on = false;
+    uint32_t res_uav = kNone, res_off = 0;
+};
+
 class Engine {
   public:
     Device dev;
@@ -487,7 +494,7 @@ class Engine {
 
     // MI355X decode path: router + rotation, routed gate/up, down + combine.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
-                    int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
+                    int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
             throw NativeError(-1, "decode path needs TQ2_T, no shared expert, E % 1024 == 0, F == 512, top-8 of <= 256 "
@@ -495,7 +502,9 @@ class Engine {
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
-                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
+                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
+                              st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
+                              bits(L.norm_eps)},
                              std::max(NE, E / 128));
         dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
                              {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0, base_lo,
@@ -504,7 +513,7 @@ class Engine {
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
                              {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
                               2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                              out_off, E, F, U, n, parts, NE},
+                              out_off, E, F, U, n, parts, NE, st.res_uav, st.res_off},
                              E / 8, n);
     }
 
@@ -518,7 +527,8 @@ class Engine {
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
     // down GEMMs, combine. bracket: 1 router, 2 gate/up, 3 down, 4 top-k, 5 sort, 6 combine.
     void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
-                     int bracket = 0, std::vector<uint32_t> *marks = nullptr) {
+                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, uint32_t res_uav = kNone,
+                     uint32_t res_off = 0) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
             throw NativeError(-1, "prefill path needs TQ2_T, no shared expert, E and F multiples of 256, top-8 of "
@@ -542,7 +552,8 @@ class Engine {
                               codebook.srv, down.uav, 0, E, F},
                              tiles, E / 128);
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
-                             {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U}, (E + 1023) / 1024, n);
+                             {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav, res_off}, (E + 1023) / 1024,
+                             n);
     }
 
     void ffn(uint32_t path, uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav,
@@ -560,22 +571,39 @@ class Engine {
     }
 
     // One stack pass over n tokens whose residual stream starts at x (x_uav, x_off) and ends in
-    // (y_uav, y_off): per layer, the residual add of the previous layer's output and the layer's
-    // RMSNorm (moe_stack_norm, which also writes the stream to y), the MoE layer into `out`; the
-    // last layer's output is added by ew. y may be x.
+    // (y_uav, y_off); y may be x. Per layer l, with s the stream (x before the first layer, y
+    // after): y = s + MoE_l(RMSNorm_l(s)).
+    //   decode:    the router normalises s itself and the down kernel adds s (three launches);
+    //   prefill:   moe_stack_norm writes RMSNorm_l(s) to hn, the combine adds s;
+    //   others:    moe_stack_norm also adds the previous layer's output (in `out`) to the stream
+    //              and writes it to y; the path writes `out`; ew adds the last one.
     void stack(const uint32_t *list, uint32_t n_layers, uint32_t path, uint32_t n, uint32_t x_uav, uint32_t x_off,
                uint32_t y_uav, uint32_t y_off) {
         if (E > 4096) throw NativeError(-1, "stack RMSNorm covers E <= 4096");
         for (uint32_t l = 0; l < n_layers; ++l) {
             const Layer &L = layers.at(list[l]);
             const bool first = l == 0;
-            dispatch("moe_stack_norm", {first ? x_uav : y_uav, first ? x_off : y_off, first ? kNone : out.uav, 0,
-                                        L.has_norm ? L.norm.srv : kNone, 0, hn.uav, 0, E, bits(L.norm_eps), y_uav,
-                                        y_off},
-                     n);
-            ffn(path, list[l], n, hn.uav, 0, out.uav, 0);
+            const uint32_t s_uav = first ? x_uav : y_uav, s_off = first ? x_off : y_off;
+            const uint32_t w_srv = L.has_norm ? L.norm.srv : kNone;
+            if (path == GM_PATH_DECODE) {
+                StackStep st;
+                st.on = true;
+                st.res_uav = s_uav;
+                st.res_off = s_off;
+                ffn_decode(list[l], n, s_uav, s_off, y_uav, y_off, 0, nullptr, st);
+            } else if (path == GM_PATH_PREFILL) {
+                dispatch("moe_stack_norm",
+                         {s_uav, s_off, kNone, 0, w_srv, 0, hn.uav, 0, E, bits(L.norm_eps), kNone, 0}, n);
+                ffn_prefill(list[l], n, hn.uav, 0, y_uav, y_off, 0, nullptr, s_uav, s_off);
+            } else {
+                dispatch("moe_stack_norm", {s_uav, s_off, first ? kNone : out.uav, 0, w_srv, 0, hn.uav, 0, E,
+                                            bits(L.norm_eps), y_uav, y_off},
+                         n);
+                ffn(path, list[l], n, hn.uav, 0, out.uav, 0);
+                if (l + 1 == n_layers)
+                    dispatch("ew", {y_uav, y_off, E, out.uav, 0, E, y_uav, y_off, E, E, n, 2}, (E * n + 255) / 256);
+            }
         }
-        dispatch("ew", {y_uav, y_off, E, out.uav, 0, E, y_uav, y_off, E, E, n, 2}, (E * n + 255) / 256);
     }
 
     void check_stack(const uint32_t *list, uint32_t n_layers) const {
