@@ -14,8 +14,10 @@
 // Constants: 0 gu_uav 1 gu_off 2 ids_uav 3 ids_off 4 weights_uav 5 weights_off 6 base_lo
 // 7 base_hi 8 slot_stride 9 down_off (bytes from an expert's bundle start) 10 codebook_srv
 // 11 signs_srv (0xffffffff: none) 12 signs_off 13 out_uav 14 out_off 15 E 16 F 17 n_used
-// 18 n_tok 19 parts 20 n_expert 21 res_uav (0xffffffff: none) 22 res_off: when given, each
-// output adds res[t][row] after the combine (the residual step of a stack; res may alias out).
+// 18 n_tok 19 parts 20 n_expert 21 residual (0: none, 1: add) 22 res_uav 23 res_off: with the
+// residual each output adds res[t][row] after the combine (the residual step of a stack; res
+// may alias out). Constants past the caller's count read zero, so a 21-constant dispatch has
+// no residual.
 // Requires TQ2_T experts, n_used == 8, F == 512 and at most 2 K-parts.
 #include "gyro_fast.h"
 
@@ -172,7 +174,7 @@ GD_PIPELINE_NAMED(moe_decode_down, 256) {
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < DN_U; ++k) acc += wts[k] * dk[k][tid];
-        if (a.c[21] != 0xffffffffu) acc = gd_buf<const float>(a, a.c[21])[a.c[22] + t * E + row0 + tid] + acc;
+        if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + t * E + row0 + tid] + acc;
         gd_buf<float>(a, a.c[13])[a.c[14] + t * E + row0 + tid] = acc;
     }
 }

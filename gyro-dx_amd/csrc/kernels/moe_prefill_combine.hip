@@ -4,7 +4,8 @@
 //   the residual step of a stack; res may alias out)
 // Grid: (ceil(E / 1024), n); 256 threads, four columns per thread.
 // Constants: 0 down32_uav 1 down32_off 2 weights_uav 3 weights_off 4 out_uav 5 out_off
-// 6 E 7 n_used 8 res_uav (0xffffffff: none) 9 res_off.
+// 6 E 7 n_used 8 residual (0: none, 1: add; zero when the caller passes 8 constants) 9 res_uav
+// 10 res_off.
 #include "gd_kernel.h"
 
 GD_PIPELINE_NAMED(moe_prefill_combine, 256) {
@@ -22,8 +23,8 @@ GD_PIPELINE_NAMED(moe_prefill_combine, 256) {
         acc.z += w * d.z;
         acc.w += w * d.w;
     }
-    if (a.c[8] != 0xffffffffu) {
-        const float4 r = *reinterpret_cast<const float4 *>(gd_buf<const float>(a, a.c[8]) + a.c[9] + (size_t)t * E + c);
+    if (a.c[8]) {
+        const float4 r = *reinterpret_cast<const float4 *>(gd_buf<const float>(a, a.c[9]) + a.c[10] + (size_t)t * E + c);
         acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
     }
     *reinterpret_cast<float4 *>(gd_buf<float>(a, a.c[4]) + a.c[5] + (size_t)t * E + c) = acc;

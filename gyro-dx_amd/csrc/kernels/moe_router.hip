@@ -12,7 +12,8 @@
 // Constants: 0 x_uav 1 x_off 2 x_stride 3 n_tok 4 router_srv 5 router_off 6 n_expert 7 E
 // 8 bias_srv (0xffffffff: none) 9 bias_off 10 logits_uav 11 logits_off 12 signs_srv
 // (0xffffffff: copy) 13 signs_off 14 xh16_uav 15 xh16_off (words) 16 norm (0: none, 1: RMSNorm
-// without weight, 2: with weight) 17 norm_w_srv 18 norm_w_off 19 eps (fp32 bits).
+// without weight, 2: with weight; zero when the caller passes 16 constants) 17 norm_w_srv
+// 18 norm_w_off 19 eps (fp32 bits).
 #include "fwht.h"
 
 #define ROUTER_MAX_TOK 8

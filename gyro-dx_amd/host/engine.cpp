@@ -513,7 +513,7 @@ class Engine {
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
                              {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
                               2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                              out_off, E, F, U, n, parts, NE, st.res_uav, st.res_off},
+                              out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
                              E / 8, n);
     }
 
@@ -552,7 +552,9 @@ class Engine {
                               codebook.srv, down.uav, 0, E, F},
                              tiles, E / 128);
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
-                             {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav, res_off}, (E + 1023) / 1024,
+                             {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u, res_uav,
+                              res_off},
+                             (E + 1023) / 1024,
                              n);
     }
 
