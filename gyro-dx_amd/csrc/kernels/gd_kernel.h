@@ -59,6 +59,9 @@ __device__ __forceinline__ float gd_half_exact(uint32_t h) {
 __device__ __forceinline__ float gd_silu(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float gd_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float gd_silu_accurate(float x) { return x / (1.0f + expf(-x)); }
+// silu through the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of an IEEE division;
+// for results rounded to binary16 afterwards.
+__device__ __forceinline__ float gd_silu_rcp(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float gd_sigmoid_accurate(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Gyro type table, src/gyro.zig:32-41: k (new bits per step), steps, block bytes.

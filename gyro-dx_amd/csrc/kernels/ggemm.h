@@ -80,6 +80,30 @@ __device__ __forceinline__ uint32_t gg_chunk(uint32_t wave, uint32_t lane, int i
     return ((lane & 15u) ^ (row & 15u)) * 16u;
 }
 
+// Eight-wave groups: wave w fills activation rows 16 w .. 16 w + 15 with 4 loads of 4 rows.
+__device__ __forceinline__ void gg_stage_a8(GgLds &sm, uint32_t buf, uint32_t wave, const void *gbase,
+                                            const uint32_t roff[4], uint32_t kb) {
+    const uint32_t base = gg_lds_addr(&sm.a[buf][0]) + wave * 16u * GG_ROW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gg_dma16(base + i * 4u * GG_ROW, gbase, roff[i] + kb * 256u);
+}
+__device__ __forceinline__ uint32_t gg_chunk8(uint32_t wave, uint32_t lane, int i, uint32_t &row) {
+    row = wave * 16u + (uint32_t)i * 4u + (lane >> 4);
+    return ((lane & 15u) ^ (row & 15u)) * 16u;
+}
+
+// Eight-wave groups, 256 weight rows (768 pieces of 16 bytes): waves 0..3 issue loads 2 w and
+// 2 w + 1, waves 4..7 load 4 + w; load L covers pieces 64 L .. 64 L + 63 at LDS byte 1024 L of
+// the buffer.
+__device__ __forceinline__ uint32_t gg_w8_load(uint32_t wave, int i) { return wave < 4u ? wave * 2u + (uint32_t)i : wave + 4u; }
+__device__ __forceinline__ void gg_stage_w8(GgLds &sm, uint32_t buf, uint32_t wave, const void *wbase,
+                                            const uint32_t woff[2], uint32_t kb) {
+    const uint32_t base = gg_lds_addr(&sm.w[buf][0]);
+    const uint32_t kbo = (kb * 34u) & ~3u;
+    gg_dma16(base + gg_w8_load(wave, 0) * 1024u, wbase, woff[0] + kbo);
+    if (wave < 4u) gg_dma16(base + gg_w8_load(wave, 1) * 1024u, wbase, woff[1] + kbo);
+}
+
 // Weight blocks of K block kb into buffer buf: NW loads per wave of 64 lanes, 3 lanes (48 bytes)
 // per weight row, so the 4 waves cover 4 NW 64 / 3 rows; woff[i] is the byte offset (from
 // wbase) of this lane's 16 bytes of block 0, and block kb adds (34 kb) & ~3.

@@ -4,18 +4,21 @@
 //   a = H_128 (down_signs * silu(g) * u)    src/engine.zig:603-607
 //
 // A group takes one tile of the sort (expert e, up to 128 sorted rows) and one 128-column block
-// of F. Wave w owns F columns 32 w .. 32 w + 31 of the block for both gate and up, so no
-// weight is decoded twice; each decoded fragment feeds all of the tile's 32-row blocks
-// (v_mfma_f32_32x32x16_f16, fp32 accumulation). K runs over the E / 128 Gyro blocks: the
-// tile's activation rows (binary16 rows of the rotated input, gathered through route_order)
-// and the 256 weight rows' blocks arrive in LDS by direct loads issued two blocks ahead
-// (ggemm.h); each lane decodes the block of its own gate and up rows into B operands.
+// of F. Eight waves: wave w owns F columns 32 (w % 4) .. + 31 of the block for the gate (w < 4)
+// or the up projection (w >= 4), so no weight is decoded twice, and the gate and up waves of one
+// column range share a SIMD: while one issues MFMAs the other decodes. Each decoded fragment
+// feeds all of the tile's 32-row blocks (v_mfma_f32_32x32x16_f16, fp32 accumulation). K runs
+// over the E / 128 Gyro blocks: the tile's activation rows (binary16 rows of the rotated input,
+// gathered through route_order) and the 256 weight rows' blocks arrive in LDS by direct loads
+// issued two blocks ahead (ggemm.h); each lane decodes the block of its own row into B operands.
 // The fp16 products scale x codebook stay finite: the host checks every layer's scales.
-// Epilogue: silu(g) * u times the down signs, rounded to binary16 into LDS rows, the 128-point
-// Walsh-Hadamard transform of every row as one more fp16 MFMA product with H_128 (exact +-1
-// entries, fp32 accumulation, then x 1/sqrt(128)), and binary16 rows act16[sorted row][F].
-// Grid: (max tiles, F / 128); 256 threads, one group per CU (141 KB of LDS); the groups beyond
-// the sort's tile count exit.
+// Epilogue: the up waves pass u through LDS (fp32); the gate waves form silu(g) * u times the
+// down signs, rounded to binary16 into LDS rows; the 128-point Walsh-Hadamard transform of every
+// row runs as one more fp16 MFMA product with H_128 (exact +-1 entries, fp32 accumulation, then
+// x 1/sqrt(128)), split over the eight waves; binary16 rows go to act16[sorted row][F].
+// Grid: (F / 128, max tiles); 512 threads, one group per CU (141 KB of LDS); groups start tile
+// by tile in the sort's longest-first order, all column blocks of a tile together; the groups
+// beyond the sort's tile count exit.
 // Requires TQ2_T experts, E % 256 == 0 (rows start at 4-byte boundaries, an even block count),
 // F % 128 == 0, |xh|, |act| < 65504.
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 xh16_uav 4 xh16_off (words) 5 base_lo
@@ -23,78 +26,65 @@
 // 11 signs_off 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used.
 #include "ggemm.h"
 
-#define GU_LOADS 11        // global-to-LDS loads per wave and K block: 8 activation + 3 weight
-
 struct GuState {
     const void *xbase, *wbase;  // activation rows; the layer's slot arena (expert bundles)
-    uint32_t roff[8], woff[3];
-    uint32_t wave, m, h, sel, nk;
+    uint32_t roff[4], woff[2];
+    uint32_t wave, m, h, sel, nk, wq;  // wq: the staged weight row this lane decodes
 };
+
+// Start of K block kb: this wave's loads of block kb have landed once at most the loads of
+// block kb + 1 are outstanding (4 activation loads, plus 2 or 1 weight loads by wave class).
+__device__ __forceinline__ void gu_sync(const GuState &t, uint32_t kb) {
+    if (kb + 1u < t.nk) {
+        if (t.wave < 4u) gg_sync<6>();
+        else gg_sync<5>();
+    } else {
+        gg_sync<0>();
+    }
+}
 
 // K block kb from buffer BUF for NRB 32-row blocks; stages block kb + 2 into buffer
 // (BUF + 2) % 3, the buffer of block kb - 1, which every wave has left once past the sync.
 template <int BUF, int NRB>
-__device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb, f32x16 (&accg)[NRB],
-                                        f32x16 (&accu)[NRB]) {
-    if (kb + 1u < t.nk) gg_sync<GU_LOADS>();
-    else gg_sync<0>();
+__device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb, f32x16 (&acc)[NRB]) {
+    gu_sync(t, kb);
     if (kb + 2u < t.nk) {
-        gg_stage_a(sm, (BUF + 2) % 3, t.wave, t.xbase, t.roff, kb + 2u);
-        gg_stage_w<3>(sm, (BUF + 2) % 3, t.wave, t.wbase, t.woff, kb + 2u);
+        gg_stage_a8(sm, (BUF + 2) % 3, t.wave, t.xbase, t.roff, kb + 2u);
+        gg_stage_w8(sm, (BUF + 2) % 3, t.wave, t.wbase, t.woff, kb + 2u);
     }
-    GgBlk gc, uc;
-    gg_read_w(sm, BUF, t.wave * 32u + t.m, gc);
-    gg_read_w(sm, BUF, 128u + t.wave * 32u + t.m, uc);
-    const bool odd = kb & 1u;
-    float gs, us;
-    uint32_t gq[8], uq[8];
-    tq2_unpack(gc.d, odd, gs, gq);
-    tq2_unpack(uc.d, odd, us, uq);
-    const half2_t gs2 = {(_Float16)gs, (_Float16)gs}, us2 = {(_Float16)us, (_Float16)us};
+    GgBlk wc;
+    gg_read_w(sm, BUF, t.wq, wc);
+    float sc;
+    uint32_t q[8];
+    tq2_unpack(wc.d, kb & 1u, sc, q);
+    const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
     // Software pipeline over the 8 K-steps with an explicit schedule (sched_barrier fences keep
-    // the compiler from regrouping it). Everything step s + 1 reads from LDS is issued during
-    // step s, between its MFMAs: first the codebook gathers of its decode (one trellis state per
-    // piece), then its A operands. LDS reads retire in order, so step s + 1 finds them complete
-    // and never waits inside its MFMA sequence.
-    uint32_t rg[4], ru[4], pg = 0, pu = 0;
-    gg_gather(gq, 0, t.sel, sm.book, rg);
-    gg_gather(uq, 0, t.sel, sm.book, ru);
+    // the compiler from regrouping it): between the MFMAs of step s go the codebook gathers of
+    // step s + 1 (one trellis state per piece, over the first two slots) and its A operands
+    // (one per slot). LDS reads retire in order, so step s + 1 finds them complete.
+    uint32_t raw[4], pr = 0;
+    gg_gather(q, 0, t.sel, sm.book, raw);
     f16x8 av[NRB];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) av[rb] = gg_a(sm, BUF, rb * 32u + t.m, 0, t.h);
-    constexpr int kSlots = 2 * NRB;
-    constexpr int kPieceSlots = kSlots < 4 ? kSlots : 4;  // slots that carry gathers
+    constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const f16x8 bg = gg_scale(rg, gs2), bu = gg_scale(ru, us2);
+        const f16x8 bv = gg_scale(raw, sc2);
         f16x8 cur[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) cur[rb] = av[rb];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-            const int rb = i >> 1;
-            if ((i & 1) == 0) accg[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[rb], bg, accg[rb], 0, 0, 0);
-            else accu[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[rb], bu, accu[rb], 0, 0, 0);
+        for (int i = 0; i < NRB; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (s < 7) {
-                // Gathers: pieces 0..3 = (gate state a, gate state b, up a, up b) over the first
-                // kPieceSlots slots.
 #pragma unroll
-                for (int piece = 0; piece < 4; ++piece) {
-                    if (i < kPieceSlots && piece * kPieceSlots / 4 == i) {
-                        if (piece < 2) gg_gather_piece(gq, s + 1, piece, t.sel, sm.book, pg, rg);
-                        else gg_gather_piece(uq, s + 1, piece - 2, t.sel, sm.book, pu, ru);
-                    }
-                }
-                // A operands of step s + 1 over the remaining slots (all in the last slot when
-                // every slot carries gathers).
-#pragma unroll
-                for (int r = 0; r < NRB; ++r) {
-                    const int slot = kSlots - NRB + r;
-                    if (slot == i || (slot < kPieceSlots && i == kSlots - 1))
-                        av[r] = gg_a(sm, BUF, r * 32u + t.m, s + 1, t.h);
-                }
+                for (int piece = 0; piece < 2; ++piece)
+                    if (i < kPieceSlots && piece * kPieceSlots / 2 == i)
+                        gg_gather_piece(q, s + 1, piece, t.sel, sm.book, pr, raw);
+                av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -105,97 +95,104 @@ __device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb
 template <int NRB>
 __device__ __forceinline__ void gu_tile(GgLds &sm, const GuState &t, const GdArgs &a, uint32_t row0, uint32_t rows,
                                         uint32_t fb, uint32_t F) {
-    const uint32_t lane = threadIdx.x & 63u;
-    f32x16 accg[NRB], accu[NRB];
+    f32x16 acc[NRB];
 #pragma unroll
-    for (int r = 0; r < NRB; ++r) {
-        accg[r] = (f32x16){};
-        accu[r] = (f32x16){};
-    }
+    for (int r = 0; r < NRB; ++r) acc[r] = (f32x16){};
     // Blocks rotate through the three buffers: block kb in buffer kb % 3.
     for (uint32_t kb = 0; kb < t.nk; kb += 3u) {
-        gu_step<0, NRB>(sm, t, kb, accg, accu);
-        if (kb + 1u < t.nk) gu_step<1, NRB>(sm, t, kb + 1u, accg, accu);
-        if (kb + 2u < t.nk) gu_step<2, NRB>(sm, t, kb + 2u, accg, accu);
+        gu_step<0, NRB>(sm, t, kb, acc);
+        if (kb + 1u < t.nk) gu_step<1, NRB>(sm, t, kb + 1u, acc);
+        if (kb + 2u < t.nk) gu_step<2, NRB>(sm, t, kb + 2u, acc);
     }
     gg_sync<0>();  // every wave is done with the buffers
 
-    // Epilogue. (1) act = down_signs * silu(g) * u, rounded to binary16, into activation buffer
-    // 0 in the A-operand layout (row i, column c = 32 wave + m of the F block).
+    // Epilogue. (1) The up waves store u, fp32 [row][column of the F block], over activation
+    // buffers 0 and 1 (64 KB).
+    const bool up = t.wave >= 4u;
+    const uint32_t cq = t.wave & 3u, col = cq * 32u + t.m;
+    float *ubuf = reinterpret_cast<float *>(&sm.a[0][0]);
+    if (up) {
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ubuf[(rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4)) * 128u + col] = acc[rb][r];
+    }
+    __syncthreads();
+    // (2) The gate waves form act = down_signs * silu(g) * u, rounded to binary16, into
+    // activation buffer 2 in the A-operand layout (row i, column col of the F block).
     const bool has_signs = a.c[10] != 0xffffffffu;
-    const uint32_t col = t.wave * 32u + t.m;
-    const float sgn = has_signs ? gd_buf<const float>(a, a.c[10])[a.c[11] + fb * 128u + col] : 1.0f;
-    _Float16 *act = reinterpret_cast<_Float16 *>(&sm.a[0][0]);
+    _Float16 *act = reinterpret_cast<_Float16 *>(&sm.a[2][0]);
+    if (!up) {
+        const float sgn = has_signs ? gd_buf<const float>(a, a.c[10])[a.c[11] + fb * 128u + col] : 1.0f;
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
+        for (int rb = 0; rb < NRB; ++rb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-            act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
-                (_Float16)(gd_silu(accg[rb][r]) * accu[rb][r] * sgn);
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
+                act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
+                    (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[i * 128u + col] * sgn);
+            }
         }
     }
     __syncthreads();
     uint32_t *out = gd_buf<uint32_t>(a, a.c[12]) + a.c[13];
     if (has_signs) {
-        // (2) The 128-point Walsh-Hadamard transform of every row as a GEMM with H_128 (entries
-        // (-1)^popcount(k & j), exact in binary16): wave w computes output columns 32 w .. +31.
-        // The B operand of lane (j, h) at K-step s holds H[16 s + 8 h + e][j] for e = 0..7, which
-        // is the lane's fixed pattern (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j).
-        const uint32_t j = t.wave * 32u + t.m;
+        // (3) The 128-point Walsh-Hadamard transform of every row as a GEMM with H_128 (entries
+        // (-1)^popcount(k & j), exact in binary16): wave w computes output columns 32 (w % 4)
+        // .. + 31 of the row blocks rb with rb % 2 == w / 4. The B operand of lane (j, h) at
+        // K-step s holds H[16 s + 8 h + e][j] for e = 0..7, which is the lane's fixed pattern
+        // (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j).
+        const uint32_t j = col, half = t.wave >> 2;
         f16x8 hp, hn;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             hp[e] = (__builtin_popcount((uint32_t)e & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
             hn[e] = -hp[e];
         }
-        f32x16 rot[NRB];
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) rot[rb] = (f32x16){};
-#pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-            const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * t.h) & j) & 1) ? hn : hp;
-#pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
-                rot[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gg_a(sm, 0, rb * 32u + t.m, s8, t.h), hb, rot[rb], 0, 0, 0);
-        }
-        // (3) Scaled rows into activation buffer 1 (same layout), then 16-byte row copies out.
-        _Float16 *res = reinterpret_cast<_Float16 *>(&sm.a[1][0]);
+        _Float16 *res = reinterpret_cast<_Float16 *>(&sm.a[0][0]);
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
+            if ((uint32_t)(rb & 1) != half) continue;  // uniform per wave
+            f32x16 rot = (f32x16){};
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * t.h) & j) & 1) ? hn : hp;
+                rot = __builtin_amdgcn_mfma_f32_32x32x16_f16(gg_a(sm, 2, rb * 32u + t.m, s8, t.h), hb, rot, 0, 0, 0);
+            }
+            // (4) Scaled rows into activation buffer 0 (same layout).
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[rb][r] * GD_INV_SQRT128);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
             }
         }
         __syncthreads();
     }
     // Rows of 128 binary16 values (16 chunks of 16 bytes, swizzled) to act16[row0 + i][fb * 128 ..].
-    const gd_u32x4 *rows_src = has_signs ? &sm.a[1][0] : &sm.a[0][0];
-    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 256u) {
+    const gd_u32x4 *rows_src = has_signs ? &sm.a[0][0] : &sm.a[2][0];
+    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
         const uint32_t i = idx >> 4, c = idx & 15u;
         *reinterpret_cast<gd_u32x4 *>(out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u) =
             rows_src[i * 16u + (c ^ (i & 15u))];
     }
 }
 
-GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 1) {
+GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 2) {
     __shared__ GgLds sm;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const uint32_t *meta = gd_buf<const uint32_t>(a, a.c[0]);
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = blockIdx.y;
     if (tile >= __builtin_amdgcn_readfirstlane(meta[1023])) return;
     const uint4 td = reinterpret_cast<const uint4 *>(meta + 1024u)[tile];
     // Uniform per group: scalar branches over the row blocks.
     const uint32_t e = __builtin_amdgcn_readfirstlane(td.x), row0 = __builtin_amdgcn_readfirstlane(td.y),
                    rows = __builtin_amdgcn_readfirstlane(td.z);
-    const uint32_t E = a.c[14], F = a.c[15], U = a.c[16], fb = blockIdx.y;
+    const uint32_t E = a.c[14], F = a.c[15], U = a.c[16], fb = blockIdx.x;
 
     const uint4 *cb = gd_buf<const uint4>(a, a.c[9]);
     reinterpret_cast<uint4 *>(sm.book)[tid] = cb[tid];
-    reinterpret_cast<uint4 *>(sm.book)[tid + 256u] = cb[tid + 256u];
     if (tid < GG_TM) sm.src[tid] = gd_buf<const uint32_t>(a, a.c[1])[a.c[2] + row0 + min(tid, rows - 1u)] / U;
     __syncthreads();
 
@@ -205,28 +202,29 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 256, 1) {
     t.h = lane >> 5;
     t.sel = gg_sel(t.h);
     t.nk = E / 128u;
+    t.wq = (wave >> 2) * 128u + (wave & 3u) * 32u + t.m;
     t.xbase = gd_buf<const uint32_t>(a, a.c[3]) + a.c[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
         uint32_t r;
-        const uint32_t c = gg_chunk(wave, lane, i, r);
+        const uint32_t c = gg_chunk8(wave, lane, i, r);
         t.roff[i] = sm.src[r] * (E * 2u) + c;
     }
-    // Weight rows q < 128: gate row fb * 128 + q; q >= 128: up row fb * 128 + q - 128.
+    // Staged weight row q < 128: gate row fb * 128 + q; q >= 128: up row fb * 128 + q - 128.
+    // Load L carries pieces 64 L + lane: row g / 3, 16-byte piece g % 3.
     const uint64_t base = ((uint64_t)a.c[6] << 32) | a.c[5];
     t.wbase = reinterpret_cast<const void *>(base);
     const uint32_t row_bytes = (E / 128u) * 34u, proj_bytes = a.c[8];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        uint32_t q, piece;
-        gg_w_piece<3>(wave, lane, i, q, piece);
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t g = gg_w8_load(wave, i) * 64u + lane, q = g / 3u, piece = g - q * 3u;
         t.woff[i] = e * a.c[7] + (q >> 7) * proj_bytes + (fb * 128u + (q & 127u)) * row_bytes + piece * 16u;
     }
-    gg_stage_a(sm, 0, wave, t.xbase, t.roff, 0);
-    gg_stage_w<3>(sm, 0, wave, t.wbase, t.woff, 0);
+    gg_stage_a8(sm, 0, wave, t.xbase, t.roff, 0);
+    gg_stage_w8(sm, 0, wave, t.wbase, t.woff, 0);
     if (t.nk > 1u) {
-        gg_stage_a(sm, 1, wave, t.xbase, t.roff, 1);
-        gg_stage_w<3>(sm, 1, wave, t.wbase, t.woff, 1);
+        gg_stage_a8(sm, 1, wave, t.xbase, t.roff, 1);
+        gg_stage_w8(sm, 1, wave, t.wbase, t.woff, 1);
     }
     switch ((rows + 31u) >> 5) {
         case 1: gu_tile<1>(sm, t, a, row0, rows, fb, F); break;

@@ -9,8 +9,10 @@
 // then over experts; pass 2 walks each run again in slot order and places every slot at its
 // cursor plus its rank among the lanes of the same round that chose the same expert (found
 // with ten ballots over the expert id bits); the highest such lane advances the cursor.
-// Tiles: each expert's segment is cut into tiles of at most tile_rows sorted rows, listed
-// expert by expert.
+// Tiles: each expert's segment is cut into tiles of at most tile_rows sorted rows. The list
+// holds the full tiles first (expert by expert), then the partial tiles by decreasing row count
+// (ties by expert), so that the grouped GEMMs, whose groups start in list order, begin with the
+// longest tiles and end with the shortest.
 // Output meta (u32 words): [0, n_expert] order_start, [1023] tile count,
 // [1024 + 4 i ..] tile i = {expert, first sorted row, rows, 0}.
 // Grid: 1; 1024 threads. Requires n_expert <= 512.
@@ -23,7 +25,8 @@
 
 GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
     __shared__ uint32_t cur[SORT_WAVES][SORT_MAX_E];
-    __shared__ uint32_t start[SORT_MAX_E + 1], tstart[SORT_MAX_E + 1];
+    __shared__ uint32_t start[SORT_MAX_E + 1], tstart[SORT_MAX_E + 1], fstart[SORT_MAX_E + 1];
+    __shared__ uint32_t psz[SORT_MAX_E];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n_slots = a.c[2], NE = a.c[3], TM = a.c[7];
     const uint32_t *ids = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1];
@@ -48,33 +51,38 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
     }
     // Exclusive prefix over experts of the counts and of the tile counts (wave 0..7 hold
     // experts 0..511; each wave scans its 64, then the 8 wave totals are added).
-    __shared__ uint32_t wsum[8][2];
-    uint32_t cnt = tid < NE ? total : 0u, tiles = (cnt + TM - 1u) / TM;
-    uint32_t ic = cnt, it = tiles;
+    __shared__ uint32_t wsum[8][3];
+    uint32_t cnt = tid < NE ? total : 0u, tiles = (cnt + TM - 1u) / TM, full = cnt / TM;
+    uint32_t ic = cnt, it = tiles, iff = full;
+    if (tid < NE) psz[tid] = cnt - full * TM;
     if (wave < 8u) {
 #pragma unroll
         for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t pc = __shfl_up(ic, o, 64), pt = __shfl_up(it, o, 64);
+            const uint32_t pc = __shfl_up(ic, o, 64), pt = __shfl_up(it, o, 64), pf = __shfl_up(iff, o, 64);
             if (lane >= o) {
                 ic += pc;
                 it += pt;
+                iff += pf;
             }
         }
         if (lane == 63u) {
             wsum[wave][0] = ic;
             wsum[wave][1] = it;
+            wsum[wave][2] = iff;
         }
     }
     __syncthreads();
     if (wave < 8u) {
-        uint32_t bc = 0, bt = 0;
+        uint32_t bc = 0, bt = 0, bf = 0;
         for (uint32_t w = 0; w < wave; ++w) {
             bc += wsum[w][0];
             bt += wsum[w][1];
+            bf += wsum[w][2];
         }
         if (tid <= NE) {  // tid == NE (< 512) receives the grand totals
             start[tid] = bc + ic - cnt;
             tstart[tid] = bt + it - tiles;
+            fstart[tid] = bf + iff - full;
         }
     }
     __syncthreads();
@@ -102,16 +110,19 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
             if (lane == 63u - (uint32_t)__builtin_clzll(peers)) cur[wave][e] += (uint32_t)__builtin_popcountll(peers);
         }
     }
-    // Tile list.
+    // Tile list: full tiles at the exclusive prefix of the full-tile counts, then the partial
+    // tile of each expert at the full-tile total plus its rank by decreasing size.
     if (tid < NE) {
-        const uint32_t c = start[tid + 1] - start[tid];
-        for (uint32_t j = 0; j * TM < c; ++j) {
-            uint4 d;
-            d.x = tid;
-            d.y = start[tid] + j * TM;
-            d.z = min(TM, c - j * TM);
-            d.w = 0u;
-            reinterpret_cast<uint4 *>(meta + 1024u)[tstart[tid] + j] = d;
+        uint4 *list = reinterpret_cast<uint4 *>(meta + 1024u);
+        const uint32_t c = start[tid + 1] - start[tid], nf = c / TM, p = c - nf * TM;
+        for (uint32_t j = 0; j < nf; ++j) list[fstart[tid] + j] = make_uint4(tid, start[tid] + j * TM, TM, 0u);
+        if (p) {
+            uint32_t rank = 0;
+            for (uint32_t e2 = 0; e2 < NE; ++e2) {
+                const uint32_t q = psz[e2];
+                rank += (q > p || (q == p && e2 < tid)) ? 1u : 0u;
+            }
+            list[fstart[NE] + rank] = make_uint4(tid, start[tid] + nf * TM, p, 0u);
         }
     }
 }

@@ -546,11 +546,11 @@ class Engine {
         dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
                              {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
                               codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, act.uav, 0, E, F, U},
-                             tiles, F / 128);
+                             F / 128, tiles);
         dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down",
                              {meta.uav, order.uav, 0, act.uav, 0, base_lo, base_hi, slot_stride, 2 * L.gate_bytes,
                               codebook.srv, down.uav, 0, E, F},
-                             tiles, E / 128);
+                             E / 256, tiles);
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
                              {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u, res_uav,
                               res_off},
