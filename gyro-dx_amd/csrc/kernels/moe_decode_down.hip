@@ -20,6 +20,7 @@
 // no residual.
 // Requires TQ2_T experts, n_used == 8, F == 512 and at most 2 K-parts.
 #include "gyro_fast.h"
+#include "fwht.h"
 
 #define DN_ROWS 8
 #define DN_U 8
@@ -28,10 +29,6 @@
 #define DN_ROW_BYTES (DN_NB * 34)
 #define DN_BLOCK_STRIDE 132  // floats per 128-block in LDS (bank spread for the 8 x streams)
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return gd_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)gd_f32_bits(v), CTRL, 0xf, 0xf, true));
-}
 
 GD_PIPELINE_NAMED(moe_decode_down, 256) {
     __shared__ uint4 book4[512];
@@ -130,18 +127,18 @@ GD_PIPELINE_NAMED(moe_decode_down, 256) {
         // Widths 16, 32, 64: partners are lanes l8 ^ 1, ^ 2, ^ 4 of the 8-lane group.
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float p1 = dpp_f<0xB1>(v[j]);  // quad_perm [1,0,3,2]
+            const float p1 = gd_dpp_f<0xB1>(v[j]);  // quad_perm [1,0,3,2]
             v[j] = (l8 & 1u) ? p1 - v[j] : v[j] + p1;
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float p2 = dpp_f<0x4E>(v[j]);  // quad_perm [2,3,0,1]
+            const float p2 = gd_dpp_f<0x4E>(v[j]);  // quad_perm [2,3,0,1]
             v[j] = (l8 & 2u) ? p2 - v[j] : v[j] + p2;
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float up4 = dpp_f<0x104>(v[j]);  // row_shl:4, lane + 4
-            const float dn4 = dpp_f<0x114>(v[j]);  // row_shr:4, lane - 4
+            const float up4 = gd_dpp_f<0x104>(v[j]);  // row_shl:4, lane + 4
+            const float dn4 = gd_dpp_f<0x114>(v[j]);  // row_shr:4, lane - 4
             v[j] = (l8 & 4u) ? dn4 - v[j] : v[j] + up4;
         }
 #pragma unroll
@@ -164,8 +161,8 @@ GD_PIPELINE_NAMED(moe_decode_down, 256) {
         tq2_unpack(d, (off & 2u) != 0u, sc, q);
         float s = sc * tq2_block_dot(q, reinterpret_cast<const uint32_t *>(book4),
                                      act + (k * DN_NB + bb) * DN_BLOCK_STRIDE);
-        s = s + dpp_f<0xB1>(s);  // b0 + b1, b2 + b3
-        s = s + dpp_f<0x4E>(s);  // (b0 + b1) + (b2 + b3)
+        s = s + gd_dpp_f<0xB1>(s);  // b0 + b1, b2 + b3
+        s = s + gd_dpp_f<0x4E>(s);  // (b0 + b1) + (b2 + b3)
         if (bb == 0) dk[k][r] = s;
     }
     __syncthreads();

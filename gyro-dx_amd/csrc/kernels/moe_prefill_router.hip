@@ -4,70 +4,145 @@
 //   xh16[t]      = H_128 (gate_signs * x[t]) per 128-block, as binary16 pairs
 //                                                      src/engine.zig:547-551
 // Group (bx, by) computes the 32 x 32 logit tile of tokens 32 bx.. and experts 32 by.. with
-// v_mfma_f32_32x32x2_f32; its eight waves split K = E into eighths and their partial tiles
-// are added in wave order through LDS. Each lane half feeds four consecutive k per 16-byte
-// load (lane half h takes k + 4h .. k + 4h + 3 of every 8), the same k for A and B, so every
-// product x[t][k] W[r][k] enters the sum once. The rotation of all n * E/128 blocks is spread
-// over every wave of the grid, one block per wave at a time.
-// Grid: (ceil(n / 32), ceil(n_expert / 32)); 512 threads. Requires E % 128 == 0.
+// v_mfma_f32_32x32x2_f32; its four waves split K = E into quarters and their partial tiles are
+// added in wave order through LDS. The MFMA operands take one row per lane, so each wave stages
+// its own 32-wide K chunks of the 32 token rows and the 32 router rows into LDS first: direct
+// global-to-LDS loads (8 lanes per 128-byte row, whole rows per load), the 16-byte chunk q of
+// row r stored at position q ^ (r % 8), two chunks ahead in three buffers per wave; only the
+// wave's own load count is waited for, so the K loop has no barrier. Lane half h takes k + 4h
+// .. k + 4h + 3 of every 8 for both operands, so every product x[t][k] W[r][k] enters the sum
+// once. The rotation of all n * E/128 blocks is spread over every wave of the grid, eight
+// blocks per wave at a time.
+// Grid: (ceil(n / 32), ceil(n_expert / 32)); 256 threads. Requires E % 128 == 0.
 // Constants: 0 x_uav 1 x_off (words; rows of E floats) 2 n_tok 3 E 4 router_srv 5 router_off
 // 6 n_expert 7 bias_srv (0xffffffff: none) 8 bias_off 9 logits_uav 10 logits_off
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
 // 14 xh16_off (words).
+#include "ggemm.h"
 #include "fwht.h"
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+#define RT_WAVES 4
+#define RT_KC 32    // K per staged chunk
+#define RT_NBUF 3
 
-GD_PIPELINE_NAMED(moe_prefill_router, 512) {
-    __shared__ float red[8][32 * 32];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+struct __attribute__((aligned(16))) RtLds {
+    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 128 bytes
+    gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_KC / 4];
+};
+
+// Stages chunk c (K = kq + 32 c ..) of this wave's 32 token rows and 32 router rows: 4 + 4
+// loads, lane l of load i carrying row 8 i + l / 8, position l % 8.
+__device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf, const void *xbase,
+                                         const void *wbase, const uint32_t xoff[4], const uint32_t woff[4],
+                                         uint32_t kbytes) {
+    const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xbase, xoff[i] + kbytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
+}
+
+GD_PIPELINE_NAMED(moe_prefill_router, 256) {
+    __shared__ RtLds sm;
+    __shared__ float red[RT_WAVES][32 * 32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = a.c[2], E = a.c[3], NE = a.c[6];
     const float *X = gd_buf<const float>(a, a.c[0]) + a.c[1];
+    const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
 
-    // Rotation share of this group.
+    // Router tile: start the staging of this wave's first chunks before the rotation share.
+    const uint32_t t0 = blockIdx.x * 32u, r0 = blockIdx.y * 32u;
+    const uint32_t kq = wave * (E / 4u), nc = E / 4u / RT_KC;
+    uint32_t xoff[4], woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = (lane & 7u) ^ (r & 7u);
+        xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
+        woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
+    }
+    rt_stage(sm, wave, 0, X, W, xoff, woff, 0);
+    if (nc > 1u) rt_stage(sm, wave, 1, X, W, xoff, woff, RT_KC * 4u);
+
+    // Rotation share of this group: each wave transforms eight 128-blocks at a time, an 8-lane
+    // group per block holding 16 consecutive values per lane (gd_fwht128_x16); the blocks
+    // b = 8 (first + waves j) + lane / 8.
     {
         const uint32_t nblk = E / 128u, total = n * nblk;
-        const uint32_t waves = gridDim.x * gridDim.y * 8u;
-        const uint32_t first = (blockIdx.y * gridDim.x + blockIdx.x) * 8u + wave;
+        const uint32_t waves = gridDim.x * gridDim.y * RT_WAVES;
+        const uint32_t first = (blockIdx.y * gridDim.x + blockIdx.x) * RT_WAVES + wave;
         const bool has_signs = a.c[11] != 0xffffffffu;
         const float *S = has_signs ? gd_buf<const float>(a, a.c[11]) + a.c[12] : nullptr;
         uint32_t *XH = gd_buf<uint32_t>(a, a.c[13]) + a.c[14];
-        for (uint32_t b = first; b < total; b += waves) {
-            const uint32_t t = b / nblk, blk = b - t * nblk, i = blk * 128u + 2u * lane;
-            const float2 xv = *reinterpret_cast<const float2 *>(X + (size_t)t * E + i);
-            float x0 = xv.x, x1 = xv.y;
-            if (has_signs) {
-                const float2 sv = *reinterpret_cast<const float2 *>(S + i);
-                x0 *= sv.x;
-                x1 *= sv.y;
-                gd_fwht128_wave(x0, x1);
-                x0 *= GD_INV_SQRT128;
-                x1 *= GD_INV_SQRT128;
+        const uint32_t l8 = lane & 7u;
+        for (uint32_t g = first; g * 8u < total; g += waves) {
+            const uint32_t b = g * 8u + (lane >> 3);
+            if (b < total) {
+                const uint32_t t = b / nblk, blk = b - t * nblk, i = blk * 128u + 16u * l8;
+                float v[16];
+                const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)t * E + i);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 f = src[q];
+                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+                }
+                if (has_signs) {
+                    const float4 *sg = reinterpret_cast<const float4 *>(S + i);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 f = sg[q];
+                        v[4 * q] *= f.x; v[4 * q + 1] *= f.y; v[4 * q + 2] *= f.z; v[4 * q + 3] *= f.w;
+                    }
+                }
+                // The DPP stages read lanes of the same 8-lane group only, and whole groups share
+                // b < total, so every source lane is active.
+                if (has_signs) {
+                    gd_fwht128_x16(v, l8);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[j] *= GD_INV_SQRT128;
+                }
+                gd_u32x4 o[2];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
+                    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+                    o[j >> 2][j & 3] = h0 | (h1 << 16);
+                }
+                gd_u32x4 *dst = reinterpret_cast<gd_u32x4 *>(XH + (size_t)t * (E / 2u) + blk * 64u + 8u * l8);
+                dst[0] = o[0];
+                dst[1] = o[1];
             }
-            const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)x0);
-            const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)x1);
-            XH[(size_t)t * (E / 2u) + blk * 64u + lane] = h0 | (h1 << 16);
         }
     }
 
-    // Router tile.
-    const uint32_t t0 = blockIdx.x * 32u, r0 = blockIdx.y * 32u;
+    // K loop over this wave's quarter. Rows beyond n or n_expert were staged as copies of the last
+    // row; their operands are zeroed here.
     const uint32_t m = lane & 31u, h = lane >> 5;
     const bool tv = t0 + m < n, rv = r0 + m < NE;
-    const float *xa = X + (size_t)(tv ? t0 + m : 0u) * E + 4u * h;
-    const float *wb = gd_buf<const float>(a, a.c[4]) + a.c[5] + (size_t)(rv ? r0 + m : 0u) * E + 4u * h;
-    const uint32_t kpw = E / 8u, k0 = wave * kpw;
     f32x16 acc = {};
-#pragma unroll 4
-    for (uint32_t k = k0; k < k0 + kpw; k += 8u) {
-        float4 av = *reinterpret_cast<const float4 *>(xa + k);
-        float4 bv = *reinterpret_cast<const float4 *>(wb + k);
-        if (!tv) av = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!rv) bv = make_float4(0.f, 0.f, 0.f, 0.f);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+    for (uint32_t c = 0; c < nc; ++c) {
+        if (c + 1u < nc) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c + 1 may be in flight
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t buf = c % RT_NBUF;
+        float4 xv[4], wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
+            xv[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
+            wv[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float4 av = xv[j], bv = wv[j];
+            if (!tv) av = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (!rv) bv = make_float4(0.f, 0.f, 0.f, 0.f);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+        }
+        // Chunk c + 2 into the buffer of chunk c - 1, whose reads completed before its MFMAs.
+        if (c + 2u < nc) rt_stage(sm, wave, (c + 2u) % RT_NBUF, X, W, xoff, woff, (c + 2u) * RT_KC * 4u);
     }
     // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m.
 #pragma unroll
@@ -76,13 +151,13 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
     const bool has_bias = a.c[7] != 0xffffffffu;
     float *L = gd_buf<float>(a, a.c[9]) + a.c[10];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const uint32_t idx = tid + 512u * q, i = idx >> 5, j = idx & 31u;
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t idx = tid + 256u * q, i = idx >> 5, j = idx & 31u;
         const uint32_t t = t0 + i, r = r0 + j;
         if (t < n && r < NE) {
             float v = red[0][idx];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) v += red[w][idx];
+            for (int w = 1; w < RT_WAVES; ++w) v += red[w][idx];
             if (has_bias) v += gd_buf<const float>(a, a.c[7])[a.c[8] + r];
             L[(size_t)t * NE + r] = v;
         }

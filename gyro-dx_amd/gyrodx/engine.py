@@ -47,6 +47,7 @@ def lib() -> C.CDLL:
         L.gm_run_bracketed.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, u32, C.POINTER(C.c_double),
                                        C.POINTER(C.c_double), C.POINTER(C.c_double)]
         L.gm_read_outputs.argtypes = [vp, f32p, u32]
+        L.gm_last_tiles.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(u32)]
         L.gm_forward_stack.argtypes = [vp, C.POINTER(u32), u32, u32, f32p, u32, f32p]
         L.gm_run_stack.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
                                    C.POINTER(C.c_double)]
@@ -154,6 +155,14 @@ class Engine:
         self._check(lib().gm_run_bracketed(self._h, path, batch, calls, first, arr, len(layers), bracket,
                                            C.byref(dev), C.byref(wall), C.byref(br)), "gm_run")
         return dev.value, wall.value, br.value
+
+    def last_tiles(self, max_tiles: int = 4096) -> np.ndarray:
+        """Tile list of the last prefill call: [count, 4] u32 {expert, first row, rows, 0}."""
+        buf = np.zeros((max_tiles, 4), np.uint32)
+        cnt = C.c_uint32()
+        self._check(lib().gm_last_tiles(self._h, max_tiles, buf.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(cnt)),
+                    "gm_last_tiles")
+        return buf[:cnt.value].copy()
 
     def forward_stack(self, layers, x: np.ndarray, path: int = PATH_DECODE) -> np.ndarray:
         """x <- x + MoE_l(RMSNorm_l(x)) over the given layer indices."""

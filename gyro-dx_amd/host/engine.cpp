@@ -533,6 +533,7 @@ class Engine {
         if (!prefill_supported(L))
             throw NativeError(-1, "prefill path needs TQ2_T, no shared expert, E and F multiples of 256, top-8 of "
                                   "<= 256 experts and binary16-finite scale x codebook products");
+        if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (4096 tokens of top-8)");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
@@ -711,6 +712,18 @@ extern "C" int gm_last_sort(gm_engine *g, uint32_t n, uint32_t *order, uint32_t 
         gyro::check(gd_readback(e.dev.ctx, e.order.handle, 0, n * e.U * 4, order, gyro::kTimeoutMs), "gd_readback");
         gyro::check(gd_readback(e.dev.ctx, e.meta.handle, 0, (e.NE + 1) * 4, order_start, gyro::kTimeoutMs),
                     "gd_readback");
+    });
+}
+
+extern "C" int gm_last_tiles(gm_engine *g, uint32_t max_tiles, uint32_t *tiles, uint32_t *count) {
+    if (!tiles || !count) return -1;
+    return guarded(g, [&] {
+        Engine &e = g->e;
+        uint32_t n = 0;
+        gyro::check(gd_readback(e.dev.ctx, e.meta.handle, 1023 * 4, 4, &n, gyro::kTimeoutMs), "gd_readback");
+        if (n > max_tiles) throw gyro::NativeError(-1, "tile list longer than max_tiles");
+        if (n) gyro::check(gd_readback(e.dev.ctx, e.meta.handle, 1024 * 4, n * 16, tiles, gyro::kTimeoutMs), "gd_readback");
+        *count = n;
     });
 }
 

@@ -80,6 +80,9 @@ GM_API int gm_last_routes(gm_engine *e, uint32_t n, uint32_t *ids, float *weight
  * 553-564): order[n * n_used] lists the slots t * n_used + k grouped by expert, stable in slot
  * order; order_start[n_expert + 1] is the exclusive prefix of the expert counts. */
 GM_API int gm_last_sort(gm_engine *e, uint32_t n, uint32_t *order, uint32_t *order_start);
+/* Reads the tile list of the last prefill-path call: count (out) tiles of 4 words each
+ * {expert, first sorted row, rows, 0}, at most max_tiles of them. */
+GM_API int gm_last_tiles(gm_engine *e, uint32_t max_tiles, uint32_t *tiles, uint32_t *count);
 /* Decodes rows [row0, row0 + rows) of one expert projection to fp32 with the fast path's
  * device decoder (bit-exact check of the in-kernel dequantisation). */
 GM_API int gm_dequant(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,

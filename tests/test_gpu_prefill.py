@@ -28,6 +28,22 @@ def separable(oracle_layer, x, U, margin=1e-5):
     return (s[:, U - 1] - s[:, U]) > margin * s[:, U - 1]
 
 
+def check_tiles(tiles, order_start, tm=128):
+    """The tile list covers every expert segment exactly once in tiles of <= tm rows: full tiles
+    first in expert order, then the partial tiles by decreasing size, ties by expert."""
+    start = np.asarray(order_start, np.int64)
+    expect_full, expect_part = [], []
+    for e in range(len(start) - 1):
+        c = int(start[e + 1] - start[e])
+        for j in range(c // tm):
+            expect_full.append((e, int(start[e]) + j * tm, tm))
+        if c % tm:
+            expect_part.append((e, int(start[e]) + (c // tm) * tm, c % tm))
+    expect_part.sort(key=lambda t: (-t[2], t[0]))
+    got = [tuple(int(v) for v in t[:3]) for t in tiles]
+    assert got == expect_full + expect_part
+
+
 def run_case(oracle_mod, layer, x, max_tok, what):
     eng = Engine(max_tok=max_tok)
     try:
@@ -46,6 +62,7 @@ def run_case(oracle_mod, layer, x, max_tok, what):
             order, start = eng.last_sort(n)
             np.testing.assert_array_equal(start, tr["order_start"])
             np.testing.assert_array_equal(order, tr["route_order"])
+        check_tiles(eng.last_tiles(), tr["order_start"] if sep.all() else eng.last_sort(n)[1])
         r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
         print(f"{what}: rel_rms={r:.3e} cosine={c:.8f}", flush=True)
         assert r <= REL_RMS and c >= COSINE, (what, r, c)
