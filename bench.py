@@ -22,6 +22,11 @@ Reported beside the throughput:
                 a 4096-token prefill, each with tok/s and the fraction of its binding roofline
                 (HBM: measured distinct experts' packed bytes plus the router matrices per step;
                 MFMA: routed-expert FLOPs), and the CPU oracle on a sample of 8 tokens.
+  --mixed       (its own JSON line) the mixed-quant layer: routed experts' projections assigned
+                by seed across the eight Gyro types, plus the always-on bf16 shared SwiGLU expert of
+                width 1024; batch-1 decode and a 512-token prefill, with
+                packed-byte and FLOP rooflines, and the CPU oracle on a sample. Decode runs the
+                decode path's type-generic kernels, prefill the generic path.
   prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (four cycled
                 copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
                 and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
@@ -283,6 +288,68 @@ def stack_bench(args):
     }
 
 
+SHARED_F = 1024
+SHARED_BYTES = 3 * SHARED_F * E * 2  # bf16 gate, up, down of the shared expert
+
+
+def mixed_bench(args):
+    """The mixed-quant layer with the shared expert (see the module doc)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from gyrodx import synth
+    from gyrodx.engine import PATH_DECODE, PATH_GENERIC, Engine
+
+    layer = synth.make_layer(args.seed + 50, mixed_types=True, SF=SHARED_F)
+    copies = args.copies
+    eng = Engine(max_tok=512)
+    ids = [eng.add_layer(layer) for _ in range(copies)]
+    res = {"workload": f"mixed-quant MoE layer: hidden {E}, {N_EXPERT} experts of mixed Gyro types (all 8), "
+                       f"top-{TOP_K}, F {F}, bf16 shared expert of width {SHARED_F}",
+           "types_present": sorted(int(t) for t in np.unique(layer.types)), "layer_copies": copies}
+    # Packed bytes of the experts the decode tokens select (measured per token), shared expert and router.
+    steps = args.mixed_steps
+    x = synth.make_tokens(args.seed + 51, steps + 16)
+    eng.set_tokens(x)
+    eng.run(PATH_DECODE, 1, 16, ids, first=0)
+    dev_ms, wall_ms, _ = eng.run(PATH_DECODE, 1, steps, ids, first=16)
+    gpu = eng.read_outputs(steps + 16)[16:]
+    expert_bytes = []
+    for t in range(min(steps, 32)):
+        eng.forward(ids[0], x[16 + t:17 + t], PATH_DECODE)
+        r, _ = eng.last_routes(1)
+        expert_bytes.append(sum(layer.expert_bytes(int(e)) for e in r[0]))
+    step_s = wall_ms / steps * 1e-3
+    per_tok = float(np.mean(expert_bytes)) + SHARED_BYTES + ROUTER_BYTES
+    res["decode"] = {"path": "decode (moe_router, moe_decode_gu_x, shared expert, moe_decode_down_x)",
+                     "tok_s": round(1.0 / step_s, 1), "us_per_token": round(step_s * 1e6, 2),
+                     "bytes_per_token": int(per_tok), "hbm_gbs": round(per_tok / step_s / 1e9, 1),
+                     "roofline": {"bound": "hbm", "frac": round(per_tok / step_s / 1e9 / HBM_PEAK_GBS, 4)}}
+    # 512-token prefill.
+    xp = synth.make_tokens(args.seed + 52, 512 * 4, bf16=True)
+    eng.set_tokens(xp)
+    eng.run(PATH_GENERIC, 512, 1, ids, first=0)
+    dev_ms, wall_ms, _ = eng.run(PATH_GENERIC, 512, 4, ids, first=0)
+    pout = eng.read_outputs(512)
+    call_s = wall_ms / 4 * 1e-3
+    flops = 512 * (LAYER_FLOPS_PER_TOKEN + 3 * 2 * E * SHARED_F)
+    res["prefill"] = {"path": "generic", "tokens": 512, "tok_s": round(512 / call_s, 1), "us_per_call": round(call_s * 1e6, 2),
+                      "flops_per_call": flops, "tflops": round(flops / call_s / 1e12, 2),
+                      "roofline": {"bound": "mfma", "frac": round(flops / call_s / 1e12 / MFMA_PEAK_TFLOPS, 4)}}
+    eng.close()
+    if not args.no_cpu:
+        threads = cpu_threads()
+        ol = oracle.OracleLayer(layer)
+        t0 = time.perf_counter()
+        ref = ol.forward(x[16:16 + 16], threads=threads)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(16 / dt, 1), "unit": "tok/s", "cores": threads, "kind": "port",
+                               "sample": f"16 batch-1 decode tokens, {dt:.2f} s on {threads} threads"}
+        refp = ol.forward(xp[:64], threads=threads)
+        res["parity"] = {"decode_rel_rms": oracle.rel_rms(ref, gpu[:16]), "decode_cosine": oracle.cosine(ref, gpu[:16]),
+                         "prefill_rel_rms_first64": oracle.rel_rms(refp, pout[:64])}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,6 +365,9 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true",
                     help="the 48-layer stack batch sweep and 4096-token prefill, printed as its own JSON line")
     ap.add_argument("--stack-layers", type=int, default=48)
+    ap.add_argument("--mixed", action="store_true",
+                    help="the mixed-quant layer with the shared expert, printed as its own JSON line")
+    ap.add_argument("--mixed-steps", type=int, default=500)
     ap.add_argument("--stack-batches", default="1,8,32,64,4096", help="sweep points of --stack (of 1,8,32,64,4096)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
@@ -313,6 +383,9 @@ def main() -> int:
 
     if args.stack:
         print(json.dumps({"stack": stack_bench(args)}), flush=True)
+        return 0
+    if args.mixed:
+        print(json.dumps({"mixed": mixed_bench(args)}), flush=True)
         return 0
     layer = synth.make_layer(args.seed)
     if args.prefill_only:

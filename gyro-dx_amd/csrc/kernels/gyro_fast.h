@@ -124,3 +124,125 @@ __device__ __forceinline__ void tq2_unpack(const uint32_t *d, bool odd_half, flo
         for (int j = 0; j < 8; ++j) q[j] = d[j + 1];
     }
 }
+
+// ---- Every Gyro type (src/gyro.zig:32-41) from packed words -------------------------------
+// GyroT<ID>: K new bits per step, S steps, BB block bytes (2 scale bytes + S K / 8 stream
+// bytes), NW stream words.
+template <int ID> struct GyroT;
+template <> struct GyroT<144> { static constexpr int K = 8, S = 32, BB = 34; };
+template <> struct GyroT<145> { static constexpr int K = 6, S = 32, BB = 26; };
+template <> struct GyroT<146> { static constexpr int K = 7, S = 32, BB = 30; };
+template <> struct GyroT<147> { static constexpr int K = 5, S = 64, BB = 42; };
+template <> struct GyroT<148> { static constexpr int K = 6, S = 64, BB = 50; };
+template <> struct GyroT<149> { static constexpr int K = 7, S = 64, BB = 58; };
+template <> struct GyroT<150> { static constexpr int K = 5, S = 32, BB = 22; };
+template <> struct GyroT<151> { static constexpr int K = 4, S = 32, BB = 18; };
+template <int ID> constexpr int gyro_nw() { return (GyroT<ID>::BB - 2) / 4; }
+
+// Scale and stream words of a block that starts at an even byte offset inside the words d[]
+// (d[0] holds the block's first bytes when odd_half is false, else they start at byte 2 of
+// d[0]); d holds NW + 1 words.
+template <int ID>
+__device__ __forceinline__ void gyro_unpack(const uint32_t *d, bool odd_half, float &scale,
+                                            uint32_t (&w)[gyro_nw<ID>()]) {
+    if (!odd_half) {
+        scale = gd_half(d[0] & 0xffffu);
+#pragma unroll
+        for (int j = 0; j < gyro_nw<ID>(); ++j) w[j] = __builtin_amdgcn_alignbyte(d[j + 1], d[j], 2);
+    } else {
+        scale = gd_half(d[0] >> 16);
+#pragma unroll
+        for (int j = 0; j < gyro_nw<ID>(); ++j) w[j] = d[j + 1];
+    }
+}
+
+// 15-bit state of step t (a constant after unrolling) of a k-bit type (src/gyro.zig:107-117):
+// the 16-bit window at stream bit (S - 1 - t) K of the circular little-endian stream, masked to
+// 15 bits as the hash reads it.
+template <int ID>
+__device__ __forceinline__ uint32_t gyro_kstate(const uint32_t (&w)[gyro_nw<ID>()], int t) {
+    constexpr int NW = gyro_nw<ID>();
+    const int off = (GyroT<ID>::S - 1 - t) * GyroT<ID>::K;
+    const int i = off >> 5, i1 = (i + 1) % NW;
+    return __builtin_amdgcn_alignbit(w[i1], w[i], (uint32_t)(off & 31)) & 0x7fffu;
+}
+
+// Unscaled dot of one block with its activations held as binary16 pairs in xs (pair j =
+// elements 2j, 2j+1): 32-step types give two codebook pairs per step (weights 4t .. 4t+3),
+// 64-step types one (weights 2t, 2t+1).
+template <int ID>
+__device__ __forceinline__ float gyro_block_dot_h(const uint32_t (&w)[gyro_nw<ID>()], const uint32_t *book,
+                                                  const uint32_t xs[64]) {
+    if constexpr (ID == 144) {
+        return tq2_block_dot_h(w, book, xs);
+    } else {
+        float acc0 = 0.f, acc1 = 0.f;
+        if constexpr (GyroT<ID>::S == 32) {
+#pragma unroll
+            for (int t = 0; t < 32; ++t) {
+                uint32_t a0, a1;
+                cb_addr(gyro_kstate<ID>(w, t), a0, a1);
+                acc0 = __builtin_amdgcn_fdot2(as_half2(lds_word(book, a0)), as_half2(xs[2 * t]), acc0, false);
+                acc1 = __builtin_amdgcn_fdot2(as_half2(lds_word(book, a1)), as_half2(xs[2 * t + 1]), acc1, false);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 64; t += 2) {
+                const uint32_t b0 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t)));
+                const uint32_t b1 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t + 1)));
+                acc0 = __builtin_amdgcn_fdot2(as_half2(b0), as_half2(xs[t]), acc0, false);
+                acc1 = __builtin_amdgcn_fdot2(as_half2(b1), as_half2(xs[t + 1]), acc1, false);
+            }
+        }
+        return acc0 + acc1;
+    }
+}
+
+// As gyro_block_dot_h with fp32 activations x[128] (an LDS or uniform pointer).
+template <int ID, typename XP>
+__device__ __forceinline__ float gyro_block_dot(const uint32_t (&w)[gyro_nw<ID>()], const uint32_t *book, XP x) {
+    if constexpr (ID == 144) {
+        return tq2_block_dot(w, book, x);
+    } else {
+        float acc0 = 0.f, acc1 = 0.f;
+        if constexpr (GyroT<ID>::S == 32) {
+#pragma unroll
+            for (int t = 0; t < 32; ++t) {
+                uint32_t a0, a1;
+                cb_addr(gyro_kstate<ID>(w, t), a0, a1);
+                const uint32_t p0 = lds_word(book, a0), p1 = lds_word(book, a1);
+                acc0 = fma_hi(p0, x[4 * t + 1], fma_lo(p0, x[4 * t], acc0));
+                acc1 = fma_hi(p1, x[4 * t + 3], fma_lo(p1, x[4 * t + 2], acc1));
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 64; t += 2) {
+                const uint32_t p0 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t)));
+                const uint32_t p1 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t + 1)));
+                acc0 = fma_hi(p0, x[2 * t + 1], fma_lo(p0, x[2 * t], acc0));
+                acc1 = fma_hi(p1, x[2 * t + 3], fma_lo(p1, x[2 * t + 2], acc1));
+            }
+        }
+        return acc0 + acc1;
+    }
+}
+
+// Expands X(ID) for the (uniform) Gyro type id; unknown ids do nothing.
+#define GYRO_TYPE_SWITCH(id, X)       \
+    switch (id) {                     \
+        case 144: X(144); break;      \
+        case 145: X(145); break;      \
+        case 146: X(146); break;      \
+        case 147: X(147); break;      \
+        case 148: X(148); break;      \
+        case 149: X(149); break;      \
+        case 150: X(150); break;      \
+        case 151: X(151); break;      \
+        default: break;               \
+    }
+
+// Block bytes of a Gyro type id (the host admits only the eight types; other ids read as 34).
+__device__ __forceinline__ uint32_t block_bytes_of_type(uint32_t id) {
+    GyroType t;
+    return gd_type(id, t) ? t.block_bytes : 34u;
+}

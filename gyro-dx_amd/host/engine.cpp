@@ -488,17 +488,18 @@ class Engine {
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
-    bool decode_supported(const Layer &L, uint32_t n) const {
-        return L.type_id == 144 && !L.SF && E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
+    bool decode_supported(const Layer &, uint32_t n) const {
+        return E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
     }
+    // Layers other than uniform TQ2_T without a shared expert take the type-generic kernels.
+    static bool decode_generic_types(const Layer &L) { return L.type_id != 144 || L.SF; }
 
     // MI355X decode path: router + rotation, routed gate/up, down + combine.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
-            throw NativeError(-1, "decode path needs TQ2_T, no shared expert, E % 1024 == 0, F == 512, top-8 of <= 256 "
-                                  "experts, n <= 8");
+            throw NativeError(-1, "decode path needs E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
@@ -506,14 +507,29 @@ class Engine {
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
                               bits(L.norm_eps)},
                              std::max(NE, E / 128));
-        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
-                             {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0, base_lo,
-                              base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
+        if (!decode_generic_types(L)) {
+            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
+                                 {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
+                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
+                                 F / 64, 2 * parts, n * U);
+            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
+                                 {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
+                                  2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
+                                  out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
+                                  st.res_off},
+                                 E / 8, n);
+            return;
+        }
+        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_x",
+                             {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
+                              L.xtab.srv, codebook.srv, gu_part.uav, 0, E, F, n},
                              F / 64, 2 * parts, n * U);
-        dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
-                             {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
-                              2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                              out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
+        if (L.SF) shared_expert(L, n, x_uav, x_off);  // on the layer input (not stack-normalised here)
+        dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
+                             {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
+                              L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
+                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, sh_o.uav, 0,
+                              sh_g.uav, 0},
                              E / 8, n);
     }
 
@@ -588,12 +604,20 @@ class Engine {
             const bool first = l == 0;
             const uint32_t s_uav = first ? x_uav : y_uav, s_off = first ? x_off : y_off;
             const uint32_t w_srv = L.has_norm ? L.norm.srv : kNone;
-            if (path == GM_PATH_DECODE) {
+            if (path == GM_PATH_DECODE && !L.SF) {
                 StackStep st;
                 st.on = true;
                 st.res_uav = s_uav;
                 st.res_off = s_off;
                 ffn_decode(list[l], n, s_uav, s_off, y_uav, y_off, 0, nullptr, st);
+            } else if (path == GM_PATH_DECODE) {
+                // The shared expert reads the normalised input, so the norm is its own step.
+                dispatch("moe_stack_norm",
+                         {s_uav, s_off, kNone, 0, w_srv, 0, hn.uav, 0, E, bits(L.norm_eps), kNone, 0}, n);
+                StackStep st;
+                st.res_uav = s_uav;
+                st.res_off = s_off;
+                ffn_decode(list[l], n, hn.uav, 0, y_uav, y_off, 0, nullptr, st);
             } else if (path == GM_PATH_PREFILL) {
                 dispatch("moe_stack_norm",
                          {s_uav, s_off, kNone, 0, w_srv, 0, hn.uav, 0, E, bits(L.norm_eps), kNone, 0}, n);

@@ -56,3 +56,23 @@ def test_reference_path_with_shared_expert(oracle_mod):
     layer = synth.make_layer(101, E=1024, F=256, n_expert=32, n_used=8, SF=256)
     check(oracle_mod, layer, synth.make_tokens(102, 9, layer.E), PATH_REFERENCE, "reference + shared")
     check(oracle_mod, layer, synth.make_tokens(103, 9, layer.E), PATH_GENERIC, "generic + shared")
+
+
+def test_decode_path_mixed_quant_and_shared(oracle_mod):
+    """The decode path's type-generic kernels (moe_decode_gu_x, moe_decode_down_x) on the
+    mixed-quant configuration, with and without the shared expert, at batch 1 and 8."""
+    from gyrodx.engine import PATH_DECODE
+    mixed = synth.make_layer(111, mixed_types=True)
+    check(oracle_mod, mixed, synth.make_tokens(112, 1, mixed.E), PATH_DECODE, "decode mixed n=1")
+    check(oracle_mod, mixed, synth.make_tokens(113, 8, mixed.E), PATH_DECODE, "decode mixed n=8")
+    shared = synth.make_layer(91, mixed_types=True, SF=1024)
+    check(oracle_mod, shared, synth.make_tokens(114, 1, shared.E), PATH_DECODE, "decode mixed + shared n=1")
+    check(oracle_mod, shared, synth.make_tokens(115, 5, shared.E), PATH_DECODE, "decode mixed + shared n=5")
+
+
+@pytest.mark.parametrize("type_id", [145, 147, 149, 151])
+def test_decode_path_uniform_other_types(oracle_mod, type_id):
+    """Uniform non-TQ2_T layers (32- and 64-step trellises) through the type-generic decode."""
+    from gyrodx.engine import PATH_DECODE
+    layer = synth.make_layer(120 + type_id, type_id=type_id)
+    check(oracle_mod, layer, synth.make_tokens(121 + type_id, 3, layer.E), PATH_DECODE, f"decode type {type_id}")
