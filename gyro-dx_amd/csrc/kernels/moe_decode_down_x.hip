@@ -11,8 +11,12 @@
 // Constants: 0 gu_uav 1 gu_off 2 ids_uav 3 ids_off 4 weights_uav 5 weights_off 6 xtab_srv
 // 7 (unused) 8 (unused) 9 (unused) 10 codebook_srv 11 signs_srv (0xffffffff: none) 12 signs_off
 // 13 out_uav 14 out_off 15 E 16 F 17 n_used 18 n_tok 19 parts 20 n_expert 21 residual (0: none,
-// 1: add) 22 res_uav 23 res_off 24 shared (0: none, 1: add sigmoid(g[t]) sh[t][row]) 25 sh_uav
-// 26 sh_off 27 shg_uav 28 shg_off. The combine adds the shared term, then the residual.
+// 1: add) 22 res_uav 23 res_off 24 shared (0: none, 1: the layer's shared expert) 25 sh_h_uav
+// (fp32 [n][2 SF]: W_sg x then W_su x, from moe_router) 26 (unused) 27 shg_uav (g . x [n])
+// 28 shg_off 29 sh_down_srv (bf16 [E][SF]) 30 SF (<= 1024, a multiple of 256). The shared
+// expert's SwiGLU a = silu(W_sg x) * W_su x is formed in LDS and its 8 down rows of the group
+// are dotted with it (32 lanes per row); the combine adds sigmoid(g . x) times that, then the
+// residual.
 // Requires n_used == 8, F == 512 and at most 2 K-parts.
 #include "gyro_fast.h"
 #include "fwht.h"
@@ -23,6 +27,7 @@
 #define DN_NB (DN_F / 128)
 #define DN_MAX_BB 58
 #define DN_EXPERT_WORDS (DN_ROWS * DN_NB * DN_MAX_BB / 4)  // 8 rows of the widest type
+#define DN_SH_MAX_F 1024
 #define DN_BLOCK_STRIDE 132  // floats per 128-block in LDS (bank spread for the 8 x streams)
 
 
@@ -46,6 +51,8 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 256) {
     __shared__ uint32_t rows[DN_U * DN_EXPERT_WORDS];
     __shared__ float act[DN_U * DN_NB * DN_BLOCK_STRIDE];
     __shared__ float dk[DN_U][DN_ROWS];
+    __shared__ float sh_a[DN_SH_MAX_F];
+    __shared__ float shs[DN_ROWS];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t E = a.c[15], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
     const uint32_t t = blockIdx.y, row0 = blockIdx.x * DN_ROWS;
@@ -68,6 +75,24 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 256) {
         const uint32_t c = lane + 64u * j;
         rv0[j] = *reinterpret_cast<const uint4 *>(src0 + min(c, n0 - 1u) * 16u);
         rv1[j] = *reinterpret_cast<const uint4 *>(src1 + min(c, n1 - 1u) * 16u);
+    }
+    // Shared expert inputs, issued with the rows: thread (r = tid / 32, q = tid % 32) holds 8
+    // bf16 of down row row0 + r at columns 8 q + 256 m; thread tid holds the gate and up values
+    // of columns tid + 256 i.
+    const bool shared = a.c[24] != 0u;
+    const uint32_t SF = shared ? a.c[30] : 0u;
+    uint4 sw[DN_SH_MAX_F / 256];
+    float shgv[DN_SH_MAX_F / 256], shuv[DN_SH_MAX_F / 256];
+    if (shared) {
+        const uint16_t *Wsd = gd_buf<const uint16_t>(a, a.c[29]) + (size_t)(row0 + (tid >> 5)) * SF + 8u * (tid & 31u);
+        const float *Hs = gd_buf<const float>(a, a.c[25]) + (size_t)t * 2u * SF;
+#pragma unroll
+        for (int m = 0; m < DN_SH_MAX_F / 256; ++m)
+            if (256u * m < SF) {
+                sw[m] = *reinterpret_cast<const uint4 *>(Wsd + 256u * m);
+                shgv[m] = Hs[tid + 256u * m];
+                shuv[m] = Hs[SF + tid + 256u * m];
+            }
     }
     const uint4 *cb4 = gd_buf<const uint4>(a, a.c[10]);
     const uint4 cb0 = cb4[tid], cb1 = cb4[tid + 256u];
@@ -164,6 +189,11 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 256) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) v[j] *= GD_INV_SQRT128;
     }
+    if (shared) {
+#pragma unroll
+        for (int m = 0; m < DN_SH_MAX_F / 256; ++m)
+            if (256u * m < SF) sh_a[tid + 256u * m] = gd_silu_accurate(shgv[m]) * shuv[m];
+    }
     float4 *dst = reinterpret_cast<float4 *>(act + (kk * DN_NB + b) * DN_BLOCK_STRIDE + l8 * 16u);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
@@ -184,15 +214,33 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 256) {
         s = s + gd_dpp_f<0x4E>(s);  // (b0 + b1) + (b2 + b3)
         if (blk == 0) dk[k][r] = s;
     }
+    if (shared) {  // shared down row row0 + tid / 32 over 32 lanes
+        float p = 0.f;
+        const uint32_t q = tid & 31u;
+#pragma unroll
+        for (int m = 0; m < DN_SH_MAX_F / 256; ++m) {
+            if (256u * m >= SF) break;
+            const uint32_t ww[4] = {sw[m].x, sw[m].y, sw[m].z, sw[m].w};
+            const float *av = sh_a + 8u * q + 256u * m;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                p += gd_bits_f32(ww[e] << 16) * av[2 * e];
+                p += gd_bits_f32(ww[e] & 0xffff0000u) * av[2 * e + 1];
+            }
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
+        if (q == 0) shs[tid >> 5] = p;
+    }
     __syncthreads();
     if (tid < DN_ROWS) {
         cfloat *wts = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * DN_U);
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < DN_U; ++k) acc += wts[k] * dk[k][tid];
-        if (a.c[24]) {
+        if (shared) {
             const float g = gd_sigmoid_accurate(gd_buf<const float>(a, a.c[27])[a.c[28] + t]);
-            acc += g * gd_buf<const float>(a, a.c[25])[a.c[26] + t * E + row0 + tid];
+            acc += g * shs[tid];
         }
         if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + t * E + row0 + tid] + acc;
         gd_buf<float>(a, a.c[13])[a.c[14] + t * E + row0 + tid] = acc;

@@ -13,11 +13,61 @@
 // 8 bias_srv (0xffffffff: none) 9 bias_off 10 logits_uav 11 logits_off 12 signs_srv
 // (0xffffffff: copy) 13 signs_off 14 xh16_uav 15 xh16_off (words) 16 norm (0: none, 1: RMSNorm
 // without weight, 2: with weight; zero when the caller passes 16 constants) 17 norm_w_srv
-// 18 norm_w_off 19 eps (fp32 bits).
+// 18 norm_w_off 19 eps (fp32 bits) 20 shared rows (2 SF; 0: no shared expert) 21 sh_w_srv (bf16
+// [2 SF][E]: gate rows then up rows) 22 sh_h_uav (fp32 [n][2 SF]) 23 sh_gate_srv (fp32 [E])
+// 24 sh_g_uav (fp32 [n]). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 16 + 1
+// further groups after the max(n_expert, E / 128) above: each of the first computes 16 bf16 rows
+// (4 per wave) of W_sg x and W_su x on the unrotated input, the last the gate dot g . x. The
+// shared groups require E <= 2048.
 #include "fwht.h"
 
 #define ROUTER_MAX_TOK 8
 #define ROUTER_MAX_E 4096
+
+#define SH_ROWS_PER_GROUP 16
+#define SH_MAX_E 2048  // hidden width covered by the fused shared-expert rows
+
+// Shared expert rows of group sg: wave w takes rows 16 sg + 4 w .. + 3 of W_sh (bf16, E columns);
+// lane l covers columns 8 l + 512 m (m < E / 512) of every row.
+__device__ __forceinline__ void router_shared_rows(const GdArgs &a, uint32_t sg, uint32_t n_tok, uint32_t E) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t rows = a.c[20], r0 = sg * SH_ROWS_PER_GROUP + wave * 4u;
+    const uint16_t *Wsh = gd_buf<const uint16_t>(a, a.c[21]);
+    const float *X = gd_buf<const float>(a, a.c[0]);
+    float *H = gd_buf<float>(a, a.c[22]);
+    constexpr int MM = SH_MAX_E / 512;  // column chunks
+    uint4 w[4][MM];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+            if (r0 + (uint32_t)i < rows && 512u * m < E)
+                w[i][m] = *reinterpret_cast<const uint4 *>(Wsh + (size_t)(r0 + i) * E + 8u * lane + 512u * m);
+    for (uint32_t t = 0; t < n_tok; ++t) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            if (512u * m >= E) break;
+            const float4 *xp = reinterpret_cast<const float4 *>(X + a.c[1] + t * a.c[2] + 8u * lane + 512u * m);
+            const float4 x0 = xp[0], x1 = xp[1];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ww[4] = {w[i][m].x, w[i][m].y, w[i][m].z, w[i][m].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    acc[i] += gd_bits_f32(ww[q] << 16) * xv[2 * q];
+                    acc[i] += gd_bits_f32(ww[q] & 0xffff0000u) * xv[2 * q + 1];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = gd_wave_sum(acc[i]);
+            if (lane == 0 && r0 + (uint32_t)i < rows) H[t * rows + r0 + i] = v;
+        }
+    }
+}
 
 GD_PIPELINE_NAMED(moe_router, 256) {
     __shared__ float red[4][ROUTER_MAX_TOK], reds[4][ROUTER_MAX_TOK];
@@ -26,6 +76,26 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     const uint32_t n_tok = a.c[3] < ROUTER_MAX_TOK ? a.c[3] : ROUTER_MAX_TOK;
     const uint32_t norm = a.c[16];
     const float *X = gd_buf<const float>(a, a.c[0]);
+    {
+        // Shared-expert groups follow the router and rotation groups (uniform per group).
+        const uint32_t first_sh = max(NE, E / 128u);
+        if (a.c[20] && row >= first_sh) {
+            const uint32_t sg = row - first_sh, n_sg = a.c[20] / SH_ROWS_PER_GROUP;
+            if (sg < n_sg) {
+                router_shared_rows(a, sg, n_tok, E);
+            } else {
+                // The gate dot g . x (fp32 row), one wave per token.
+                const float *G = gd_buf<const float>(a, a.c[23]);
+                for (uint32_t t = wave; t < n_tok; t += 4u) {
+                    float acc = 0.f;
+                    for (uint32_t i = lane; i < E; i += 64u) acc += G[i] * X[x_off + t * x_stride + i];
+                    acc = gd_wave_sum(acc);
+                    if (lane == 0) gd_buf<float>(a, a.c[24])[t] = acc;
+                }
+            }
+            return;
+        }
+    }
     const float *NW = norm == 2u ? gd_buf<const float>(a, a.c[17]) + a.c[18] : nullptr;
     const bool rotate_here = wave == 0 && row < E / 128u;
 

@@ -488,8 +488,10 @@ class Engine {
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
-    bool decode_supported(const Layer &, uint32_t n) const {
-        return E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8;
+    bool decode_supported(const Layer &L, uint32_t n) const {
+        // A shared expert runs fused into moe_router and moe_decode_down_x.
+        const bool shared_ok = !L.SF || (L.SF <= 1024 && L.SF % 256 == 0 && E <= 2048);
+        return E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8 && shared_ok;
     }
     // Layers other than uniform TQ2_T without a shared expert take the type-generic kernels.
     static bool decode_generic_types(const Layer &L) { return L.type_id != 144 || L.SF; }
@@ -499,14 +501,16 @@ class Engine {
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
-            throw NativeError(-1, "decode path needs E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8");
+            throw NativeError(-1, "decode path needs E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8, and "
+                                  "a shared expert (if any) of width <= 1024, a multiple of 256, with E <= 2048");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
-                              bits(L.norm_eps)},
-                             std::max(NE, E / 128));
+                              bits(L.norm_eps), 2 * L.SF, L.SF ? L.sh_gu.srv : 0u, L.SF ? sh_h.uav : 0u,
+                              L.SF ? L.sh_gate.srv : 0u, L.SF ? sh_g.uav : 0u},
+                             std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 16 + 1 : 0));
         if (!decode_generic_types(L)) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
                                  {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
@@ -524,12 +528,11 @@ class Engine {
                              {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
                               L.xtab.srv, codebook.srv, gu_part.uav, 0, E, F, n},
                              F / 64, 2 * parts, n * U);
-        if (L.SF) shared_expert(L, n, x_uav, x_off);  // on the layer input (not stack-normalised here)
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
                              {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
-                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, sh_o.uav, 0,
-                              sh_g.uav, 0},
+                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, sh_h.uav, 0,
+                              sh_g.uav, 0, L.SF ? L.sh_down.srv : 0u, L.SF},
                              E / 8, n);
     }
 
