@@ -27,12 +27,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 #define GG_WROWS 256
 #define GG_NBUF 3
 
-struct __attribute__((aligned(16))) GgLds {
+template <int WROW>
+struct __attribute__((aligned(16))) GgLdsT {
     uint32_t book[2048];
-    gd_u32x4 a[GG_NBUF][GG_ABUF / 16];                // 16-byte chunks
-    gd_u32x4 w[GG_NBUF][GG_WROWS * GG_WROW / 16];     // 16-byte chunks
+    gd_u32x4 a[GG_NBUF][GG_ABUF / 16];             // 16-byte chunks
+    gd_u32x4 w[GG_NBUF][GG_WROWS * WROW / 16];     // 16-byte chunks
     uint32_t src[GG_TM];
 };
+typedef GgLdsT<GG_WROW> GgLds;  // TQ2_T: 3 pieces of 16 bytes per staged block
+typedef GgLdsT<64> GxLds;       // every Gyro type: up to 4 pieces (152.5 KB in all)
 
 // Start of K block kb: waits until at most NEWER of this wave's global-to-LDS loads are
 // outstanding (the loads of the following block), then for LDS traffic, and synchronises the
@@ -63,25 +66,9 @@ __device__ __forceinline__ uint32_t gg_lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 
-// Activations of K block kb into buffer buf: wave w fills rows 32 w .. 32 w + 31 with 8 loads of
-// 4 rows each; roff[i] is the byte offset (from gbase) of this lane's source row for load i plus
-// its swizzled chunk, so block kb adds kb * 256 bytes.
-__device__ __forceinline__ void gg_stage_a(GgLds &sm, uint32_t buf, uint32_t wave, const void *gbase,
-                                           const uint32_t roff[8], uint32_t kb) {
-    const uint32_t base = gg_lds_addr(&sm.a[buf][0]) + wave * 32u * GG_ROW;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) gg_dma16(base + i * 4u * GG_ROW, gbase, roff[i] + kb * 256u);
-}
-
-// Chunk offset of activation load i for a lane: row r = 32 w + 4 i + lane / 16, LDS position
-// p = lane % 16, source chunk p ^ (r % 16).
-__device__ __forceinline__ uint32_t gg_chunk(uint32_t wave, uint32_t lane, int i, uint32_t &row) {
-    row = wave * 32u + (uint32_t)i * 4u + (lane >> 4);
-    return ((lane & 15u) ^ (row & 15u)) * 16u;
-}
-
 // Eight-wave groups: wave w fills activation rows 16 w .. 16 w + 15 with 4 loads of 4 rows.
-__device__ __forceinline__ void gg_stage_a8(GgLds &sm, uint32_t buf, uint32_t wave, const void *gbase,
+template <class LDS>
+__device__ __forceinline__ void gg_stage_a8(LDS &sm, uint32_t buf, uint32_t wave, const void *gbase,
                                             const uint32_t roff[4], uint32_t kb) {
     const uint32_t base = gg_lds_addr(&sm.a[buf][0]) + wave * 16u * GG_ROW;
 #pragma unroll
@@ -104,26 +91,6 @@ __device__ __forceinline__ void gg_stage_w8(GgLds &sm, uint32_t buf, uint32_t wa
     if (wave < 4u) gg_dma16(base + gg_w8_load(wave, 1) * 1024u, wbase, woff[1] + kbo);
 }
 
-// Weight blocks of K block kb into buffer buf: NW loads per wave of 64 lanes, 3 lanes (48 bytes)
-// per weight row, so the 4 waves cover 4 NW 64 / 3 rows; woff[i] is the byte offset (from
-// wbase) of this lane's 16 bytes of block 0, and block kb adds (34 kb) & ~3.
-template <int NW>
-__device__ __forceinline__ void gg_stage_w(GgLds &sm, uint32_t buf, uint32_t wave, const void *wbase,
-                                           const uint32_t woff[NW], uint32_t kb) {
-    const uint32_t base = gg_lds_addr(&sm.w[buf][0]) + wave * NW * 1024u;
-    const uint32_t kbo = (kb * 34u) & ~3u;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) gg_dma16(base + i * 1024u, wbase, woff[i] + kbo);
-}
-
-// The weight row and 16-byte piece that lane `lane` of wave `wave` stages with load i.
-template <int NW>
-__device__ __forceinline__ void gg_w_piece(uint32_t wave, uint32_t lane, int i, uint32_t &row, uint32_t &piece) {
-    const uint32_t g = (wave * NW + (uint32_t)i) * 64u + lane;
-    row = g / 3u;
-    piece = g - row * 3u;
-}
-
 // Weight row q's 9 words of a staged block (scale and stream from the block's 4-byte-aligned
 // start, as tq2_unpack expects).
 struct GgBlk {
@@ -141,7 +108,8 @@ __device__ __forceinline__ void gg_read_w(const GgLds &sm, uint32_t buf, uint32_
 }
 
 // A operand of K-step s (k = 16 s + 8 h .. + 7) for tile row r: chunk 2 s + h of the row.
-__device__ __forceinline__ f16x8 gg_a(const GgLds &sm, uint32_t buf, uint32_t r, int s, uint32_t h) {
+template <class LDS>
+__device__ __forceinline__ f16x8 gg_a(const LDS &sm, uint32_t buf, uint32_t r, int s, uint32_t h) {
     const uint32_t p = ((uint32_t)(2 * s) + h) ^ (r & 15u);
     return __builtin_bit_cast(f16x8, sm.a[buf][r * 16u + p]);
 }
@@ -188,3 +156,265 @@ __device__ __forceinline__ f16x8 gg_scale(const uint32_t raw[4], half2_t scale2)
 // v_perm selectors of gg_gather_piece: lane half 0 takes steps 4i, 4i+1, lane half 1 steps
 // 4i+2, 4i+3.
 __device__ __forceinline__ uint32_t gg_sel(uint32_t h) { return h ? 0x06070506u : 0x04050304u; }
+
+// ---- Every Gyro type (the type-generic grouped GEMMs) ------------------------------------
+// A staged weight row holds the block of K block kb from its 4-byte-aligned start (kb BB) & ~3
+// (every Gyro block size is 2 mod 4, so the block starts at byte 2 (kb % 2) of it) in
+// P = ceil((BB + 2) / 16) pieces of 16 bytes; the rows of one matrix are packed at 16 P bytes.
+__device__ __forceinline__ uint32_t gx_pieces_of(uint32_t bb) { return (bb + 2u + 15u) / 16u; }
+
+// LDS byte address of the codebook pair idx0 of a 15-bit state (as gg_cb_addr).
+__device__ __forceinline__ uint32_t gg_cb_addr0(uint32_t s) {
+    const uint32_t p = __umul24(s, 0x3779B1u);
+    uint32_t t;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(t) : "v"(s), "s"(0x13C0u), "v"(p >> 19));
+    return t & 0x1ffcu;
+}
+
+// Stream words of a k-bit block as lane half h reads them. The B operand of K-step s for half h
+// covers k = 16 s + 8 h .. + 7: trellis steps 4 s + 2 h, + 1 of a 32-step type (two pairs per
+// step), 8 s + 4 h .. + 3 of a 64-step type (one pair per step). Half 1's steps are D = 2 or 4
+// steps after half 0's, i.e. its windows sit D K bits lower in the circular stream; rotating
+// the stream up by D K bits (< 32) for half 1 gives both halves the same window offsets.
+template <int ID>
+__device__ __forceinline__ void gx_half_stream(uint32_t (&w)[gyro_nw<ID>()], uint32_t h) {
+    constexpr int NW = gyro_nw<ID>(), R = (GyroT<ID>::S == 32 ? 2 : 4) * GyroT<ID>::K;
+    uint32_t r[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) r[i] = __builtin_amdgcn_alignbit(w[i], w[(i + NW - 1) % NW], 32 - R);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = h ? r[i] : w[i];
+}
+
+// Codebook reads of piece p (0, 1) of K-step s from the half-adjusted stream words: a 32-step
+// type's state of step 4 s + p (pairs idx0, idx1), a 64-step type's states of steps 8 s + 2 p
+// and + 1 (pair idx0 each); into raw[2 p], raw[2 p + 1], the weights in k order.
+template <int ID>
+__device__ __forceinline__ void gx_gather_piece(const uint32_t (&w)[gyro_nw<ID>()], int s, int p, const uint32_t *book,
+                                                uint32_t raw[4]) {
+    if constexpr (GyroT<ID>::S == 32) {
+        uint32_t a0, a1;
+        gg_cb_addr(gyro_kstate<ID>(w, 4 * s + p), a0, a1);
+        raw[2 * p] = book[a0 >> 2];
+        raw[2 * p + 1] = book[a1 >> 2];
+    } else {
+        raw[2 * p] = book[gg_cb_addr0(gyro_kstate<ID>(w, 8 * s + 2 * p)) >> 2];
+        raw[2 * p + 1] = book[gg_cb_addr0(gyro_kstate<ID>(w, 8 * s + 2 * p + 1)) >> 2];
+    }
+}
+
+// K loop of the type-generic grouped GEMMs (moe_prefill_gu_x, moe_prefill_down_x): eight waves,
+// 128 activation rows and 256 staged weight rows per K block in the three-buffer direct-load
+// pipeline of the TQ2_T kernels; each wave decodes blocks of one (uniform) Gyro type.
+struct GxState {
+    const void *xbase;                   // activation rows
+    const void *wb[2];                   // matrix of each of this wave's weight loads
+    uint32_t roff[4], woff[2], wbb[2];   // per load: lane offset at block 0, block bytes
+    uint32_t nwl;                        // weight loads per block of this wave (1 or 2)
+    uint32_t wave, m, h, nk;
+    uint32_t wrow;                       // LDS byte offset (in a weight buffer) of this lane's row
+};
+
+// Start of K block kb: the wave's loads of block kb have landed once at most the loads of block
+// kb + 1 (4 activation loads and nwl weight loads) are outstanding.
+__device__ __forceinline__ void gx_sync(const GxState &t, uint32_t kb) {
+    if (kb + 1u < t.nk) {
+        if (t.nwl == 2u) gg_sync<6>();
+        else gg_sync<5>();
+    } else {
+        gg_sync<0>();
+    }
+}
+
+// Stages K block kb into buffer buf: the wave's 4 activation loads, then its weight loads w and
+// (nwl == 2) w + 8 at LDS byte 1024 L of the weight buffer; block kb of a row starts at its
+// matrix row's byte (kb BB) & ~3.
+__device__ __forceinline__ void gx_stage(GxLds &sm, uint32_t buf, const GxState &t, uint32_t kb) {
+    gg_stage_a8(sm, buf, t.wave, t.xbase, t.roff, kb);
+    const uint32_t base = gg_lds_addr(&sm.w[buf][0]);
+    gg_dma16(base + t.wave * 1024u, t.wb[0], t.woff[0] + ((kb * t.wbb[0]) & ~3u));
+    if (t.nwl == 2u) gg_dma16(base + (t.wave + 8u) * 1024u, t.wb[1], t.woff[1] + ((kb * t.wbb[1]) & ~3u));
+}
+
+// K block kb from buffer BUF for NRB 32-row blocks with blocks of Gyro type ID, in the software
+// pipeline of the TQ2_T kernels: between the MFMAs of K-step s go the codebook reads of step
+// s + 1 (two pieces over the first two slots) and its A operands (one per slot).
+template <int ID, int BUF, int NRB>
+__device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb, f32x16 (&acc)[NRB]) {
+    gx_sync(t, kb);
+    if (kb + 2u < t.nk) gx_stage(sm, (BUF + 2) % 3, t, kb + 2u);
+    constexpr int NW = gyro_nw<ID>(), NQ = (NW + 1 + 3) / 4;
+    const gd_u32x4 *rq = reinterpret_cast<const gd_u32x4 *>(reinterpret_cast<const uint8_t *>(&sm.w[BUF][0]) + t.wrow);
+    uint32_t d[4 * NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        const gd_u32x4 v = rq[j];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d[4 * j + c] = v[c];
+    }
+    float sc;
+    uint32_t w[NW], raw[4], pr = 0;
+    const uint32_t sel = gg_sel(t.h);
+    if constexpr (ID == 144) {
+        tq2_unpack(d, (kb & 1u) != 0u, sc, w);
+        gg_gather(w, 0, sel, sm.book, raw);
+    } else {
+        gyro_unpack<ID>(d, (kb & 1u) != 0u, sc, w);
+        gx_half_stream<ID>(w, t.h);
+        gx_gather_piece<ID>(w, 0, 0, sm.book, raw);
+        gx_gather_piece<ID>(w, 0, 1, sm.book, raw);
+    }
+    const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
+    f16x8 av[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) av[rb] = gg_a(sm, BUF, rb * 32u + t.m, 0, t.h);
+    constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const f16x8 bv = gg_scale(raw, sc2);
+        f16x8 cur[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) cur[rb] = av[rb];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s < 7) {
+#pragma unroll
+                for (int piece = 0; piece < 2; ++piece) {
+                    if (i < kPieceSlots && piece * kPieceSlots / 2 == i) {
+                        if constexpr (ID == 144) gg_gather_piece(w, s + 1, piece, sel, sm.book, pr, raw);
+                        else gx_gather_piece<ID>(w, s + 1, piece, sm.book, raw);
+                    }
+                }
+                av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// The whole K loop of a tile for the wave's Gyro type `type` (uniform per wave; the callers
+// admit only the eight types, so every wave takes one case and reaches every sync). Blocks
+// rotate through the three buffers: block kb in buffer kb % 3.
+template <int ID, int NRB>
+__device__ __forceinline__ void gx_kloop(GxLds &sm, const GxState &t, f32x16 (&acc)[NRB]) {
+    for (uint32_t kb = 0; kb < t.nk; kb += 3u) {
+        gx_step<ID, 0, NRB>(sm, t, kb, acc);
+        if (kb + 1u < t.nk) gx_step<ID, 1, NRB>(sm, t, kb + 1u, acc);
+        if (kb + 2u < t.nk) gx_step<ID, 2, NRB>(sm, t, kb + 2u, acc);
+    }
+}
+template <int NRB>
+__device__ __forceinline__ void gx_run(GxLds &sm, const GxState &t, uint32_t type, f32x16 (&acc)[NRB]) {
+#pragma unroll
+    for (int r = 0; r < NRB; ++r) acc[r] = (f32x16){};
+#define GX_KLOOP(ID) gx_kloop<ID, NRB>(sm, t, acc)
+    GYRO_TYPE_SWITCH(type, GX_KLOOP)
+#undef GX_KLOOP
+    gg_sync<0>();  // every wave is done with the buffers
+}
+
+// ---- Epilogues shared by the TQ2_T and the type-generic kernels ---------------------------
+// Gate/up epilogue of a tile of NRB 32-row blocks after the K loop (every wave past its last
+// sync): wave w holds, for rows rb * 32 + 8 (r / 4) + 4 h + r % 4 and F-block column
+// 32 (w % 4) + m, the gate (w < 4) or up (w >= 4) products in acc[rb][r].
+// (1) The up waves store u, fp32 [row][column], over activation buffers 0 and 1 (64 KB).
+// (2) The gate waves form act = down_signs * silu(g) * u, rounded to binary16, into activation
+//     buffer 2 in the A-operand layout.
+// (3) With down signs, the 128-point Walsh-Hadamard transform of every row as a GEMM with H_128
+//     (entries (-1)^popcount(k & j), exact in binary16): wave w computes output columns
+//     32 (w % 4) .. + 31 of the row blocks rb with rb % 2 == w / 4. The B operand of lane (j, h)
+//     at K-step s holds H[16 s + 8 h + e][j] for e = 0..7, the lane's fixed pattern
+//     (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j). Scaled rows go to activation
+//     buffer 0 (same layout).
+// (4) Rows of 128 binary16 values (16 swizzled chunks) to out[row0 + i][fb * 128 ..].
+template <class LDS, int NRB>
+__device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
+                                               uint32_t h, const float *signs, uint32_t *out, uint32_t row0,
+                                               uint32_t rows, uint32_t fb, uint32_t F) {
+    const bool up = wave >= 4u;
+    const uint32_t cq = wave & 3u, col = cq * 32u + m;
+    float *ubuf = reinterpret_cast<float *>(&sm.a[0][0]);
+    if (up) {
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ubuf[(rb * 32u + (r / 4) * 8u + h * 4u + (r % 4)) * 128u + col] = acc[rb][r];
+    }
+    __syncthreads();
+    _Float16 *act = reinterpret_cast<_Float16 *>(&sm.a[2][0]);
+    if (!up) {
+        const float sgn = signs ? signs[fb * 128u + col] : 1.0f;
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
+                act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
+                    (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[i * 128u + col] * sgn);
+            }
+        }
+    }
+    __syncthreads();
+    if (signs) {
+        const uint32_t j = col, half = wave >> 2;
+        f16x8 hp, hn;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            hp[e] = (__builtin_popcount((uint32_t)e & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
+            hn[e] = -hp[e];
+        }
+        _Float16 *res = reinterpret_cast<_Float16 *>(&sm.a[0][0]);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            if ((uint32_t)(rb & 1) != half) continue;  // uniform per wave
+            f32x16 rot = (f32x16){};
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * h) & j) & 1) ? hn : hp;
+                rot = __builtin_amdgcn_mfma_f32_32x32x16_f16(gg_a(sm, 2, rb * 32u + m, s8, h), hb, rot, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
+            }
+        }
+        __syncthreads();
+    }
+    const gd_u32x4 *rows_src = signs ? &sm.a[0][0] : &sm.a[2][0];
+    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
+        const uint32_t i = idx >> 4, c = idx & 15u;
+        *reinterpret_cast<gd_u32x4 *>(out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u) =
+            rows_src[i * 16u + (c ^ (i & 15u))];
+    }
+}
+
+// Down epilogue: wave w holds output columns 32 w + m of rows rb * 32 + 8 (r / 4) + 4 h + r % 4.
+// The results pass through LDS rows of 256 floats (the 128-byte half of row i's 64-column pair
+// at half (w ^ (i >> 2)) & 1, so that the two lane halves, rows i and i + 4, write different
+// banks), then every sorted row i leaves as 64 chunks of 16 bytes to out[src[i]][eb * 256 ..].
+template <class LDS, int NRB>
+__device__ __forceinline__ void gg_down_epilogue(LDS &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
+                                                 uint32_t h, float *out, uint32_t rows, uint32_t eb, uint32_t E) {
+    float *res = reinterpret_cast<float *>(&sm.a[0][0]);
+    static_assert(sizeof(sm.a) + sizeof(sm.w) >= 128u * 256u * 4u, "result rows fit the K-loop buffers");
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
+            const uint32_t w = wave ^ ((i >> 2) & 1u);
+            res[i * 256u + w * 32u + m] = acc[rb][r];
+        }
+    }
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < rows * 64u; idx += 512u) {
+        const uint32_t i = idx >> 6, c = idx & 63u;    // chunk c: columns 4 c .. 4 c + 3
+        const uint32_t w = (c >> 3) ^ ((i >> 2) & 1u);  // the 32-column group's stored half
+        const float4 v = *reinterpret_cast<const float4 *>(res + i * 256u + w * 32u + (c & 7u) * 4u);
+        *reinterpret_cast<float4 *>(out + (size_t)sm.src[i] * E + eb * 256u + c * 4u) = v;
+    }
+}

@@ -91,29 +91,7 @@ __device__ __forceinline__ void dn_tile(GgLds &sm, const DnState &t, const GdArg
         if (kb + 2u < t.nk) dn_step<2, NRB>(sm, t, kb + 2u, acc);
     }
     gg_sync<0>();  // every wave is done with the buffers
-    // Results into LDS rows of 256 floats; the 128-byte half (32 columns) of row i sits at half
-    // ((w ^ (i >> 2)) & 1) of its 64-column pair so that the two lane halves (rows i, i + 4)
-    // write different banks.
-    float *res = reinterpret_cast<float *>(&sm.a[0][0]);
-    static_assert(sizeof(sm.a) + sizeof(sm.w) >= 128u * 256u * 4u, "result rows fit the K-loop buffers");
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-            const uint32_t w = t.wave ^ ((i >> 2) & 1u);
-            res[i * 256u + w * 32u + t.m] = acc[rb][r];
-        }
-    }
-    __syncthreads();
-    // Sorted row i (slot sm.src[i]): 64 chunks of 16 bytes to down32[slot][eb * 256 ..].
-    float *out = gd_buf<float>(a, a.c[10]) + a.c[11];
-    for (uint32_t idx = threadIdx.x; idx < rows * 64u; idx += 512u) {
-        const uint32_t i = idx >> 6, c = idx & 63u;        // chunk c: columns 4 c .. 4 c + 3
-        const uint32_t w = (c >> 3) ^ ((i >> 2) & 1u);      // the 32-column group's stored half
-        const float4 v = *reinterpret_cast<const float4 *>(res + i * 256u + w * 32u + (c & 7u) * 4u);
-        *reinterpret_cast<float4 *>(out + (size_t)sm.src[i] * E + eb * 256u + c * 4u) = v;
-    }
+    gg_down_epilogue(sm, acc, t.wave, t.m, t.h, gd_buf<float>(a, a.c[10]) + a.c[11], rows, eb, E);
 }
 
 GD_PIPELINE_NAMED_OCC(moe_prefill_down, 512, 2) {

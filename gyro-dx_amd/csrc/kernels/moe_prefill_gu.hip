@@ -105,77 +105,8 @@ __device__ __forceinline__ void gu_tile(GgLds &sm, const GuState &t, const GdArg
         if (kb + 2u < t.nk) gu_step<2, NRB>(sm, t, kb + 2u, acc);
     }
     gg_sync<0>();  // every wave is done with the buffers
-
-    // Epilogue. (1) The up waves store u, fp32 [row][column of the F block], over activation
-    // buffers 0 and 1 (64 KB).
-    const bool up = t.wave >= 4u;
-    const uint32_t cq = t.wave & 3u, col = cq * 32u + t.m;
-    float *ubuf = reinterpret_cast<float *>(&sm.a[0][0]);
-    if (up) {
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ubuf[(rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4)) * 128u + col] = acc[rb][r];
-    }
-    __syncthreads();
-    // (2) The gate waves form act = down_signs * silu(g) * u, rounded to binary16, into
-    // activation buffer 2 in the A-operand layout (row i, column col of the F block).
-    const bool has_signs = a.c[10] != 0xffffffffu;
-    _Float16 *act = reinterpret_cast<_Float16 *>(&sm.a[2][0]);
-    if (!up) {
-        const float sgn = has_signs ? gd_buf<const float>(a, a.c[10])[a.c[11] + fb * 128u + col] : 1.0f;
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-                act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
-                    (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[i * 128u + col] * sgn);
-            }
-        }
-    }
-    __syncthreads();
-    uint32_t *out = gd_buf<uint32_t>(a, a.c[12]) + a.c[13];
-    if (has_signs) {
-        // (3) The 128-point Walsh-Hadamard transform of every row as a GEMM with H_128 (entries
-        // (-1)^popcount(k & j), exact in binary16): wave w computes output columns 32 (w % 4)
-        // .. + 31 of the row blocks rb with rb % 2 == w / 4. The B operand of lane (j, h) at
-        // K-step s holds H[16 s + 8 h + e][j] for e = 0..7, which is the lane's fixed pattern
-        // (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j).
-        const uint32_t j = col, half = t.wave >> 2;
-        f16x8 hp, hn;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            hp[e] = (__builtin_popcount((uint32_t)e & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
-            hn[e] = -hp[e];
-        }
-        _Float16 *res = reinterpret_cast<_Float16 *>(&sm.a[0][0]);
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-            if ((uint32_t)(rb & 1) != half) continue;  // uniform per wave
-            f32x16 rot = (f32x16){};
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8) {
-                const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * t.h) & j) & 1) ? hn : hp;
-                rot = __builtin_amdgcn_mfma_f32_32x32x16_f16(gg_a(sm, 2, rb * 32u + t.m, s8, t.h), hb, rot, 0, 0, 0);
-            }
-            // (4) Scaled rows into activation buffer 0 (same layout).
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t i = rb * 32u + (r / 4) * 8u + t.h * 4u + (r % 4);
-                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
-            }
-        }
-        __syncthreads();
-    }
-    // Rows of 128 binary16 values (16 chunks of 16 bytes, swizzled) to act16[row0 + i][fb * 128 ..].
-    const gd_u32x4 *rows_src = has_signs ? &sm.a[0][0] : &sm.a[2][0];
-    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
-        const uint32_t i = idx >> 4, c = idx & 15u;
-        *reinterpret_cast<gd_u32x4 *>(out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u) =
-            rows_src[i * 16u + (c ^ (i & 15u))];
-    }
+    const float *signs = a.c[10] != 0xffffffffu ? gd_buf<const float>(a, a.c[10]) + a.c[11] : nullptr;
+    gg_gu_epilogue(sm, acc, t.wave, t.m, t.h, signs, gd_buf<uint32_t>(a, a.c[12]) + a.c[13], row0, rows, fb, F);
 }
 
 GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 2) {

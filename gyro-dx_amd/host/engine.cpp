@@ -83,14 +83,16 @@ float half_to_float(uint16_t h) {
     return f;
 }
 
-// Largest |scale| of the TQ2_T blocks in `bytes` bytes of packed rows (34-byte blocks).
-float max_block_scale(const uint8_t *p, uint64_t bytes) {
+// Largest |scale| of the Gyro blocks (bb bytes each, the scale in the first two) in `bytes`
+// bytes of packed rows; a NaN scale reads as infinite.
+float max_block_scale(const uint8_t *p, uint64_t bytes, uint32_t bb) {
     float m = 0;
-    for (uint64_t off = 0; off + 34 <= bytes; off += 34) {
+    for (uint64_t off = 0; off + bb <= bytes; off += bb) {
         uint16_t h;
         std::memcpy(&h, p + off, 2);
         const float v = std::fabs(half_to_float(h));
-        if (!(v <= m)) m = v;  // NaN propagates as "too large"
+        if (v != v) return INFINITY;
+        m = std::max(m, v);
     }
     return m;
 }
@@ -310,9 +312,9 @@ class Engine {
             upload(arena, off, d.gate[e], gb[e]);
             upload(arena, off + gb[e], d.up[e], ub[e]);
             upload(arena, off + gb[e] + ub[e], d.down[e], db[e]);
-            if (uniform && d.types[0] == 144)
-                L.max_scale = std::max({L.max_scale, max_block_scale(d.gate[e], gb[e]), max_block_scale(d.up[e], ub[e]),
-                                        max_block_scale(d.down[e], db[e])});
+            L.max_scale = std::max({L.max_scale, max_block_scale(d.gate[e], gb[e], block_bytes_of(d.types[e * 3])),
+                                    max_block_scale(d.up[e], ub[e], block_bytes_of(d.types[e * 3 + 1])),
+                                    max_block_scale(d.down[e], db[e], block_bytes_of(d.types[e * 3 + 2]))});
             lookup.words()[il * NE + e] = slot;
             desc[e].gate = arena.gpu + off;
             desc[e].up = arena.gpu + off + gb[e];
@@ -537,10 +539,10 @@ class Engine {
     }
 
     // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;
-    // every such product must be finite in binary16.
+    // every such product must be finite in binary16. Uniform TQ2_T layers take moe_prefill_gu /
+    // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
     bool prefill_supported(const Layer &L) const {
-        return L.type_id == 144 && !L.SF && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
-               L.max_scale * max_codebook < 65504.0f;
+        return !L.SF && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 && L.max_scale * max_codebook < 65504.0f;
     }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
@@ -550,11 +552,12 @@ class Engine {
                      uint32_t res_off = 0) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
-            throw NativeError(-1, "prefill path needs TQ2_T, no shared expert, E and F multiples of 256, top-8 of "
-                                  "<= 256 experts and binary16-finite scale x codebook products");
+            throw NativeError(-1, "prefill path needs no shared expert, E and F multiples of 256, top-8 of <= 256 "
+                                  "experts and binary16-finite scale x codebook products");
         if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (4096 tokens of top-8)");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
+        const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
@@ -563,14 +566,24 @@ class Engine {
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0}, (n + 3) / 4);
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
                              {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows}, 1);
-        dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
-                             {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
-                              codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, act.uav, 0, E, F, U},
-                             F / 128, tiles);
-        dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down",
-                             {meta.uav, order.uav, 0, act.uav, 0, base_lo, base_hi, slot_stride, 2 * L.gate_bytes,
-                              codebook.srv, down.uav, 0, E, F},
-                             E / 256, tiles);
+        if (L.type_id == 144) {
+            dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
+                                 {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
+                                  codebook.srv, signs, E, act.uav, 0, E, F, U},
+                                 F / 128, tiles);
+            dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down",
+                                 {meta.uav, order.uav, 0, act.uav, 0, base_lo, base_hi, slot_stride, 2 * L.gate_bytes,
+                                  codebook.srv, down.uav, 0, E, F},
+                                 E / 256, tiles);
+        } else {
+            dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu_x",
+                                 {meta.uav, order.uav, 0, xh.uav, 0, L.xtab.srv, codebook.srv, signs, E, act.uav, 0, E,
+                                  F, U},
+                                 F / 128, tiles);
+            dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down_x",
+                                 {meta.uav, order.uav, 0, act.uav, 0, L.xtab.srv, codebook.srv, down.uav, 0, E, F},
+                                 E / 256, tiles);
+        }
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
                              {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u, res_uav,
                               res_off},

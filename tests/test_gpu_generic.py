@@ -22,7 +22,7 @@ def separable(oracle_layer, x, U, margin=1e-5):
 
 
 def check(oracle_mod, layer, x, path, what, max_tok=16):
-    eng = Engine(max_tok=max_tok)
+    eng = Engine(max_tok=max(max_tok, x.shape[0]))
     try:
         eng.add_layer(layer)
         ol = oracle_mod.OracleLayer(layer)
@@ -76,3 +76,38 @@ def test_decode_path_uniform_other_types(oracle_mod, type_id):
     from gyrodx.engine import PATH_DECODE
     layer = synth.make_layer(120 + type_id, type_id=type_id)
     check(oracle_mod, layer, synth.make_tokens(121 + type_id, 3, layer.E), PATH_DECODE, f"decode type {type_id}")
+
+
+def test_prefill_path_mixed_types(oracle_mod):
+    """The type-generic grouped GEMMs (moe_prefill_gu_x, moe_prefill_down_x) on the mixed-quant
+    layer: a Gyro type per expert and projection drawn from all eight, rotations; 512 tokens and
+    a ragged 37."""
+    from gyrodx.engine import PATH_PREFILL
+    layer = synth.make_layer(131, mixed_types=True)
+    check(oracle_mod, layer, synth.make_tokens(132, 512, layer.E), PATH_PREFILL, "prefill mixed n=512")
+    check(oracle_mod, layer, synth.make_tokens(133, 37, layer.E), PATH_PREFILL, "prefill mixed n=37")
+
+
+@pytest.mark.parametrize("type_id", [145, 147, 149, 151])
+def test_prefill_path_uniform_other_types(oracle_mod, type_id):
+    """Uniform non-TQ2_T layers (32- and 64-step trellises, 18- to 58-byte blocks) through the
+    type-generic prefill GEMMs, without rotations for one of them."""
+    from gyrodx.engine import PATH_PREFILL
+    layer = synth.make_layer(140 + type_id, type_id=type_id, signs=type_id != 147)
+    check(oracle_mod, layer, synth.make_tokens(141 + type_id, 200, layer.E), PATH_PREFILL, f"prefill type {type_id}")
+
+
+def test_prefill_refuses_fp16_overflowing_scales_any_type():
+    """A block scale of any Gyro type whose products with the codebook overflow binary16 makes the
+    prefill path refuse the layer."""
+    from gyrodx.engine import PATH_PREFILL
+    layer = synth.make_layer(151, E=1024, F=256, n_expert=16, n_used=8, mixed_types=True)
+    e = 3
+    layer.down[e][7, 0:2] = np.frombuffer(np.float16(60000.0).tobytes(), np.uint8)
+    eng = Engine(max_tok=8)
+    try:
+        eng.add_layer(layer)
+        with pytest.raises(RuntimeError, match="binary16-finite"):
+            eng.forward(0, synth.make_tokens(152, 4, layer.E), PATH_PREFILL)
+    finally:
+        eng.close()
