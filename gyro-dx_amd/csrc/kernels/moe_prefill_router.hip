@@ -17,7 +17,8 @@
 // Constants: 0 x_uav 1 x_off (words; rows of E floats) 2 n_tok 3 E 4 router_srv 5 router_off
 // 6 n_expert 7 bias_srv (0xffffffff: none) 8 bias_off 9 logits_uav 10 logits_off
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
-// 14 xh16_off (words).
+// 14 xh16_off (words) 15 x16 (1: also write the unrotated input as binary16, for the shared
+// expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words).
 #include "ggemm.h"
 #include "fwht.h"
 
@@ -40,6 +41,20 @@ __device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf,
     for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xbase, xoff[i] + kbytes);
 #pragma unroll
     for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
+}
+
+// Sixteen values as binary16 pairs (32 bytes) at dst.
+__device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16]) {
+    gd_u32x4 o[2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
+        const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+        o[j >> 2][j & 3] = h0 | (h1 << 16);
+    }
+    gd_u32x4 *d = reinterpret_cast<gd_u32x4 *>(dst);
+    d[0] = o[0];
+    d[1] = o[1];
 }
 
 GD_PIPELINE_NAMED(moe_prefill_router, 256) {
@@ -86,6 +101,7 @@ GD_PIPELINE_NAMED(moe_prefill_router, 256) {
                     const float4 f = src[q];
                     v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
                 }
+                if (a.c[15]) rt_store_h16(gd_buf<uint32_t>(a, a.c[16]) + a.c[17] + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v);
                 if (has_signs) {
                     const float4 *sg = reinterpret_cast<const float4 *>(S + i);
 #pragma unroll
@@ -101,16 +117,7 @@ GD_PIPELINE_NAMED(moe_prefill_router, 256) {
 #pragma unroll
                     for (int j = 0; j < 16; ++j) v[j] *= GD_INV_SQRT128;
                 }
-                gd_u32x4 o[2];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
-                    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
-                    o[j >> 2][j & 3] = h0 | (h1 << 16);
-                }
-                gd_u32x4 *dst = reinterpret_cast<gd_u32x4 *>(XH + (size_t)t * (E / 2u) + blk * 64u + 8u * l8);
-                dst[0] = o[0];
-                dst[1] = o[1];
+                rt_store_h16(XH + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v);
             }
         }
     }

@@ -63,6 +63,8 @@ struct Layer {
     float max_scale = 0;      // largest |block scale| over the layer's experts
     uint32_t SF = 0;          // shared expert width (0: none)
     Buffer sh_gu, sh_down, sh_gate;  // bf16 [2 SF][E] (gate rows, then up rows), [E][SF]; fp32 [E]
+    Buffer sh_gu16, sh_down16;       // binary16 copies x 2^k per matrix (prefill path)
+    float sh_unscale[3] = {1, 1, 1}; // 2^-k of the gate, up and down copies
     Buffer norm;                     // fp32 [E] RMSNorm weight of the layer's input in a stack
     bool has_norm = false;
     float norm_eps = 0;
@@ -97,6 +99,54 @@ float max_block_scale(const uint8_t *p, uint64_t bytes, uint32_t bb) {
     return m;
 }
 
+float bf16_to_float(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// float -> binary16, round to nearest even (subnormals included; overflow to infinity).
+uint16_t float_to_half(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    x &= 0x7fffffffu;
+    if (x >= 0x7f800000u) return sign | 0x7c00u | (x > 0x7f800000u ? 0x200u : 0u);
+    const int e = (int)(x >> 23) - 127;
+    if (e < -14) {  // subnormal binary16: units of 2^-24
+        const double q = std::nearbyint((double)std::fabs(f) * 16777216.0);  // ties to even
+        return sign | (uint16_t)q;  // q == 1024 is the smallest normal, same bits
+    }
+    uint32_t m = (x & 0x7fffffu) | 0x800000u, r = m >> 13;
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    int eb = e + 15;
+    if (r == 0x800u) {
+        r = 0x400u;
+        ++eb;
+    }
+    if (eb >= 31) return sign | 0x7c00u;
+    return sign | (uint16_t)(eb << 10) | (uint16_t)(r & 0x3ffu);
+}
+
+// Binary16 copy of n bf16 values times 2^k, k chosen so that the largest finite |value| lands in
+// [2^14, 2^15) (every bf16 value whose scaled magnitude is a normal binary16 converts exactly:
+// bf16 carries 8 significant bits, binary16 11). Returns 2^-k.
+float bf16_to_scaled_half(const uint16_t *src, size_t n, std::vector<uint16_t> &dst) {
+    float mx = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const float v = std::fabs(bf16_to_float(src[i]));
+        if (v == v && v != INFINITY) mx = std::max(mx, v);
+    }
+    int ex = 0;
+    if (mx > 0) std::frexp(mx, &ex);  // mx < 2^ex
+    const int k = mx > 0 ? 15 - ex : 0;
+    dst.resize(n);
+    for (size_t i = 0; i < n; ++i) dst[i] = float_to_half(std::ldexp(bf16_to_float(src[i]), k));
+    return std::ldexp(1.0f, -k);
+}
+
 std::vector<uint8_t> read_file(const std::string &path) {
     std::ifstream f(path, std::ios::binary);
     return std::vector<uint8_t>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
@@ -128,6 +178,7 @@ class Engine {
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
     Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
     Buffer sh_h, sh_a, sh_o, sh_g;  // shared expert: [T][2 SF], [T][SF], [T][E], [T]
+    Buffer x16;                     // prefill shared expert: the unrotated input [T][E] binary16
     uint32_t sh_width = 0;          // SF the shared buffers are sized for
     Buffer tokens, outputs;
     Buffer hn;  // stack: the normalised input of the current layer [T][E]
@@ -362,6 +413,16 @@ class Engine {
             upload(L.sh_down, 0, d.sh_down, half);
             L.sh_gate = dev.buffer((uint64_t)E * 4, Kind::device);
             upload(L.sh_gate, 0, d.sh_gate_inp, (uint64_t)E * 4);
+            std::vector<uint16_t> h16;
+            L.sh_gu16 = dev.buffer(2 * half, Kind::device);
+            L.sh_unscale[0] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_gate), half / 2, h16);
+            upload(L.sh_gu16, 0, h16.data(), half);
+            L.sh_unscale[1] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_up), half / 2, h16);
+            upload(L.sh_gu16, half, h16.data(), half);
+            L.sh_down16 = dev.buffer(half, Kind::device);
+            L.sh_unscale[2] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_down), half / 2, h16);
+            upload(L.sh_down16, 0, h16.data(), half);
+            if (!x16.handle) x16 = dev.buffer((uint64_t)max_tok * E * 2, Kind::device);
             if (d.SF > sh_width) {
                 for (Buffer *b : {&sh_h, &sh_a, &sh_o, &sh_g})
                     if (b->handle) dev.release(*b);
@@ -541,26 +602,31 @@ class Engine {
     // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;
     // every such product must be finite in binary16. Uniform TQ2_T layers take moe_prefill_gu /
     // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
+    // A shared expert runs as moe_prefill_shared (SF a multiple of 64).
     bool prefill_supported(const Layer &L) const {
-        return !L.SF && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 && L.max_scale * max_codebook < 65504.0f;
+        return L.SF % 64 == 0 && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
+               L.max_scale * max_codebook < 65504.0f;
     }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
-    // down GEMMs, combine. bracket: 1 router, 2 gate/up, 3 down, 4 top-k, 5 sort, 6 combine.
+    // down GEMMs, shared expert, combine. bracket: 1 router, 2 gate/up, 3 down, 4 top-k, 5 sort,
+    // 6 combine, 7 shared gate/up, 8 shared down.
     void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                      int bracket = 0, std::vector<uint32_t> *marks = nullptr, uint32_t res_uav = kNone,
                      uint32_t res_off = 0) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
-            throw NativeError(-1, "prefill path needs no shared expert, E and F multiples of 256, top-8 of <= 256 "
-                                  "experts and binary16-finite scale x codebook products");
+            throw NativeError(-1, "prefill path needs E and F multiples of 256, top-8 of <= 256 experts, a shared "
+                                  "expert (if any) of width a multiple of 64 and binary16-finite scale x codebook "
+                                  "products");
         if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (4096 tokens of top-8)");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
-                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0},
+                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
+                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0},
                              (n + 31) / 32, (NE + 31) / 32);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0}, (n + 3) / 4);
@@ -584,9 +650,23 @@ class Engine {
                                  {meta.uav, order.uav, 0, act.uav, 0, L.xtab.srv, codebook.srv, down.uav, 0, E, F},
                                  E / 256, tiles);
         }
+        if (L.SF) {
+            // Shared expert (bracket 7): a = silu(W_g x) * W_u x into sh_a (binary16), then
+            // W_d a into sh_o; the combine adds sigmoid(x . shared_gate) * sh_o.
+            const uint32_t tt = (n + 63) / 64;
+            dispatch_maybe_timed(bracket == 7, marks, "moe_prefill_shared",
+                                 {0, x16.uav, 0, E, L.sh_gu16.srv, 0, E, sh_a.uav, 0, n, L.SF, bits(L.sh_unscale[0]),
+                                  bits(L.sh_unscale[1]), L.SF},
+                                 L.SF / 64, tt);
+            dispatch_maybe_timed(bracket == 8, marks, "moe_prefill_shared",
+                                 {1, sh_a.uav, 0, L.SF, L.sh_down16.srv, 0, L.SF, sh_o.uav, 0, n, 0,
+                                  bits(L.sh_unscale[2]), 0, E},
+                                 E / 128, tt);
+        }
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
                              {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u, res_uav,
-                              res_off},
+                              res_off, L.SF ? 1u : 0u, L.SF ? sh_o.uav : 0u, 0, x_uav, x_off,
+                              L.SF ? L.sh_gate.srv : 0u},
                              (E + 1023) / 1024,
                              n);
     }

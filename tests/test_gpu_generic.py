@@ -111,3 +111,15 @@ def test_prefill_refuses_fp16_overflowing_scales_any_type():
             eng.forward(0, synth.make_tokens(152, 4, layer.E), PATH_PREFILL)
     finally:
         eng.close()
+
+
+def test_prefill_path_with_shared_expert(oracle_mod):
+    """The prefill path's shared expert (moe_prefill_shared gate/up and down on binary16 copies of
+    the bf16 weights, the gate dot in moe_prefill_combine) on the mixed-quant configuration (SF
+    1024) at 512 tokens and a ragged 37, and on a uniform TQ2_T layer with SF 256."""
+    from gyrodx.engine import PATH_PREFILL
+    mixed = synth.make_layer(91, mixed_types=True, SF=1024)
+    check(oracle_mod, mixed, synth.make_tokens(161, 512, mixed.E), PATH_PREFILL, "prefill mixed + shared n=512")
+    check(oracle_mod, mixed, synth.make_tokens(162, 37, mixed.E), PATH_PREFILL, "prefill mixed + shared n=37")
+    tq2 = synth.make_layer(163, E=1024, F=256, n_expert=32, n_used=8, SF=256)
+    check(oracle_mod, tq2, synth.make_tokens(164, 100, tq2.E), PATH_PREFILL, "prefill TQ2_T + shared n=100")
