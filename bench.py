@@ -297,7 +297,7 @@ def mixed_bench(args):
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     from gyrodx import synth
-    from gyrodx.engine import PATH_DECODE, PATH_GENERIC, Engine
+    from gyrodx.engine import PATH_DECODE, PATH_PREFILL, Engine
 
     layer = synth.make_layer(args.seed + 50, mixed_types=True, SF=SHARED_F)
     copies = args.copies
@@ -324,17 +324,27 @@ def mixed_bench(args):
                      "tok_s": round(1.0 / step_s, 1), "us_per_token": round(step_s * 1e6, 2),
                      "bytes_per_token": int(per_tok), "hbm_gbs": round(per_tok / step_s / 1e9, 1),
                      "roofline": {"bound": "hbm", "frac": round(per_tok / step_s / 1e9 / HBM_PEAK_GBS, 4)}}
-    # 512-token prefill.
-    xp = synth.make_tokens(args.seed + 52, 512 * 4, bf16=True)
+    # 512-token prefill on the prefill path (type-generic grouped GEMMs, shared expert GEMMs).
+    calls = 8
+    xp = synth.make_tokens(args.seed + 52, 512 * calls, bf16=True)
     eng.set_tokens(xp)
-    eng.run(PATH_GENERIC, 512, 1, ids, first=0)
-    dev_ms, wall_ms, _ = eng.run(PATH_GENERIC, 512, 4, ids, first=0)
+    eng.run(PATH_PREFILL, 512, 2, ids, first=0)
+    dev_ms, wall_ms, _ = eng.run(PATH_PREFILL, 512, calls, ids, first=0)
     pout = eng.read_outputs(512)
-    call_s = wall_ms / 4 * 1e-3
+    us = {}
+    for name, br in (("moe_prefill_router", 1), ("moe_prefill_topk", 4), ("moe_prefill_sort", 5),
+                     ("moe_prefill_gu_x", 2), ("moe_prefill_down_x", 3), ("moe_prefill_shared gate/up", 7),
+                     ("moe_prefill_shared down", 8), ("moe_prefill_combine", 6)):
+        us[name] = round(eng.run(PATH_PREFILL, 512, calls, ids, bracket=br, first=0)[2], 3)
+    call_s = wall_ms / calls * 1e-3
+    dev_s = dev_ms / calls * 1e-3
     flops = 512 * (LAYER_FLOPS_PER_TOKEN + 3 * 2 * E * SHARED_F)
-    res["prefill"] = {"path": "generic", "tokens": 512, "tok_s": round(512 / call_s, 1), "us_per_call": round(call_s * 1e6, 2),
-                      "flops_per_call": flops, "tflops": round(flops / call_s / 1e12, 2),
-                      "roofline": {"bound": "mfma", "frac": round(flops / call_s / 1e12 / MFMA_PEAK_TFLOPS, 4)}}
+    res["prefill"] = {"path": "prefill (router, top-k, sort, moe_prefill_gu_x, moe_prefill_down_x, "
+                              "moe_prefill_shared x2, combine)",
+                      "tokens": 512, "calls": calls, "tok_s": round(512 / call_s, 1),
+                      "us_per_call": round(call_s * 1e6, 2), "device_us_per_call": round(dev_s * 1e6, 2),
+                      "kernel_us": us, "flops_per_call": flops, "tflops": round(flops / dev_s / 1e12, 2),
+                      "roofline": {"bound": "mfma", "frac": round(flops / dev_s / 1e12 / MFMA_PEAK_TFLOPS, 4)}}
     eng.close()
     if not args.no_cpu:
         threads = cpu_threads()

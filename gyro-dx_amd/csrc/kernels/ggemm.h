@@ -62,6 +62,26 @@ __device__ __forceinline__ void gg_dma16(uint32_t lds, const void *gbase, uint32
                  : "memory", "m0");
 }
 
+// Start of a K block for a wave that issues `newer` loads per block (activation and weight):
+// at most the loads of the following block stay outstanding (none before the last block).
+// newer is 1, 2, 5 or 6 (0 or 4 activation loads, 1 or 2 weight loads), uniform per wave.
+__device__ __forceinline__ void gg_sync_block(uint32_t newer, bool last) {
+    if (last) {
+        gg_sync<0>();
+        return;
+    }
+    switch (newer) {
+        case 6: gg_sync<6>(); break;
+        case 5: gg_sync<5>(); break;
+        case 2: gg_sync<2>(); break;
+        default: gg_sync<1>(); break;
+    }
+}
+
+// Activation loads per block of wave w for a tile of nrb 32-row blocks: the waves whose 16 rows
+// lie in the tile's row blocks stage them (4 loads), the others none.
+__device__ __forceinline__ uint32_t gg_a_loads(uint32_t wave, uint32_t nrb) { return wave < 2u * nrb ? 4u : 0u; }
+
 __device__ __forceinline__ uint32_t gg_lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
@@ -211,26 +231,20 @@ struct GxState {
     const void *wb[2];                   // matrix of each of this wave's weight loads
     uint32_t roff[4], woff[2], wbb[2];   // per load: lane offset at block 0, block bytes
     uint32_t nwl;                        // weight loads per block of this wave (1 or 2)
+    uint32_t nal;                        // activation loads per block of this wave (0 or 4)
     uint32_t wave, m, h, nk;
     uint32_t wrow;                       // LDS byte offset (in a weight buffer) of this lane's row
 };
 
 // Start of K block kb: the wave's loads of block kb have landed once at most the loads of block
-// kb + 1 (4 activation loads and nwl weight loads) are outstanding.
-__device__ __forceinline__ void gx_sync(const GxState &t, uint32_t kb) {
-    if (kb + 1u < t.nk) {
-        if (t.nwl == 2u) gg_sync<6>();
-        else gg_sync<5>();
-    } else {
-        gg_sync<0>();
-    }
-}
+// kb + 1 (nal activation loads and nwl weight loads) are outstanding.
+__device__ __forceinline__ void gx_sync(const GxState &t, uint32_t kb) { gg_sync_block(t.nal + t.nwl, kb + 1u >= t.nk); }
 
-// Stages K block kb into buffer buf: the wave's 4 activation loads, then its weight loads w and
+// Stages K block kb into buffer buf: the wave's activation loads (if any), then its weight loads w and
 // (nwl == 2) w + 8 at LDS byte 1024 L of the weight buffer; block kb of a row starts at its
 // matrix row's byte (kb BB) & ~3.
 __device__ __forceinline__ void gx_stage(GxLds &sm, uint32_t buf, const GxState &t, uint32_t kb) {
-    gg_stage_a8(sm, buf, t.wave, t.xbase, t.roff, kb);
+    if (t.nal) gg_stage_a8(sm, buf, t.wave, t.xbase, t.roff, kb);
     const uint32_t base = gg_lds_addr(&sm.w[buf][0]);
     gg_dma16(base + t.wave * 1024u, t.wb[0], t.woff[0] + ((kb * t.wbb[0]) & ~3u));
     if (t.nwl == 2u) gg_dma16(base + (t.wave + 8u) * 1024u, t.wb[1], t.woff[1] + ((kb * t.wbb[1]) & ~3u));

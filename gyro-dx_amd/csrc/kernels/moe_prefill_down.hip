@@ -22,18 +22,14 @@
 struct DnState {
     const void *abase, *wbase;  // act16 rows; the layer's slot arena
     uint32_t roff[4], woff[2];
+    uint32_t nal;  // activation loads per block of this wave (0 or 4)
     uint32_t wave, m, h, sel, nk;
 };
 
 // Start of K block kb (as the gate/up kernel: 4 activation loads, plus 2 or 1 weight loads by
 // wave class, belong to the following block).
 __device__ __forceinline__ void dn_sync(const DnState &t, uint32_t kb) {
-    if (kb + 1u < t.nk) {
-        if (t.wave < 4u) gg_sync<6>();
-        else gg_sync<5>();
-    } else {
-        gg_sync<0>();
-    }
+    gg_sync_block(t.nal + (t.wave < 4u ? 2u : 1u), kb + 1u >= t.nk);
 }
 
 // K block kb from buffer BUF for NRB 32-row blocks (see gu_step of the gate/up kernel).
@@ -41,7 +37,7 @@ template <int BUF, int NRB>
 __device__ __forceinline__ void dn_step(GgLds &sm, const DnState &t, uint32_t kb, f32x16 (&acc)[NRB]) {
     dn_sync(t, kb);
     if (kb + 2u < t.nk) {
-        gg_stage_a8(sm, (BUF + 2) % 3, t.wave, t.abase, t.roff, kb + 2u);
+        if (t.nal) gg_stage_a8(sm, (BUF + 2) % 3, t.wave, t.abase, t.roff, kb + 2u);
         gg_stage_w8(sm, (BUF + 2) % 3, t.wave, t.wbase, t.woff, kb + 2u);
     }
     GgBlk cur;
@@ -135,10 +131,11 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_down, 512, 2) {
         t.woff[i] = e * a.c[7] + a.c[8] + (eb * 256u + q) * row_bytes + piece * 16u;
     }
     __syncthreads();  // codebook and slot numbers
-    gg_stage_a8(sm, 0, wave, t.abase, t.roff, 0);
+    t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
+    if (t.nal) gg_stage_a8(sm, 0, wave, t.abase, t.roff, 0);
     gg_stage_w8(sm, 0, wave, t.wbase, t.woff, 0);
     if (t.nk > 1u) {
-        gg_stage_a8(sm, 1, wave, t.abase, t.roff, 1);
+        if (t.nal) gg_stage_a8(sm, 1, wave, t.abase, t.roff, 1);
         gg_stage_w8(sm, 1, wave, t.wbase, t.woff, 1);
     }
     switch ((rows + 31u) >> 5) {

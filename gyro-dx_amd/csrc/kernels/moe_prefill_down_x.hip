@@ -72,6 +72,7 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_down_x, 512, 2) {
         t.woff[i] = (eb * 256u + r) * row_bytes + piece * 16u;
     }
     __syncthreads();  // codebook and slot numbers
+    t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
     gx_stage(sm, 0, t, 0);
     if (t.nk > 1u) gx_stage(sm, 1, t, 1);
     switch ((rows + 31u) >> 5) {

@@ -29,18 +29,14 @@
 struct GuState {
     const void *xbase, *wbase;  // activation rows; the layer's slot arena (expert bundles)
     uint32_t roff[4], woff[2];
+    uint32_t nal;  // activation loads per block of this wave (0 or 4)
     uint32_t wave, m, h, sel, nk, wq;  // wq: the staged weight row this lane decodes
 };
 
 // Start of K block kb: this wave's loads of block kb have landed once at most the loads of
 // block kb + 1 are outstanding (4 activation loads, plus 2 or 1 weight loads by wave class).
 __device__ __forceinline__ void gu_sync(const GuState &t, uint32_t kb) {
-    if (kb + 1u < t.nk) {
-        if (t.wave < 4u) gg_sync<6>();
-        else gg_sync<5>();
-    } else {
-        gg_sync<0>();
-    }
+    gg_sync_block(t.nal + (t.wave < 4u ? 2u : 1u), kb + 1u >= t.nk);
 }
 
 // K block kb from buffer BUF for NRB 32-row blocks; stages block kb + 2 into buffer
@@ -49,7 +45,7 @@ template <int BUF, int NRB>
 __device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb, f32x16 (&acc)[NRB]) {
     gu_sync(t, kb);
     if (kb + 2u < t.nk) {
-        gg_stage_a8(sm, (BUF + 2) % 3, t.wave, t.xbase, t.roff, kb + 2u);
+        if (t.nal) gg_stage_a8(sm, (BUF + 2) % 3, t.wave, t.xbase, t.roff, kb + 2u);
         gg_stage_w8(sm, (BUF + 2) % 3, t.wave, t.wbase, t.woff, kb + 2u);
     }
     GgBlk wc;
@@ -151,10 +147,11 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 2) {
         const uint32_t g = gg_w8_load(wave, i) * 64u + lane, q = g / 3u, piece = g - q * 3u;
         t.woff[i] = e * a.c[7] + (q >> 7) * proj_bytes + (fb * 128u + (q & 127u)) * row_bytes + piece * 16u;
     }
-    gg_stage_a8(sm, 0, wave, t.xbase, t.roff, 0);
+    t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
+    if (t.nal) gg_stage_a8(sm, 0, wave, t.xbase, t.roff, 0);
     gg_stage_w8(sm, 0, wave, t.wbase, t.woff, 0);
     if (t.nk > 1u) {
-        gg_stage_a8(sm, 1, wave, t.xbase, t.roff, 1);
+        if (t.nal) gg_stage_a8(sm, 1, wave, t.xbase, t.roff, 1);
         gg_stage_w8(sm, 1, wave, t.wbase, t.woff, 1);
     }
     switch ((rows + 31u) >> 5) {

@@ -85,6 +85,7 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu_x, 512, 2) {
         t.wbb[i] = bb;
         t.woff[i] = (fb * 128u + r) * ((E / 128u) * bb) + piece * 16u;
     }
+    t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
     gx_stage(sm, 0, t, 0);
     if (t.nk > 1u) gx_stage(sm, 1, t, 1);
     const uint32_t type = wave < 4u ? tg : tu;
