@@ -2,13 +2,13 @@
 //
 // Every wave computes the token's top-8 from the router logits (route_fast.h), so no separate
 // routing launch exists. A group of eight waves owns 64 rows of one projection (gate or up) of
-// one selected expert over one K-part of 8 Gyro blocks (1024 columns). All independent loads
-// are issued first: the logits, the codebook, the wave's 128 activations (binary16 pairs in
-// scalar registers); once routing names the expert, its rows stream from HBM with 16-byte
-// loads into LDS (69 words per row so that lane = row reads are bank-conflict free). Wave w
-// decodes block w of its row (32 trellis steps per lane) with two v_dot2_f32_f16 per step;
-// codebook pairs come from LDS; the eight partial sums are added in block order. Two groups
-// fit a CU, so every SIMD runs two waves.
+// one selected expert over one K-part of 8 Gyro blocks (1024 columns); lane l of wave w decodes
+// block l % 8 of row 8 w + l / 8 (32 trellis steps, two v_dot2_f32_f16 per step, codebook pairs
+// from LDS) and the 8-lane groups add their blocks with DPP ((b0 + b1) + (b2 + b3)) +
+// ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook and the
+// part's 1024 binary16 activations (both into LDS, one barrier, then each lane keeps its block's
+// 128 activations in registers). Once routing names the expert, every lane loads the 9 words of
+// its own block straight from HBM, so no further barrier is needed.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
@@ -17,90 +17,91 @@
 // 13 slot_stride 14 proj_bytes 15 codebook_srv 16 gu_uav 17 gu_off 18 E 19 F 20 n_tok.
 // Requires TQ2_T experts, E a multiple of 1024, n_expert <= 256, top-8 and F a multiple of 64.
 #include "gyro_fast.h"
+#include "fwht.h"
 #include "route_fast.h"
 
 #define GU_ROWS 64
-#define GU_ROW_WORDS 69  // 272 bytes of a part row + 4 bytes of padding
 #define GU_U 8
 
 GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint32_t rows[GU_ROWS * GU_ROW_WORDS];
-    __shared__ float red[8][GU_ROWS];
+    __shared__ uint4 xpart[128];  // the part's 1024 activations as binary16 pairs
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[18], F = a.c[19], n_tok = a.c[20];
     const uint32_t slot = blockIdx.z, t = slot / GU_U, k = slot - t * GU_U;
     const uint32_t parts = E / 1024u, proj = blockIdx.y / parts, part = blockIdx.y - proj * parts;
     const uint32_t row0 = blockIdx.x * GU_ROWS;
+    const uint32_t b = lane & 7u, r = wave * 8u + (lane >> 3);  // this lane's block and row
 
-    // Independent loads first.
+    // Independent loads first, all in flight together (global loads, which no LDS store orders).
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
-    const uint4 cbv = gd_buf<const uint4>(a, a.c[15])[tid];
-    const uint32_t xblk = __builtin_amdgcn_readfirstlane(part * 8u + wave);
-    cuint *x16 = as_const(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + xblk * 64u);
+    const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
+    const uint32_t xw = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + part * 512u)[tid];
+    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
+    // Chunk c (16 bytes) of block bx at position bx * 16 + (c + bx) % 16: the 8 blocks that a
+    // wave reads at one chunk index sit in 8 different bank groups.
+    const uint32_t bx = tid >> 6, cx = (tid >> 2) & 15u;
+    reinterpret_cast<uint32_t *>(xpart)[(bx * 16u + ((cx + bx) & 15u)) * 4u + (tid & 3u)] = xw;
+    __syncthreads();
     uint32_t xs[64];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) xs[j] = x16[j];
-
-    uint32_t ids[GU_U];
-    float wts[GU_U];
-    wave_route_fast<4, GU_U>(lv, NE, gd_bits_f32(a.c[4]), ids, wts);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && k == 0 && wave == 0 && lane < GU_U) {
-        uint32_t id = ids[0];
-        float w = wts[0];
-#pragma unroll
-        for (int j = 1; j < GU_U; ++j) {
-            id = lane == (uint32_t)j ? ids[j] : id;
-            w = lane == (uint32_t)j ? wts[j] : w;
-        }
-        gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * GU_U + lane] = id;
-        gd_buf<float>(a, a.c[7])[a.c[8] + t * GU_U + lane] = w;
+    for (int j = 0; j < 16; ++j) {
+        const uint4 v = xpart[b * 16u + ((j + b) & 15u)];
+        xs[4 * j] = v.x; xs[4 * j + 1] = v.y; xs[4 * j + 2] = v.z; xs[4 * j + 3] = v.w;
     }
-    uint32_t e = ids[0];
+
+    // Routing: this group needs the expert of rank k only, so it stops after round k; the one
+    // group that records the token's ids and weights runs all rounds and forms the weights once
+    // its own weight loads are in flight.
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
+    uint64_t key[4];
+    rf_init<4>(lv, NE, key);
+    uint32_t ids[GU_U], e = 0;
+    float top[GU_U];
 #pragma unroll
-    for (int j = 1; j < GU_U; ++j) e = k == (uint32_t)j ? ids[j] : e;
+    for (int j = 0; j < GU_U; ++j) {
+        if ((uint32_t)j <= k || writer) {  // uniform
+            ids[j] = rf_next<4>(key, top[j]);
+            if ((uint32_t)j == k) e = ids[j];
+        }
+    }
     e = e < NE ? e : NE - 1u;  // ids are always < NE for finite logits; never address past the layer
 
+    // Block b of row r of the part: 34 bytes at byte 34 b of the part (word aligned for even b),
+    // read as the 9 words from its 4-byte-aligned start.
     const uint64_t layer_base = (uint64_t)a.c[11] | ((uint64_t)a.c[12] << 32);
     const uint32_t row_bytes = E / 128u * 34u;
-    const uint8_t *base = reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)e * a.c[13] +
-                          (proj ? a.c[14] : 0u) + (uint64_t)row0 * row_bytes + part * 272u;
-    // 64 rows x 17 chunks of 16 bytes, three per thread (the last partly), all issued at once.
-    uint4 rv[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const uint32_t c = min(tid + 512u * j, GU_ROWS * 17u - 1u);
-        const uint32_t r = c / 17u, ch = c - r * 17u;
-        rv[j] = *reinterpret_cast<const uint4 *>(base + (size_t)r * row_bytes + ch * 16u);
-    }
-    book4[tid] = cbv;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const uint32_t c = tid + 512u * j;
-        if (c < GU_ROWS * 17u) {
-            const uint32_t r = c / 17u, ch = c - r * 17u;
-            uint32_t *dst = rows + r * GU_ROW_WORDS + ch * 4u;
-            dst[0] = rv[j].x; dst[1] = rv[j].y; dst[2] = rv[j].z; dst[3] = rv[j].w;
-        }
-    }
-    __syncthreads();
-
-    // Block `wave` of the part row: byte offset 34 * wave (word aligned for even waves).
-    const uint32_t *rw = rows + lane * GU_ROW_WORDS + (wave * 34u >> 2);
+    gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(
+        reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)e * a.c[13] + (proj ? a.c[14] : 0u) +
+        (uint64_t)(row0 + r) * row_bytes + part * 272u + ((b * 34u) & ~3u)));
     uint32_t d[9];
 #pragma unroll
-    for (int j = 0; j < 9; ++j) d[j] = rw[j];
+    for (int j = 0; j < 9; ++j) d[j] = w[j];
+    if (writer && wave == 0u) {
+        float wts[GU_U];
+        rf_weights<GU_U>(top, gd_bits_f32(a.c[4]), wts);
+        if (lane < GU_U) {
+            uint32_t id = ids[0];
+            float wv = wts[0];
+#pragma unroll
+            for (int j = 1; j < GU_U; ++j) {
+                id = lane == (uint32_t)j ? ids[j] : id;
+                wv = lane == (uint32_t)j ? wts[j] : wv;
+            }
+            gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * GU_U + lane] = id;
+            gd_buf<float>(a, a.c[7])[a.c[8] + t * GU_U + lane] = wv;
+        }
+    }
     float sc;
     uint32_t q[8];
-    tq2_unpack(d, (wave & 1u) != 0u, sc, q);
-    red[wave][lane] = sc * tq2_block_dot_h(q, reinterpret_cast<const uint32_t *>(book4), xs);
-    __syncthreads();
-    if (wave == 0) {
-        float v = red[0][lane];
-#pragma unroll
-        for (int w = 1; w < 8; ++w) v += red[w][lane];
+    tq2_unpack(d, (b & 1u) != 0u, sc, q);
+    float v = sc * tq2_block_dot_h(q, reinterpret_cast<const uint32_t *>(book4), xs);
+    v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
+    v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2
+    v = v + gd_dpp_f<0x104>(v);  // row_shl:4: + lane + 4 (read by lanes b < 4)
+    if (b == 0u) {
         const uint32_t n_slots = n_tok * GU_U;
-        gd_buf<float>(a, a.c[16])[a.c[17] + ((size_t)(part * n_slots + slot) * 2u + proj) * F + row0 + lane] = v;
+        gd_buf<float>(a, a.c[16])[a.c[17] + ((size_t)(part * n_slots + slot) * 2u + proj) * F + row0 + r] = v;
     }
 }

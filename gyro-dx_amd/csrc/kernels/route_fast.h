@@ -27,10 +27,11 @@ __device__ __forceinline__ float rf_unorder(uint32_t k) {
 template <int PER>
 __device__ __forceinline__ void rf_load(const float *__restrict__ logits, uint32_t NE, float v[PER]) {
     const uint32_t lane = threadIdx.x & 63u;
+    gd_guint *g = gd_global(reinterpret_cast<const uint32_t *>(logits));  // global_load: no LDS aliasing
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const uint32_t i = lane + 64u * j;
-        v[j] = logits[i < NE ? i : NE - 1u];
+        v[j] = gd_bits_f32(g[i < NE ? i : NE - 1u]);
     }
 }
 
@@ -52,14 +53,12 @@ __device__ __forceinline__ uint32_t rf_wave_reduce32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// Top-U of the logits loaded by rf_load. Returns ids and weights (uniform across the wave).
-// U is a compile-time count (the number of experts used per token).
-template <int PER, int U>
-__device__ __forceinline__ void wave_route_fast(const float v[PER], uint32_t NE, float scale, uint32_t ids[U],
-                                                float wts[U]) {
+// Round-by-round form of the selection, for callers that need only the first ranks (a decode
+// group needs the expert of its own slot, rank k) or want to overlap the weights with loads.
+// rf_init: the lane's candidate keys (logit order << 32 | ~index, 0 past NE), sorted.
+template <int PER>
+__device__ __forceinline__ void rf_init(const float v[PER], uint32_t NE, uint64_t key[PER]) {
     const uint32_t lane = threadIdx.x & 63u;
-    // Candidate keys (logit order << 32 | ~index), 0 for the slots past NE.
-    uint64_t key[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const uint32_t i = lane + 64u * j;
@@ -75,22 +74,29 @@ __device__ __forceinline__ void wave_route_fast(const float v[PER], uint32_t NE,
             key[b - 1] = hi;
             key[b] = lo;
         }
-    float top[U];
+}
+
+// rf_next: the next rank's expert id (uniform) and its logit; removes it from the candidates.
+template <int PER>
+__device__ __forceinline__ uint32_t rf_next(uint64_t key[PER], float &logit) {
+    const uint32_t h = (uint32_t)(key[0] >> 32), my = ~(uint32_t)key[0];
+    const uint32_t m = rf_wave_reduce32<true>(h);
+    const uint64_t at_max = __ballot(h == m);
+    uint32_t id;
+    if (__builtin_popcountll(at_max) == 1) id = (uint32_t)__builtin_amdgcn_readlane((int)my, (int)__builtin_ctzll(at_max));
+    else id = rf_wave_reduce32<false>(h == m ? my : 0xffffffffu);
+    logit = rf_unorder(m);
+    const bool mine = my == id;
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-        const uint32_t h = (uint32_t)(key[0] >> 32), my = ~(uint32_t)key[0];
-        const uint32_t m = rf_wave_reduce32<true>(h);
-        const uint64_t at_max = __ballot(h == m);
-        uint32_t id;
-        if (__builtin_popcountll(at_max) == 1) id = (uint32_t)__builtin_amdgcn_readlane((int)my, (int)__builtin_ctzll(at_max));
-        else id = rf_wave_reduce32<false>(h == m ? my : 0xffffffffu);
-        ids[k] = id;
-        top[k] = rf_unorder(m);
-        const bool mine = my == id;
-#pragma unroll
-        for (int j = 0; j + 1 < PER; ++j) key[j] = mine ? key[j + 1] : key[j];
-        key[PER - 1] = mine ? 0ull : key[PER - 1];
-    }
+    for (int j = 0; j + 1 < PER; ++j) key[j] = mine ? key[j + 1] : key[j];
+    key[PER - 1] = mine ? 0ull : key[PER - 1];
+    return id;
+}
+
+// rf_weights: w_k = exp(l_k - l_0) / sum_j exp(l_j - l_0) over the selected logits (descending),
+// times the layer's scale unless it is 0 or 1.
+template <int U>
+__device__ __forceinline__ void rf_weights(const float top[U], float scale, float wts[U]) {
     float total = 0.f;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
@@ -104,4 +110,17 @@ __device__ __forceinline__ void wave_route_fast(const float v[PER], uint32_t NE,
         if (scale != 0.f && scale != 1.f) w *= scale;
         wts[k] = w;
     }
+}
+
+// Top-U of the logits loaded by rf_load. Returns ids and weights (uniform across the wave).
+// U is a compile-time count (the number of experts used per token).
+template <int PER, int U>
+__device__ __forceinline__ void wave_route_fast(const float v[PER], uint32_t NE, float scale, uint32_t ids[U],
+                                                float wts[U]) {
+    uint64_t key[PER];
+    rf_init<PER>(v, NE, key);
+    float top[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) ids[k] = rf_next<PER>(key, top[k]);
+    rf_weights<U>(top, scale, wts);
 }
