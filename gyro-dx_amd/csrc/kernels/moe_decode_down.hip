@@ -29,7 +29,7 @@
 #define DN_F 512
 #define DN_NB (DN_F / 128)
 #define DN_ROW_BYTES (DN_NB * 34)
-#define DN_BLOCK_STRIDE 132  // floats per 128-block in LDS (bank spread for the 8 x streams)
+#define DN_BLOCK_STRIDE 132  // floats per 128-block in LDS (bank spread)
 
 
 GD_PIPELINE_NAMED(moe_decode_down, 512) {

@@ -1,30 +1,32 @@
 // Decode path for layers whose experts and projections mix Gyro types, step 2: routing and the
 // fused dequant-GEMV of the gate and up rows (src/engine.zig:567-602 with dotRow per matrix,
 // src/kernels.zig:201-210), structured as moe_decode_gu: a group of eight waves owns 64 rows of
-// one projection of one selected expert over one K-part of 8 Gyro blocks (1024 columns).
-// The expert's rows and their type come from the layer's expert table (ExpertDesc); the type is
-// uniform per group, so one instantiation of the block decoder runs (gyro_fast.h). The rows
-// stream into LDS with 16-byte loads (2 bb + 1 words per row for blocks of bb bytes, so that
-// lane = row reads are bank-conflict free); wave w decodes block w of its row.
+// one projection of one selected expert over one K-part of 8 Gyro blocks (1024 columns); lane l
+// of wave w decodes block l % 8 of row 8 w + l / 8 and the 8-lane groups add their blocks with
+// DPP. The expert's rows and their type come from the layer's expert table (ExpertDesc); the
+// type is uniform per group, so one instantiation of the block decoder runs (gyro_fast.h), and
+// every lane loads the NW + 1 words of its own block (from the block's 4-byte-aligned start)
+// straight from HBM.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 weights_uav 8 weights_off 9 xh16_uav 10 xh16_off (words) 11 xtab_srv
-// 12 codebook_srv 13 gu_uav 14 gu_off 15 E 16 F 17 n_tok.
+// 6 ids_off 7 w_uav 8 w_off 9 xh16_uav 10 xh16_off (words) 11 xtab_srv 12 codebook_srv 13 gu_uav
+// 14 gu_off 15 E 16 F 17 n_tok.
 // Requires E a multiple of 1024, n_expert <= 256, top-8 and F a multiple of 64.
 #include "gyro_fast.h"
+#include "fwht.h"
 #include "route_fast.h"
 
 #define GX_ROWS 64
-#define GX_MAX_ROW_WORDS 117  // 8 blocks of 58 bytes + 1 word of padding
 #define GX_U 8
 
+// Block b of the part row at `row` (bytes): its NW + 1 words from byte (b BB) & ~3, decoded
+// against the lane's 128 activations.
 template <int ID>
-__device__ __forceinline__ float gx_block(const uint32_t *row, uint32_t wave, const uint32_t *book,
-                                          const uint32_t xs[64]) {
+__device__ __forceinline__ float gx_block(const uint8_t *row, uint32_t b, const uint32_t *book, const uint32_t xs[64]) {
     constexpr int BB = GyroT<ID>::BB, NW = gyro_nw<ID>();
-    const uint32_t off = wave * BB;  // even
-    const uint32_t *rw = row + (off >> 2);
+    const uint32_t off = b * BB;  // even
+    gd_guint *rw = gd_global(reinterpret_cast<const uint32_t *>(row + (off & ~3u)));
     uint32_t d[NW + 1];
 #pragma unroll
     for (int j = 0; j <= NW; ++j) d[j] = rw[j];
@@ -36,42 +38,61 @@ __device__ __forceinline__ float gx_block(const uint32_t *row, uint32_t wave, co
 
 GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint32_t rows[GX_ROWS * GX_MAX_ROW_WORDS];
-    __shared__ float red[8][GX_ROWS];
+    __shared__ uint4 xpart[128];  // the part's 1024 activations as binary16 pairs, bank-rotated
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[15], F = a.c[16], n_tok = a.c[17];
     const uint32_t slot = blockIdx.z, t = slot / GX_U, k = slot - t * GX_U;
     const uint32_t parts = E / 1024u, proj = blockIdx.y / parts, part = blockIdx.y - proj * parts;
     const uint32_t row0 = blockIdx.x * GX_ROWS;
+    const uint32_t b = lane & 7u, r = wave * 8u + (lane >> 3);  // this lane's block and row
 
-    // Independent loads first.
+    // Independent loads first, all in flight together (global loads, which no LDS store orders).
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
-    const uint4 cbv = gd_buf<const uint4>(a, a.c[12])[tid];
-    const uint32_t xblk = __builtin_amdgcn_readfirstlane(part * 8u + wave);
-    cuint *x16 = as_const(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + xblk * 64u);
+    const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[12]))[tid];
+    const uint32_t xw = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + part * 512u)[tid];
+    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
+    // Chunk c (16 bytes) of block bx at position bx * 16 + (c + bx) % 16: the 8 blocks that a
+    // wave reads at one chunk index sit in 8 different bank groups.
+    const uint32_t bx = tid >> 6, cx = (tid >> 2) & 15u;
+    reinterpret_cast<uint32_t *>(xpart)[(bx * 16u + ((cx + bx) & 15u)) * 4u + (tid & 3u)] = xw;
+    __syncthreads();
     uint32_t xs[64];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) xs[j] = x16[j];
-
-    uint32_t ids[GX_U];
-    float wts[GX_U];
-    wave_route_fast<4, GX_U>(lv, NE, gd_bits_f32(a.c[4]), ids, wts);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && k == 0 && wave == 0 && lane < GX_U) {
-        uint32_t id = ids[0];
-        float w = wts[0];
-#pragma unroll
-        for (int j = 1; j < GX_U; ++j) {
-            id = lane == (uint32_t)j ? ids[j] : id;
-            w = lane == (uint32_t)j ? wts[j] : w;
-        }
-        gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * GX_U + lane] = id;
-        gd_buf<float>(a, a.c[7])[a.c[8] + t * GX_U + lane] = w;
+    for (int j = 0; j < 16; ++j) {
+        const uint4 v = xpart[b * 16u + ((j + b) & 15u)];
+        xs[4 * j] = v.x; xs[4 * j + 1] = v.y; xs[4 * j + 2] = v.z; xs[4 * j + 3] = v.w;
     }
-    uint32_t e = ids[0];
+
+    // Routing to this group's rank k only; the recording group runs every round (moe_decode_gu).
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
+    uint64_t key[4];
+    rf_init<4>(lv, NE, key);
+    uint32_t ids[GX_U], e = 0;
+    float top[GX_U];
 #pragma unroll
-    for (int j = 1; j < GX_U; ++j) e = k == (uint32_t)j ? ids[j] : e;
+    for (int j = 0; j < GX_U; ++j) {
+        if ((uint32_t)j <= k || writer) {  // uniform
+            ids[j] = rf_next<4>(key, top[j]);
+            if ((uint32_t)j == k) e = ids[j];
+        }
+    }
     e = __builtin_amdgcn_readfirstlane(e < NE ? e : NE - 1u);
+    if (writer && wave == 0u) {
+        float wts[GX_U];
+        rf_weights<GX_U>(top, gd_bits_f32(a.c[4]), wts);
+        if (lane < GX_U) {
+            uint32_t id = ids[0];
+            float wv = wts[0];
+#pragma unroll
+            for (int j = 1; j < GX_U; ++j) {
+                id = lane == (uint32_t)j ? ids[j] : id;
+                wv = lane == (uint32_t)j ? wts[j] : wv;
+            }
+            gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * GX_U + lane] = id;
+            gd_buf<float>(a, a.c[7])[a.c[8] + t * GX_U + lane] = wv;
+        }
+    }
 
     const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[11]);
     const uint32_t types = __builtin_amdgcn_readfirstlane(xt[e].types);
@@ -79,41 +100,18 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     GyroType gt;
     if (!gd_type(type_id, gt)) return;  // uniform: the host admits only the eight types
     const uint64_t addr = proj ? xt[e].up : xt[e].gate;
-    const uint32_t bb = gt.block_bytes, row_bytes = E / 128u * bb, chunks = bb / 2u, stride = 2u * bb + 1u;
-    const uint8_t *base = reinterpret_cast<const uint8_t *>(addr) + (uint64_t)row0 * row_bytes + part * 8u * bb;
-    // 64 rows x bb / 2 chunks of 16 bytes, up to four per thread, all issued at once.
-    uint4 rv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = min(tid + 512u * j, GX_ROWS * chunks - 1u);
-        const uint32_t r = c / chunks, ch = c - r * chunks;
-        rv[j] = *reinterpret_cast<const uint4 *>(base + (size_t)r * row_bytes + ch * 16u);
-    }
-    book4[tid] = cbv;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = tid + 512u * j;
-        if (c < GX_ROWS * chunks) {
-            const uint32_t r = c / chunks, ch = c - r * chunks;
-            uint32_t *dst = rows + r * stride + ch * 4u;
-            dst[0] = rv[j].x; dst[1] = rv[j].y; dst[2] = rv[j].z; dst[3] = rv[j].w;
-        }
-    }
-    __syncthreads();
-
-    const uint32_t *row = rows + lane * stride;
+    const uint32_t bb = gt.block_bytes, row_bytes = E / 128u * bb;
+    const uint8_t *row = reinterpret_cast<const uint8_t *>(addr) + (uint64_t)(row0 + r) * row_bytes + part * 8u * bb;
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
     float v = 0.f;
-#define GX_CASE(ID) v = gx_block<ID>(row, wave, book, xs)
+#define GX_CASE(ID) v = gx_block<ID>(row, b, book, xs)
     GYRO_TYPE_SWITCH(type_id, GX_CASE)
 #undef GX_CASE
-    red[wave][lane] = v;
-    __syncthreads();
-    if (wave == 0) {
-        float s = red[0][lane];
-#pragma unroll
-        for (int w = 1; w < 8; ++w) s += red[w][lane];
+    v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
+    v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2
+    v = v + gd_dpp_f<0x104>(v);  // row_shl:4: + lane + 4 (read by lanes b < 4)
+    if (b == 0u) {
         const uint32_t n_slots = n_tok * GX_U;
-        gd_buf<float>(a, a.c[13])[a.c[14] + ((size_t)(part * n_slots + slot) * 2u + proj) * F + row0 + lane] = s;
+        gd_buf<float>(a, a.c[13])[a.c[14] + ((size_t)(part * n_slots + slot) * 2u + proj) * F + row0 + r] = v;
     }
 }

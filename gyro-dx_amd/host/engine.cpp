@@ -596,7 +596,7 @@ class Engine {
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
                               st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, sh_h.uav, 0,
                               sh_g.uav, 0, L.SF ? L.sh_down.srv : 0u, L.SF},
-                             E / 8, n);
+                             E / 16, n);
     }
 
     // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;
