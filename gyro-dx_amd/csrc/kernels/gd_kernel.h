@@ -109,6 +109,22 @@ __device__ __forceinline__ float gd_wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+// Wave64 sum with DPP (no LDS traffic, so no wait on outstanding loads): row prefix sums by
+// row_shr 1, 2, 4, 8, then row_bcast 15 and 31 carry rows 0..2 into lane 63, which every lane
+// reads (a scalar). A fixed order: the same inputs give the same sum.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float gd_dpp_add_step(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false));
+}
+__device__ __forceinline__ float gd_wave_sum_dpp(float v) {
+    v = gd_dpp_add_step<0x111, 0xf>(v);  // row_shr:1
+    v = gd_dpp_add_step<0x112, 0xf>(v);  // row_shr:2
+    v = gd_dpp_add_step<0x114, 0xf>(v);  // row_shr:4
+    v = gd_dpp_add_step<0x118, 0xf>(v);  // row_shr:8
+    v = gd_dpp_add_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = gd_dpp_add_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 
 // Global-address-space views of table buffers. Loads through them are global_load, counted by
 // vmcnt only (a flat load also counts against lgkmcnt), so an LDS-only wait leaves them in flight.

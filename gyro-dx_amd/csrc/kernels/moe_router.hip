@@ -15,57 +15,52 @@
 // without weight, 2: with weight; zero when the caller passes 16 constants) 17 norm_w_srv
 // 18 norm_w_off 19 eps (fp32 bits) 20 shared rows (2 SF; 0: no shared expert) 21 sh_w_srv (bf16
 // [2 SF][E]: gate rows then up rows) 22 sh_h_uav (fp32 [n][2 SF]) 23 sh_gate_srv (fp32 [E])
-// 24 sh_g_uav (fp32 [n]). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 16 + 1
-// further groups after the max(n_expert, E / 128) above: each of the first computes 16 bf16 rows
-// (4 per wave) of W_sg x and W_su x on the unrotated input, the last the gate dot g . x. The
+// 24 sh_g_uav (fp32 [n]). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 4 + 1
+// further groups after the max(n_expert, E / 128) above: each of the first computes 4 bf16 rows
+// (one per wave) of W_sg x and W_su x on the unrotated input, the last the gate dot g . x. The
 // shared groups require E <= 2048.
+// Every load is a global load issued ahead of its use, and the wave sums run on DPP.
 #include "fwht.h"
 
 #define ROUTER_MAX_TOK 8
 #define ROUTER_MAX_E 4096
 
-#define SH_ROWS_PER_GROUP 16
+#define SH_ROWS_PER_GROUP 4
 #define SH_MAX_E 2048  // hidden width covered by the fused shared-expert rows
 
-// Shared expert rows of group sg: wave w takes rows 16 sg + 4 w .. + 3 of W_sh (bf16, E columns);
-// lane l covers columns 8 l + 512 m (m < E / 512) of every row.
+// Shared expert row 4 sg + w of W_sh (bf16, E columns) on wave w; lane l covers columns
+// 8 l + 512 m (m < E / 512).
+__device__ __forceinline__ float4 rt_f4(gd_u32x4 v) {
+    return make_float4(gd_bits_f32(v[0]), gd_bits_f32(v[1]), gd_bits_f32(v[2]), gd_bits_f32(v[3]));
+}
 __device__ __forceinline__ void router_shared_rows(const GdArgs &a, uint32_t sg, uint32_t n_tok, uint32_t E) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t rows = a.c[20], r0 = sg * SH_ROWS_PER_GROUP + wave * 4u;
-    const uint16_t *Wsh = gd_buf<const uint16_t>(a, a.c[21]);
-    const float *X = gd_buf<const float>(a, a.c[0]);
+    const uint32_t rows = a.c[20], r = sg * SH_ROWS_PER_GROUP + wave;
+    if (r >= rows) return;  // uniform per wave; no barrier follows
+    const uint32_t *Wsh = gd_buf<const uint32_t>(a, a.c[21]) + ((size_t)r * E + 8u * lane) / 2u;
+    const uint32_t *X = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1] + 8u * lane;
     float *H = gd_buf<float>(a, a.c[22]);
     constexpr int MM = SH_MAX_E / 512;  // column chunks
-    uint4 w[4][MM];
+    gd_u32x4 w[MM];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int m = 0; m < MM; ++m)
-            if (r0 + (uint32_t)i < rows && 512u * m < E)
-                w[i][m] = *reinterpret_cast<const uint4 *>(Wsh + (size_t)(r0 + i) * E + 8u * lane + 512u * m);
+    for (int m = 0; m < MM; ++m)
+        if (512u * m < E) w[m] = *gd_global4(Wsh + 256u * m);
     for (uint32_t t = 0; t < n_tok; ++t) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        float acc = 0.f;
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
             if (512u * m >= E) break;
-            const float4 *xp = reinterpret_cast<const float4 *>(X + a.c[1] + t * a.c[2] + 8u * lane + 512u * m);
-            const float4 x0 = xp[0], x1 = xp[1];
+            gd_gu32x4 *xp = gd_global4(X + t * a.c[2] + 512u * m);
+            const float4 x0 = rt_f4(xp[0]), x1 = rt_f4(xp[1]);
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t ww[4] = {w[i][m].x, w[i][m].y, w[i][m].z, w[i][m].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    acc[i] += gd_bits_f32(ww[q] << 16) * xv[2 * q];
-                    acc[i] += gd_bits_f32(ww[q] & 0xffff0000u) * xv[2 * q + 1];
-                }
+            for (int q = 0; q < 4; ++q) {
+                acc += gd_bits_f32(w[m][q] << 16) * xv[2 * q];
+                acc += gd_bits_f32(w[m][q] & 0xffff0000u) * xv[2 * q + 1];
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float v = gd_wave_sum(acc[i]);
-            if (lane == 0 && r0 + (uint32_t)i < rows) H[t * rows + r0 + i] = v;
-        }
+        const float v = gd_wave_sum_dpp(acc);
+        if (lane == 0) H[t * rows + r] = v;
     }
 }
 
@@ -85,11 +80,12 @@ GD_PIPELINE_NAMED(moe_router, 256) {
                 router_shared_rows(a, sg, n_tok, E);
             } else {
                 // The gate dot g . x (fp32 row), one wave per token.
-                const float *G = gd_buf<const float>(a, a.c[23]);
+                gd_guint *G = gd_global(gd_buf<const uint32_t>(a, a.c[23]));
+                gd_guint *XG = gd_global(reinterpret_cast<const uint32_t *>(X));
                 for (uint32_t t = wave; t < n_tok; t += 4u) {
                     float acc = 0.f;
-                    for (uint32_t i = lane; i < E; i += 64u) acc += G[i] * X[x_off + t * x_stride + i];
-                    acc = gd_wave_sum(acc);
+                    for (uint32_t i = lane; i < E; i += 64u) acc += gd_bits_f32(G[i]) * gd_bits_f32(XG[x_off + t * x_stride + i]);
+                    acc = gd_wave_sum_dpp(acc);
                     if (lane == 0) gd_buf<float>(a, a.c[24])[t] = acc;
                 }
             }
@@ -98,46 +94,54 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     }
     const float *NW = norm == 2u ? gd_buf<const float>(a, a.c[17]) + a.c[18] : nullptr;
     const bool rotate_here = wave == 0 && row < E / 128u;
-
-    // Rotation inputs first (independent of the router row).
-    float rx[ROUTER_MAX_TOK][2], rs[2] = {1.f, 1.f};
-    const uint32_t ri = row * 128u + 2u * lane;
+    // Rotation inputs first (independent of the router row): in pass p, lane l of wave 0 holds
+    // values 8 (l % 16) .. + 7 of block `row` of token 4 p + l / 16.
+    const uint32_t l16 = lane & 15u, ri = row * 128u + l16 * 8u;
     const bool has_signs = a.c[12] != 0xffffffffu;
+    float rx[2][8], rs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rs[j] = 1.f;
     if (rotate_here) {
         if (has_signs) {
-            const float2 sv = *reinterpret_cast<const float2 *>(gd_buf<const float>(a, a.c[12]) + a.c[13] + ri);
-            rs[0] = sv.x;
-            rs[1] = sv.y;
+            gd_gu32x4 *sv = gd_global4(gd_buf<const uint32_t>(a, a.c[12]) + a.c[13] + ri);
+            const float4 s0 = rt_f4(sv[0]), s1 = rt_f4(sv[1]);
+            rs[0] = s0.x; rs[1] = s0.y; rs[2] = s0.z; rs[3] = s0.w;
+            rs[4] = s1.x; rs[5] = s1.y; rs[6] = s1.z; rs[7] = s1.w;
         }
         if (norm == 2u) {
-            const float2 nv = *reinterpret_cast<const float2 *>(NW + ri);
-            rs[0] *= nv.x;
-            rs[1] *= nv.y;
+            gd_gu32x4 *nv = gd_global4(reinterpret_cast<const uint32_t *>(NW) + ri);
+            const float4 n0 = rt_f4(nv[0]), n1 = rt_f4(nv[1]);
+            rs[0] *= n0.x; rs[1] *= n0.y; rs[2] *= n0.z; rs[3] *= n0.w;
+            rs[4] *= n1.x; rs[5] *= n1.y; rs[6] *= n1.z; rs[7] *= n1.w;
         }
 #pragma unroll
-        for (int t = 0; t < ROUTER_MAX_TOK; ++t)
-            if ((uint32_t)t < n_tok) {
-                const float2 xv = *reinterpret_cast<const float2 *>(X + x_off + t * x_stride + ri);
-                rx[t][0] = xv.x;
-                rx[t][1] = xv.y;
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t t = 4u * (uint32_t)p + (lane >> 4);
+            if (t < n_tok) {
+                gd_gu32x4 *xv = gd_global4(reinterpret_cast<const uint32_t *>(X) + x_off + t * x_stride + ri);
+                const float4 x0 = rt_f4(xv[0]), x1 = rt_f4(xv[1]);
+                rx[p][0] = x0.x; rx[p][1] = x0.y; rx[p][2] = x0.z; rx[p][3] = x0.w;
+                rx[p][4] = x1.x; rx[p][5] = x1.y; rx[p][6] = x1.z; rx[p][7] = x1.w;
             }
+        }
     }
     // Groups with a router row compute its dot products; with the norm, every group that has a
     // router row or a rotation block also needs the tokens' sums of squares.
     const bool dot = row < NE;  // uniform per group
     if (dot || (norm && row < E / 128u)) {
-        const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5] + (size_t)(dot ? row : 0u) * E;
+        const uint32_t *W = gd_buf<const uint32_t>(a, a.c[4]) + a.c[5] + (size_t)(dot ? row : 0u) * E;
         constexpr int PER = ROUTER_MAX_E / 1024;
         float4 w[PER];
 #pragma unroll
         for (int j = 0; j < PER; ++j)
             if (dot && tid * 4u + 1024u * j < E) {
-                w[j] = *reinterpret_cast<const float4 *>(W + tid * 4u + 1024u * j);
+                w[j] = rt_f4(*gd_global4(W + tid * 4u + 1024u * j));
                 if (norm == 2u) {
-                    const float4 g = *reinterpret_cast<const float4 *>(NW + tid * 4u + 1024u * j);
+                    const float4 g = rt_f4(*gd_global4(reinterpret_cast<const uint32_t *>(NW) + tid * 4u + 1024u * j));
                     w[j] = make_float4(w[j].x * g.x, w[j].y * g.y, w[j].z * g.z, w[j].w * g.w);
                 }
             }
+        const uint32_t *XU = reinterpret_cast<const uint32_t *>(X) + x_off + tid * 4u;
 #pragma unroll
         for (int t = 0; t < ROUTER_MAX_TOK; ++t) {
             if ((uint32_t)t < n_tok) {
@@ -145,16 +149,16 @@ GD_PIPELINE_NAMED(moe_router, 256) {
 #pragma unroll
                 for (int j = 0; j < PER; ++j)
                     if (tid * 4u + 1024u * j < E) {
-                        const float4 v = *reinterpret_cast<const float4 *>(X + x_off + t * x_stride + tid * 4u + 1024u * j);
+                        const float4 v = rt_f4(*gd_global4(XU + t * x_stride + 1024u * j));
                         if (dot) acc += (w[j].x * v.x + w[j].y * v.y) + (w[j].z * v.z + w[j].w * v.w);
                         if (norm) ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
                     }
                 if (dot) {
-                    const float s = gd_wave_sum(acc);
+                    const float s = gd_wave_sum_dpp(acc);
                     if (lane == 0) red[wave][t] = s;
                 }
                 if (norm) {
-                    const float q = gd_wave_sum(ss);
+                    const float q = gd_wave_sum_dpp(ss);
                     if (lane == 0) reds[wave][t] = q;
                 }
             }
@@ -173,27 +177,71 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     if (rotate_here) {
         uint32_t *XH = gd_buf<uint32_t>(a, a.c[14]) + a.c[15];
 #pragma unroll
-        for (int t = 0; t < ROUTER_MAX_TOK; ++t) {
-            if ((uint32_t)t >= n_tok) break;
-            float x0 = rx[t][0], x1 = rx[t][1];
+        for (int p = 0; p < 2; ++p) {
+            if (4u * (uint32_t)p >= n_tok) break;  // uniform
+            const uint32_t t = 4u * (uint32_t)p + (lane >> 4);  // the same for a 16-lane row
+            const bool tv = t < n_tok;
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = tv ? rx[p][j] : 0.f;
             if (norm) {
-                const float q = (reds[0][t] + reds[1][t]) + (reds[2][t] + reds[3][t]);
+                const uint32_t tq = tv ? t : 0u;
+                const float q = (reds[0][tq] + reds[1][tq]) + (reds[2][tq] + reds[3][tq]);
                 const float sc = 1.0f / sqrtf(q / (float)E + gd_bits_f32(a.c[19]));
-                x0 *= sc;
-                x1 *= sc;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] *= sc;
             }
             if (has_signs || norm == 2u) {
-                x0 *= rs[0];
-                x1 *= rs[1];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] *= rs[j];
             }
             if (has_signs) {
-                gd_fwht128_wave(x0, x1);
-                x0 *= GD_INV_SQRT128;
-                x1 *= GD_INV_SQRT128;
+                // Widths 1, 2, 4 in registers, then 8, 16, 32, 64 with lanes l16 ^ 1, ^ 2, ^ 4,
+                // ^ 8 of the 16-lane row (the stage order of src/gyro.zig:152-172).
+#pragma unroll
+                for (int w = 1; w < 8; w <<= 1)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (!(j & w)) {
+                            const float lo = v[j], hi = v[j + w];
+                            v[j] = lo + hi;
+                            v[j + w] = lo - hi;
+                        }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p1 = gd_dpp_f<0xB1>(v[j]);  // quad_perm [1,0,3,2]
+                    v[j] = (l16 & 1u) ? p1 - v[j] : v[j] + p1;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p2 = gd_dpp_f<0x4E>(v[j]);  // quad_perm [2,3,0,1]
+                    v[j] = (l16 & 2u) ? p2 - v[j] : v[j] + p2;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float up4 = gd_dpp_f<0x104>(v[j]);  // row_shl:4, lane + 4
+                    const float dn4 = gd_dpp_f<0x114>(v[j]);  // row_shr:4, lane - 4
+                    v[j] = (l16 & 4u) ? dn4 - v[j] : v[j] + up4;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float up8 = gd_dpp_f<0x108>(v[j]);  // row_shl:8, lane + 8
+                    const float dn8 = gd_dpp_f<0x118>(v[j]);  // row_shr:8, lane - 8
+                    v[j] = (l16 & 8u) ? dn8 - v[j] : v[j] + up8;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] *= GD_INV_SQRT128;
             }
-            const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)x0);
-            const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)x1);
-            XH[t * (E / 2u) + row * 64u + lane] = h0 | (h1 << 16);
+            if (tv) {
+                gd_u32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
+                    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+                    o[j] = h0 | (h1 << 16);
+                }
+                *reinterpret_cast<gd_u32x4 *>(XH + t * (E / 2u) + row * 64u + l16 * 4u) = o;
+            }
         }
     }
 }

@@ -573,7 +573,7 @@ class Engine {
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
                               bits(L.norm_eps), 2 * L.SF, L.SF ? L.sh_gu.srv : 0u, L.SF ? sh_h.uav : 0u,
                               L.SF ? L.sh_gate.srv : 0u, L.SF ? sh_g.uav : 0u},
-                             std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 16 + 1 : 0));
+                             std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 4 + 1 : 0));
         if (!decode_generic_types(L)) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
                                  {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
