@@ -26,7 +26,8 @@ Reported beside the throughput:
                 by seed across the eight Gyro types, plus the always-on bf16 shared SwiGLU expert of
                 width 1024; batch-1 decode and a 512-token prefill, with
                 packed-byte and FLOP rooflines, and the CPU oracle on a sample. Decode runs the
-                decode path's type-generic kernels, prefill the generic path.
+                decode path's type-generic kernels, prefill the prefill path's type-generic
+                grouped GEMMs and shared-expert GEMMs.
   prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (four cycled
                 copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
                 and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
