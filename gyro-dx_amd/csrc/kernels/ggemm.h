@@ -252,7 +252,7 @@ __device__ __forceinline__ void gx_stage(GxLds &sm, uint32_t buf, const GxState 
 
 // K block kb from buffer BUF for NRB 32-row blocks with blocks of Gyro type ID, in the software
 // pipeline of the TQ2_T kernels: between the MFMAs of K-step s go the codebook reads of step
-// s + 1 (two pieces over the first two slots) and its A operands (one per slot).
+// s + 2 (two pieces over the first two slots) and the A operands of step s + 1 (one per slot).
 template <int ID, int BUF, int NRB>
 __device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb, f32x16 (&acc)[NRB]) {
     gx_sync(t, kb);
@@ -267,16 +267,20 @@ __device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb
         for (int c = 0; c < 4; ++c) d[4 * j + c] = v[c];
     }
     float sc;
-    uint32_t w[NW], raw[4], pr = 0;
+    uint32_t w[NW], raw[2][4], pr[2] = {0u, 0u};  // gathers of even and odd steps, two steps ahead
     const uint32_t sel = gg_sel(t.h);
     if constexpr (ID == 144) {
         tq2_unpack(d, (kb & 1u) != 0u, sc, w);
-        gg_gather(w, 0, sel, sm.book, raw);
+        gg_gather(w, 0, sel, sm.book, raw[0]);
+        gg_gather(w, 1, sel, sm.book, raw[1]);
     } else {
         gyro_unpack<ID>(d, (kb & 1u) != 0u, sc, w);
         gx_half_stream<ID>(w, t.h);
-        gx_gather_piece<ID>(w, 0, 0, sm.book, raw);
-        gx_gather_piece<ID>(w, 0, 1, sm.book, raw);
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0) {
+            gx_gather_piece<ID>(w, s0, 0, sm.book, raw[s0]);
+            gx_gather_piece<ID>(w, s0, 1, sm.book, raw[s0]);
+        }
     }
     const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
     f16x8 av[NRB];
@@ -285,7 +289,7 @@ __device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb
     constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const f16x8 bv = gg_scale(raw, sc2);
+        const f16x8 bv = gg_scale(raw[s & 1], sc2);
         f16x8 cur[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) cur[rb] = av[rb];
@@ -294,16 +298,16 @@ __device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb
         for (int i = 0; i < NRB; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (s < 7) {
+            if (s < 6) {
 #pragma unroll
                 for (int piece = 0; piece < 2; ++piece) {
                     if (i < kPieceSlots && piece * kPieceSlots / 2 == i) {
-                        if constexpr (ID == 144) gg_gather_piece(w, s + 1, piece, sel, sm.book, pr, raw);
-                        else gx_gather_piece<ID>(w, s + 1, piece, sm.book, raw);
+                        if constexpr (ID == 144) gg_gather_piece(w, s + 2, piece, sel, sm.book, pr[s & 1], raw[s & 1]);
+                        else gx_gather_piece<ID>(w, s + 2, piece, sm.book, raw[s & 1]);
                     }
                 }
-                av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
             }
+            if (s < 7) av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
             __builtin_amdgcn_sched_barrier(0);
         }
     }

@@ -46,15 +46,16 @@ __device__ __forceinline__ void dn_step(GgLds &sm, const DnState &t, uint32_t kb
     uint32_t q[8];
     tq2_unpack(cur.d, kb & 1u, sc, q);
     const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
-    uint32_t raw[4], pr = 0;
-    gg_gather(q, 0, t.sel, sm.book, raw);
+    uint32_t raw[2][4], pr[2] = {0u, 0u};  // gathers of even and odd steps, two steps ahead
+    gg_gather(q, 0, t.sel, sm.book, raw[0]);
+    gg_gather(q, 1, t.sel, sm.book, raw[1]);
     f16x8 av[NRB];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) av[rb] = gg_a(sm, BUF, rb * 32u + t.m, 0, t.h);
     constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const f16x8 bv = gg_scale(raw, sc2);
+        const f16x8 bv = gg_scale(raw[s & 1], sc2);
         f16x8 cur_a[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) cur_a[rb] = av[rb];
@@ -63,11 +64,13 @@ __device__ __forceinline__ void dn_step(GgLds &sm, const DnState &t, uint32_t kb
         for (int i = 0; i < NRB; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur_a[i], bv, acc[i], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (s < 7) {
+            if (s < 6) {
 #pragma unroll
                 for (int piece = 0; piece < 2; ++piece)
                     if (i < kPieceSlots && piece * kPieceSlots / 2 == i)
-                        gg_gather_piece(q, s + 1, piece, t.sel, sm.book, pr, raw);
+                        gg_gather_piece(q, s + 2, piece, t.sel, sm.book, pr[s & 1], raw[s & 1]);
+            }
+            if (s < 7) {
                 av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
             }
             __builtin_amdgcn_sched_barrier(0);

@@ -56,17 +56,19 @@ __device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb
     const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
     // Software pipeline over the 8 K-steps with an explicit schedule (sched_barrier fences keep
     // the compiler from regrouping it): between the MFMAs of step s go the codebook gathers of
-    // step s + 1 (one trellis state per piece, over the first two slots) and its A operands
-    // (one per slot). LDS reads retire in order, so step s + 1 finds them complete.
-    uint32_t raw[4], pr = 0;
-    gg_gather(q, 0, t.sel, sm.book, raw);
+    // step s + 2 (one trellis state per piece, over the first two slots; two steps ahead, so a
+    // one-block tile still hides their latency) and the A operands of step s + 1 (one per
+    // slot). Gathers of even and odd steps use separate registers.
+    uint32_t raw[2][4], pr[2] = {0u, 0u};
+    gg_gather(q, 0, t.sel, sm.book, raw[0]);
+    gg_gather(q, 1, t.sel, sm.book, raw[1]);
     f16x8 av[NRB];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) av[rb] = gg_a(sm, BUF, rb * 32u + t.m, 0, t.h);
     constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const f16x8 bv = gg_scale(raw, sc2);
+        const f16x8 bv = gg_scale(raw[s & 1], sc2);
         f16x8 cur[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) cur[rb] = av[rb];
@@ -75,11 +77,13 @@ __device__ __forceinline__ void gu_step(GgLds &sm, const GuState &t, uint32_t kb
         for (int i = 0; i < NRB; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (s < 7) {
+            if (s < 6) {
 #pragma unroll
                 for (int piece = 0; piece < 2; ++piece)
                     if (i < kPieceSlots && piece * kPieceSlots / 2 == i)
-                        gg_gather_piece(q, s + 1, piece, t.sel, sm.book, pr, raw);
+                        gg_gather_piece(q, s + 2, piece, t.sel, sm.book, pr[s & 1], raw[s & 1]);
+            }
+            if (s < 7) {
                 av[i] = gg_a(sm, BUF, i * 32u + t.m, s + 1, t.h);
             }
             __builtin_amdgcn_sched_barrier(0);
