@@ -36,16 +36,31 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     __shared__ uint4 book4[512];
     __shared__ uint32_t rows[DN_U * DN_ROWS * DN_ROW_BYTES / 4];
     __shared__ float act[DN_U * DN_NB * DN_BLOCK_STRIDE];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const uint32_t E = a.c[15], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
     const uint32_t t = blockIdx.y, row0 = blockIdx.x * DN_ROWS;
     const uint32_t n_slots = n_tok * DN_U;
+    const bool has_signs = a.c[11] != 0xffffffffu;
+
+    // Every table read up front (each is a dependent scalar load); the routes first, since the
+    // rows' loads wait for them. Without signs the codebook entry stands in (never read).
+    const uint32_t *ids_p = gd_buf<const uint32_t>(a, a.c[2]);
+    const float *wts_p = gd_buf<const float>(a, a.c[4]);
+    const uint32_t *GU = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1];
+    const uint32_t *cb_p = gd_buf<const uint32_t>(a, a.c[10]);
+    const uint32_t *sg_p = gd_buf<const uint32_t>(a, has_signs ? a.c[11] : a.c[10]);
+    cuint *ids = as_const(ids_p + a.c[3] + t * DN_U);
+    cfloat *wtp = as_const(wts_p + a.c[5] + t * DN_U);
+    const uint32_t ew = min(ids[wave], NE - 1u);
+    float wts[DN_U];  // read at the end; loaded now so that their latency overlaps the rows'
+#pragma unroll
+    for (int kx = 0; kx < DN_U; ++kx) wts[kx] = wtp[kx];
 
     // Down input of expert `wave`, block b = lane / 16, values l16 * 8 .. l16 * 8 + 7 of the
-    // block. The partials, signs and codebook go first: they do not depend on the routes.
+    // block.
     const uint32_t b = lane >> 4, l16 = lane & 15u;
     const uint32_t slot = t * DN_U + wave, i0 = b * 128u + l16 * 8u;
-    const uint32_t *GU = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1];
     gd_u32x4 g4[2][2], u4[2][2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -57,19 +72,16 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
             u4[p][j] = gp[DN_F / 4 + j];
         }
     }
-    const bool has_signs = a.c[11] != 0xffffffffu;
     gd_u32x4 s4[2];
     if (has_signs) {
-        gd_gu32x4 *S = gd_global4(gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] + i0);
+        gd_gu32x4 *S = gd_global4(sg_p + a.c[12] + i0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) s4[j] = S[j];
     }
-    const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[10]))[tid];
+    const gd_u32x4 cbv = gd_global4(cb_p)[tid];
 
     // The 16 rows of expert `wave`: 136 chunks of 16 bytes, three per lane (the last partly).
-    cuint *ids = as_const(gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * DN_U);
     const uint64_t layer_base = (uint64_t)a.c[6] | ((uint64_t)a.c[7] << 32);
-    const uint32_t ew = min(ids[wave], NE - 1u);
     const uint8_t *src = reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)ew * a.c[8] + a.c[9] +
                          (size_t)row0 * DN_ROW_BYTES;
     gd_u32x4 rv[3];
@@ -155,7 +167,6 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     sum = sum + gd_dpp_f<0xB1>(sum);  // b0 + b1, b2 + b3
     sum = sum + gd_dpp_f<0x4E>(sum);  // (b0 + b1) + (b2 + b3), in every lane of the quad
     // Lane i (0, 1) combines row 2 w + i over the experts in k order from the quads 8 k + 4 i.
-    cfloat *wts = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * DN_U);
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int kx = 0; kx < DN_U; ++kx) {

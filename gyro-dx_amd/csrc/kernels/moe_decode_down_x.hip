@@ -108,6 +108,11 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     // The 16 rows of expert `wave`: 4 bb (at most 232) chunks of 16 bytes, four loads per lane,
     // every address clamped into the expert's rows.
     cuint *ids = as_const(gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * DN_U);
+    // The route weights too, so their latency overlaps the rows' (they are read at the end).
+    cfloat *wtp = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * DN_U);
+    float wts[DN_U];
+#pragma unroll
+    for (int kx = 0; kx < DN_U; ++kx) wts[kx] = wtp[kx];
     const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[6]);
     const uint32_t ew = min(ids[wave], NE - 1u);
     const uint32_t type_id = (xt[ew].types >> 16) & 0xffu;
@@ -219,7 +224,6 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     }
     __syncthreads();
     if (tid < DN_ROWS) {
-        cfloat *wts = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * DN_U);
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < DN_U; ++k) acc += wts[k] * dk[k][tid];
