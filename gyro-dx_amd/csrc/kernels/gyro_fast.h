@@ -86,6 +86,33 @@ __device__ __forceinline__ float tq2_block_dot(const uint32_t q[8], const uint32
     return acc0 + acc1;
 }
 
+// Half of tq2_block_dot: trellis steps 16 half .. 16 half + 15 (stream words 4 half .. + 3, and
+// the word before them for the first state) against x[64 half .. 64 half + 63].
+template <typename XP>
+__device__ __forceinline__ float tq2_half_dot(const uint32_t q[8], uint32_t half, const uint32_t *book, XP x) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qi = half ? q[4 + i] : q[i];
+        const uint32_t qp = half ? q[3 + i] : q[(i + 7) & 7];
+        const uint32_t p01 = tq2_pair01(qi, qp), p23 = tq2_pair23(qi);
+        const uint32_t s[4] = {p01 & 0x7fffu, __builtin_amdgcn_ubfe(p01, 16, 15), p23 & 0x7fffu,
+                               __builtin_amdgcn_ubfe(p23, 16, 15)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t a0, a1;
+            cb_addr(s[j], a0, a1);
+            const uint32_t w0 = lds_word(book, a0), w1 = lds_word(book, a1);
+            const XP xs = x + (i * 4 + j) * 4;
+            acc0 = fma_lo(w0, xs[0], acc0);
+            acc1 = fma_hi(w0, xs[1], acc1);
+            acc0 = fma_lo(w1, xs[2], acc0);
+            acc1 = fma_hi(w1, xs[3], acc1);
+        }
+    }
+    return acc0 + acc1;
+}
+
 // As tq2_block_dot with activations as 64 packed binary16 pairs held in scalar registers
 // (xs[2t] = x[4t], x[4t+1]; xs[2t+1] = x[4t+2], x[4t+3]): two v_dot2_f32_f16 per step, fp32
 // accumulation of exact fp16 products.

@@ -2,17 +2,17 @@
 // down rows, and the route-weighted combine (src/engine.zig:603-641), with no communication
 // between groups.
 //
-// A group owns 16 output rows of one token for all 8 selected experts, so the combine is local
-// and summed in k order. The gate/up partials, signs and codebook are requested first (global
-// loads), then the routes; wave w streams the 16 down rows of expert w (2176 contiguous bytes)
+// A group owns 8 output rows of one token for all 8 selected experts, so the combine is local
+// and summed in k order. The routes, gate/up partials, signs and codebook are requested first
+// (global and scalar loads); wave w streams the 8 down rows of expert w (1088 contiguous bytes)
 // from HBM and, while they arrive, forms expert w's down input a = H_128(s_down * silu(g) * u)
 // from the gate/up partials: a 16-lane row of the wave transforms one 128-block holding 8
 // consecutive values per lane (widths 1..4 in registers, 8, 16, 32, 64 across lanes with DPP:
-// the butterfly order of src/gyro.zig:152-172). After one barrier, lane 8 k + 4 i + bb of wave w
-// decodes block bb of output row 2 w + i of expert k against its block of a in LDS; the four
-// block sums are added with DPP ((b0 + b1) + (b2 + b3)) and lanes 0 and 1 combine the experts of
-// their row in k order, with no second barrier.
-// Grid: x = E / 16, y = n_tok; 512 threads.
+// the butterfly order of src/gyro.zig:152-172). After one barrier, lane 8 k + 2 bb + hf of wave
+// w decodes half hf (16 trellis steps) of block bb of output row w of expert k against a in
+// LDS; the 8 half-block sums of an expert are added with DPP, and lane 0 combines the experts
+// in k order.
+// Grid: x = E / 8, y = n_tok; 512 threads.
 // Constants: 0 gu_uav 1 gu_off 2 ids_uav 3 ids_off 4 weights_uav 5 weights_off 6 base_lo
 // 7 base_hi 8 slot_stride 9 down_off (bytes from an expert's bundle start) 10 codebook_srv
 // 11 signs_srv (0xffffffff: none) 12 signs_off 13 out_uav 14 out_off 15 E 16 F 17 n_used
@@ -24,7 +24,7 @@
 #include "gyro_fast.h"
 #include "fwht.h"
 
-#define DN_ROWS 16
+#define DN_ROWS 8
 #define DN_U 8
 #define DN_F 512
 #define DN_NB (DN_F / 128)
@@ -80,13 +80,13 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     }
     const gd_u32x4 cbv = gd_global4(cb_p)[tid];
 
-    // The 16 rows of expert `wave`: 136 chunks of 16 bytes, three per lane (the last partly).
+    // The 8 rows of expert `wave`: 68 chunks of 16 bytes, two per lane (the second for lanes < 4).
     const uint64_t layer_base = (uint64_t)a.c[6] | ((uint64_t)a.c[7] << 32);
     const uint8_t *src = reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)ew * a.c[8] + a.c[9] +
                          (size_t)row0 * DN_ROW_BYTES;
-    gd_u32x4 rv[3];
+    gd_u32x4 rv[2];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) rv[j] = *gd_global4(reinterpret_cast<const uint32_t *>(src + min(lane + 64u * j, 135u) * 16u));
+    for (int j = 0; j < 2; ++j) rv[j] = *gd_global4(reinterpret_cast<const uint32_t *>(src + min(lane + 64u * j, 67u) * 16u));
 
     float v[8];
 #pragma unroll
@@ -144,18 +144,18 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < 2; ++j) {
         const uint32_t c = lane + 64u * j;
-        if (c < 136u) {
+        if (c < 68u) {
             uint32_t *rdst = rows + wave * (DN_ROWS * DN_ROW_BYTES / 4) + c * 4u;
             rdst[0] = rv[j][0]; rdst[1] = rv[j][1]; rdst[2] = rv[j][2]; rdst[3] = rv[j][3];
         }
     }
     __syncthreads();
 
-    // Unit (expert k, row 2 w + i, block bb) on lane 8 k + 4 i + bb.
-    const uint32_t k = lane >> 3, ri = (lane >> 2) & 1u, bb = lane & 3u, r = 2u * wave + ri;
-    const uint32_t off = k * (DN_ROWS * DN_ROW_BYTES) + r * DN_ROW_BYTES + bb * 34u;
+    // Unit (expert k, row w, block bb, half hf) on lane 8 k + 2 bb + hf.
+    const uint32_t k = lane >> 3, bb = (lane >> 1) & 3u, hf = lane & 1u;
+    const uint32_t off = k * (DN_ROWS * DN_ROW_BYTES) + wave * DN_ROW_BYTES + bb * 34u;
     const uint32_t *w = rows + (off >> 2);
     uint32_t d[9];
 #pragma unroll
@@ -163,20 +163,18 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     float sc;
     uint32_t q[8];
     tq2_unpack(d, (off & 2u) != 0u, sc, q);
-    float sum = sc * tq2_block_dot(q, reinterpret_cast<const uint32_t *>(book4), act + (k * DN_NB + bb) * DN_BLOCK_STRIDE);
-    sum = sum + gd_dpp_f<0xB1>(sum);  // b0 + b1, b2 + b3
-    sum = sum + gd_dpp_f<0x4E>(sum);  // (b0 + b1) + (b2 + b3), in every lane of the quad
-    // Lane i (0, 1) combines row 2 w + i over the experts in k order from the quads 8 k + 4 i.
-    float acc0 = 0.f, acc1 = 0.f;
+    float sum = sc * tq2_half_dot(q, hf, reinterpret_cast<const uint32_t *>(book4),
+                                  act + (k * DN_NB + bb) * DN_BLOCK_STRIDE + 64u * hf);
+    sum = sum + gd_dpp_f<0xB1>(sum);   // the two halves of a block
+    sum = sum + gd_dpp_f<0x4E>(sum);   // b0 + b1, b2 + b3
+    sum = sum + gd_dpp_f<0x104>(sum);  // row_shl:4: (b0 + b1) + (b2 + b3) in lane 8 k
+    // Lane 0 combines row w over the experts in k order from lanes 8 k.
+    float acc = 0.f;
 #pragma unroll
-    for (int kx = 0; kx < DN_U; ++kx) {
-        const float wk = wts[kx];
-        acc0 += wk * gd_bits_f32((uint32_t)__builtin_amdgcn_readlane((int)gd_f32_bits(sum), 8 * kx));
-        acc1 += wk * gd_bits_f32((uint32_t)__builtin_amdgcn_readlane((int)gd_f32_bits(sum), 8 * kx + 4));
-    }
-    if (lane < 2u) {
-        float acc = lane ? acc1 : acc0;
-        const uint32_t orow = row0 + 2u * wave + lane;
+    for (int kx = 0; kx < DN_U; ++kx)
+        acc += wts[kx] * gd_bits_f32((uint32_t)__builtin_amdgcn_readlane((int)gd_f32_bits(sum), 8 * kx));
+    if (lane == 0u) {
+        const uint32_t orow = row0 + wave;
         if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + t * E + orow] + acc;
         gd_buf<float>(a, a.c[13])[a.c[14] + t * E + orow] = acc;
     }

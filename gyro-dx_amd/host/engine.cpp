@@ -584,7 +584,7 @@ class Engine {
                                   2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
                                   out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
                                   st.res_off},
-                                 E / 16, n);
+                                 E / 8, n);
             return;
         }
         dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_x",
