@@ -80,11 +80,22 @@ GD_PIPELINE_NAMED(moe_router, 256) {
                 router_shared_rows(a, sg, n_tok, E);
             } else {
                 // The gate dot g . x (fp32 row), one wave per token.
-                gd_guint *G = gd_global(gd_buf<const uint32_t>(a, a.c[23]));
-                gd_guint *XG = gd_global(reinterpret_cast<const uint32_t *>(X));
+                // Wave w takes tokens w, w + 4, ...; lane l the 4 columns 4 l + 256 m of every
+                // 256-column chunk m, all loads in flight together (E <= 2048).
+                const uint32_t *G = gd_buf<const uint32_t>(a, a.c[23]) + 4u * lane;
+                const uint32_t *XU = reinterpret_cast<const uint32_t *>(X) + x_off + 4u * lane;
                 for (uint32_t t = wave; t < n_tok; t += 4u) {
+                    float4 gv[SH_MAX_E / 256], xv[SH_MAX_E / 256];
+#pragma unroll
+                    for (int m = 0; m < SH_MAX_E / 256; ++m)
+                        if (256u * m < E) {
+                            gv[m] = rt_f4(*gd_global4(G + 256u * m));
+                            xv[m] = rt_f4(*gd_global4(XU + t * x_stride + 256u * m));
+                        }
                     float acc = 0.f;
-                    for (uint32_t i = lane; i < E; i += 64u) acc += gd_bits_f32(G[i]) * gd_bits_f32(XG[x_off + t * x_stride + i]);
+#pragma unroll
+                    for (int m = 0; m < SH_MAX_E / 256; ++m)
+                        if (256u * m < E) acc += (gv[m].x * xv[m].x + gv[m].y * xv[m].y) + (gv[m].z * xv[m].z + gv[m].w * xv[m].w);
                     acc = gd_wave_sum_dpp(acc);
                     if (lane == 0) gd_buf<float>(a, a.c[24])[t] = acc;
                 }
