@@ -4,7 +4,7 @@
 //   xo[t] = v                            (when given: the residual stream after the add)
 //   h[t]  = v / sqrt(mean(v^2) + eps) * w
 // One group per token, 256 threads, up to 16 values per thread (E <= 4096). The sum of squares
-// is reduced per wave with shuffles, then over the four waves in order. xo may alias x: every
+// is reduced per wave with DPP, then over the four waves in order. xo may alias x: every
 // load of a thread comes before its first store, so the loads need not wait for the stores.
 // Grid: n tokens; 256 threads.
 // Constants: 0 x_uav 1 x_off 2 add_uav (0xffffffff: none) 3 add_off 4 w_srv (0xffffffff: none)
@@ -39,16 +39,23 @@ GD_PIPELINE_NAMED(moe_stack_norm, 256) {
             if (i < E) XO[i] = v[j];
         }
     }
-    ss = gd_wave_sum(ss);
+    // The norm weights are loaded before the barrier, so their latency overlaps it.
+    float wv[SN_PER];
+    const float *W = has_w ? gd_buf<const float>(a, a.c[4]) + a.c[5] : nullptr;
+#pragma unroll
+    for (int j = 0; j < SN_PER; ++j) {
+        const uint32_t i = tid + 256u * j;
+        wv[j] = has_w && i < E ? W[i] : 1.f;
+    }
+    ss = gd_wave_sum_dpp(ss);
     if (lane == 0) part[wave] = ss;
     __syncthreads();
     const float total = (part[0] + part[1]) + (part[2] + part[3]);
     const float scale = 1.0f / sqrtf(total / (float)E + gd_bits_f32(a.c[9]));
-    const float *W = has_w ? gd_buf<const float>(a, a.c[4]) + a.c[5] : nullptr;
     float *H = gd_buf<float>(a, a.c[6]) + a.c[7] + row;
 #pragma unroll
     for (int j = 0; j < SN_PER; ++j) {
         const uint32_t i = tid + 256u * j;
-        if (i < E) H[i] = has_w ? v[j] * scale * W[i] : v[j] * scale;
+        if (i < E) H[i] = has_w ? v[j] * scale * wv[j] : v[j] * scale;
     }
 }

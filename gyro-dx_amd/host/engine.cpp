@@ -604,8 +604,8 @@ class Engine {
     // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
     // A shared expert runs as moe_prefill_shared (SF a multiple of 64).
     bool prefill_supported(const Layer &L) const {
-        return L.SF % 64 == 0 && E % 256 == 0 && F % 256 == 0 && U == 8 && NE <= 256 &&
-               L.max_scale * max_codebook < 65504.0f;
+        return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % 256 == 0 && U == 8 &&
+               NE <= 256 && L.max_scale * max_codebook < 65504.0f;
     }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
@@ -617,8 +617,8 @@ class Engine {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
             throw NativeError(-1, "prefill path needs E and F multiples of 256, top-8 of <= 256 experts, a shared "
-                                  "expert (if any) of width a multiple of 64 and binary16-finite scale x codebook "
-                                  "products");
+                                  "expert (if any) of width a multiple of 64 on E <= 4096 and binary16-finite "
+                                  "scale x codebook products");
         if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (4096 tokens of top-8)");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
