@@ -436,3 +436,275 @@ __device__ __forceinline__ void gg_down_epilogue(LDS &sm, const f32x16 (&acc)[NR
         *reinterpret_cast<float4 *>(out + (size_t)sm.src[i] * E + eb * 256u + c * 4u) = v;
     }
 }
+
+// ---- Two groups per CU: the half-block pipeline of the TQ2_T kernels ----------------------
+// The same tiles and decode as above in 80 KB of LDS and at most 128 VGPRs, so that two groups
+// share a CU (four waves per SIMD): while one group waits at a barrier or on its gathers, the
+// other issues. Activations are staged in sub-blocks of 64 K (128 bytes of a row, 16 KB for
+// 128 rows) into three buffers, two sub-blocks ahead; weight blocks (128 K) go to two buffers,
+// issued three sub-blocks ahead: the buffer of block b - 1 is free once every wave has passed
+// the first sub-block of block b - 1, where each lane reads its block into registers.
+// Issue order per wave: prologue A0 W0 A1 W1; sub-block j (after its sync) stages A(j + 2) and,
+// for odd j, W((j + 3) / 2). A row's eight 16-byte chunks are XOR-swizzled (chunk c of row r
+// at position c ^ ((r >> 1) & 7)), so that the A-operand reads of 16 rows (one chunk index,
+// rows of even and odd parity in the two 128-byte bank halves) hit 16 different bank groups,
+// and the chunk of K-step s (0..3) of a sub-block sits at byte (lane's step-0 byte) ^ 32 s.
+#define GH_AROW 128
+#define GH_ABUF (GG_TM * GH_AROW)
+
+struct __attribute__((aligned(16))) GhLds {
+    uint32_t book[2048];                             // 8 KB, at offset 0
+    gd_u32x4 a[GG_NBUF][GH_ABUF / 16];               // 3 x 16 KB
+    gd_u32x4 w[2][GG_WROWS * GG_WROW / 16];          // 2 x 12 KB
+};
+static_assert(sizeof(GhLds) == 81920, "two groups fill the CU's 160 KB");
+
+struct GhState {
+    const void *abase, *wbase;  // activation rows; the layer's slot arena
+    uint32_t roff[2], woff[2];  // per load: lane offset at sub-block / block 0
+    uint32_t nal, nwl;          // activation loads per sub-block (0 or 2), weight loads per block (1 or 2)
+    uint32_t wave, m, h, sel, nk;
+    uint32_t wq;                // staged weight row this lane decodes
+    uint32_t arow;              // byte of this lane's step-0 A chunk of rows m + 32 rb in buffer 0
+};
+
+// Start of sub-block j of nj: at most the loads issued after the wave's loads of sub-block j
+// (and of its weight block) stay outstanding: A(j + 1) and a weight block before the last two
+// sub-blocks, A(j + 1) before the last one, none at the last.
+__device__ __forceinline__ void gh_sync(const GhState &t, uint32_t j, uint32_t nj) {
+    const uint32_t newer = j + 3u <= nj ? t.nal + t.nwl : (j + 2u == nj ? t.nal : 0u);
+    switch (newer) {
+        case 4: gg_sync<4>(); break;
+        case 3: gg_sync<3>(); break;
+        case 2: gg_sync<2>(); break;
+        case 1: gg_sync<1>(); break;
+        default: gg_sync<0>(); break;
+    }
+}
+
+// Activation sub-block j of rows 16 w .. 16 w + 15: two loads of 8 rows x 128 bytes; lane l
+// writes position l % 8 of row 16 w + 8 i + l / 8 (roff holds the swizzled source chunk).
+__device__ __forceinline__ void gh_stage_a(GhLds &sm, uint32_t buf, const GhState &t, uint32_t j) {
+    const uint32_t base = gg_lds_addr(&sm.a[0][0]) + buf * GH_ABUF + t.wave * 16u * GH_AROW;
+    gg_dma16(base, t.abase, t.roff[0] + j * GH_AROW);
+    gg_dma16(base + 8u * GH_AROW, t.abase, t.roff[1] + j * GH_AROW);
+}
+// Swizzled source chunk offset of load i for lane `lane` of wave `wave`, and its row.
+__device__ __forceinline__ uint32_t gh_chunk(uint32_t wave, uint32_t lane, int i, uint32_t &row) {
+    row = wave * 16u + (uint32_t)i * 8u + (lane >> 3);
+    return ((lane & 7u) ^ ((row >> 1) & 7u)) * 16u;
+}
+// Weight block kb of the 256 staged rows (as gg_stage_w8).
+__device__ __forceinline__ void gh_stage_w(GhLds &sm, uint32_t buf, const GhState &t, uint32_t kb) {
+    const uint32_t base = gg_lds_addr(&sm.w[0][0]) + buf * (uint32_t)sizeof(sm.w[0]);
+    const uint32_t kbo = (kb * 34u) & ~3u;
+    gg_dma16(base + gg_w8_load(t.wave, 0) * 1024u, t.wbase, t.woff[0] + kbo);
+    if (t.nwl == 2u) gg_dma16(base + gg_w8_load(t.wave, 1) * 1024u, t.wbase, t.woff[1] + kbo);
+}
+// Step-0 A byte of lane (m, h) in buffer 0 (row m, chunk h).
+__device__ __forceinline__ uint32_t gh_arow(const GhLds &sm, uint32_t m, uint32_t h) {
+    return (uint32_t)((const uint8_t *)&sm.a[0][0] - (const uint8_t *)&sm) + m * GH_AROW +
+           ((h ^ ((m >> 1) & 7u)) << 4);
+}
+__device__ __forceinline__ f16x8 gh_a(const GhLds &sm, uint32_t byte) {
+    return *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(&sm) + byte);
+}
+
+// Half HALF (K-steps 4 HALF .. 4 HALF + 3) of a weight block for NRB 32-row blocks, from the
+// activation buffer at byte offset abyte of buffer 0 plus this lane's row: MFMAs of step s, with
+// the codebook gathers of step s + 2 and the A operands of step s + 1 between them (as gu_step).
+template <int HALF, int NRB>
+__device__ __forceinline__ void gh_half(const GhLds &sm, uint32_t arow, const uint32_t (&q)[8], uint32_t sel,
+                                        half2_t sc2, uint32_t (&raw)[2][4], uint32_t (&pr)[2], f32x16 (&acc)[NRB]) {
+    f16x8 av[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) av[rb] = gh_a(sm, arow + rb * 32u * GH_AROW);
+    constexpr int kPieceSlots = NRB < 2 ? NRB : 2;
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) {
+        const int s = 4 * HALF + sl;
+        const f16x8 bv = gg_scale(raw[s & 1], sc2);
+        f16x8 cur[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) cur[rb] = av[rb];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s < 6) {
+#pragma unroll
+                for (int piece = 0; piece < 2; ++piece)
+                    if (i < kPieceSlots && piece * kPieceSlots / 2 == i)
+                        gg_gather_piece(q, s + 2, piece, sel, sm.book, pr[s & 1], raw[s & 1]);
+            }
+            if (sl < 3) av[i] = gh_a(sm, (arow ^ (32u * (uint32_t)(sl + 1))) + (uint32_t)i * 32u * GH_AROW);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// Weight row q's 9 words of staged block buffer buf.
+__device__ __forceinline__ void gh_read_w(const GhLds &sm, uint32_t buf, uint32_t q, GgBlk &b) {
+    const gd_u32x4 lo = sm.w[buf][q * 3u], mid = sm.w[buf][q * 3u + 1u];
+    const gd_u32x4 hi = sm.w[buf][q * 3u + 2u];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        b.d[j] = lo[j];
+        b.d[4 + j] = mid[j];
+    }
+    b.d[8] = hi[0];
+}
+
+// The K loop: blocks of 128 K as two sub-blocks, A(j) in buffer j % 3 and W(b) in buffer b % 2.
+// Requires nk >= 2 and the prologue (A0 W0 A1 W1) issued; ends with every load landed and every
+// wave past its last LDS read.
+template <int NRB>
+__device__ __forceinline__ void gh_kloop(GhLds &sm, const GhState &t, f32x16 (&acc)[NRB]) {
+#pragma unroll
+    for (int r = 0; r < NRB; ++r) acc[r] = (f32x16){};
+    const uint32_t nj = 2u * t.nk;
+    uint32_t abuf = 0;  // buffer of sub-block j: j % 3
+    for (uint32_t kb = 0; kb < t.nk; ++kb) {
+        const uint32_t j = 2u * kb;
+        // Even sub-block: stage A(j + 2); read and unpack the weight block, first gathers.
+        gh_sync(t, j, nj);
+        if (j + 2u < nj && t.nal) gh_stage_a(sm, abuf == 0u ? 2u : abuf - 1u, t, j + 2u);
+        GgBlk wc;
+        gh_read_w(sm, kb & 1u, t.wq, wc);
+        float sc;
+        uint32_t q[8];
+        tq2_unpack(wc.d, (kb & 1u) != 0u, sc, q);
+        const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
+        uint32_t raw[2][4], pr[2] = {0u, 0u};
+        gg_gather(q, 0, t.sel, sm.book, raw[0]);
+        gg_gather(q, 1, t.sel, sm.book, raw[1]);
+        gh_half<0, NRB>(sm, t.arow + abuf * GH_ABUF, q, t.sel, sc2, raw, pr, acc);
+        abuf = abuf == 2u ? 0u : abuf + 1u;
+        // Odd sub-block: stage A(j + 3) and W(kb + 2) (into the buffer of block kb, read above).
+        gh_sync(t, j + 1u, nj);
+        if (j + 3u < nj && t.nal) gh_stage_a(sm, abuf == 0u ? 2u : abuf - 1u, t, j + 3u);
+        if (kb + 2u < t.nk) gh_stage_w(sm, kb & 1u, t, kb + 2u);
+        gh_half<1, NRB>(sm, t.arow + abuf * GH_ABUF, q, t.sel, sc2, raw, pr, acc);
+        abuf = abuf == 2u ? 0u : abuf + 1u;
+    }
+    gg_sync<0>();  // every wave is done with the buffers
+}
+
+// Makes the epilogue's scalar operands (an output pointer and a size) arrive before the K loop:
+// a scalar load still outstanding there would turn every counted LDS wait of the loop into a
+// wait for all LDS traffic (scalar loads return out of order).
+template <class T>
+__device__ __forceinline__ void gh_settle(T *ptr, uint32_t n) {
+    asm volatile("" ::"s"(ptr), "s"(n));
+}
+
+// Prologue of the K loop: A0 W0 A1 W1.
+__device__ __forceinline__ void gh_prologue(GhLds &sm, const GhState &t) {
+    if (t.nal) gh_stage_a(sm, 0, t, 0);
+    gh_stage_w(sm, 0, t, 0);
+    if (t.nal) gh_stage_a(sm, 1, t, 1);
+    gh_stage_w(sm, 1, t, 1);
+}
+
+// Gate/up epilogue in the 80 KB: bytes [0, 32 K) hold u (fp32, 64 rows x 128 columns, one half
+// of the tile at a time) and later the rotated rows; bytes [32 K, 64 K) the act rows (binary16,
+// 128 rows of 16 chunks, chunk c of row i at position c ^ (i % 16)). Otherwise as
+// gg_gu_epilogue: act = down_signs * silu(g) * u rounded to binary16, then (with down signs)
+// the 128-point Walsh-Hadamard transform of every row as an MFMA product with H_128, and rows
+// of 128 binary16 values to out[row0 + i][fb * 128 ..].
+// sgn: the down sign of this gate lane's column (1 without signs), loaded before the K loop.
+template <int NRB>
+__device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
+                                               uint32_t h, bool signs, float sgn, uint32_t *out, uint32_t row0,
+                                               uint32_t rows, uint32_t fb, uint32_t F) {
+    uint8_t *lds = reinterpret_cast<uint8_t *>(&sm);
+    float *ubuf = reinterpret_cast<float *>(lds);
+    _Float16 *act = reinterpret_cast<_Float16 *>(lds + 32768);
+    gd_u32x4 *actc = reinterpret_cast<gd_u32x4 *>(lds + 32768);
+    const bool up = wave >= 4u;
+    const uint32_t cq = wave & 3u, col = cq * 32u + m;
+#pragma unroll
+    for (int p = 0; p < (NRB + 1) / 2; ++p) {
+        if (up) {
+#pragma unroll
+            for (int rb = 2 * p; rb < NRB && rb < 2 * p + 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    ubuf[((rb - 2 * p) * 32u + (r / 4) * 8u + h * 4u + (r % 4)) * 128u + col] = acc[rb][r];
+        }
+        __syncthreads();
+        if (!up) {
+#pragma unroll
+            for (int rb = 2 * p; rb < NRB && rb < 2 * p + 2; ++rb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t iu = (rb - 2 * p) * 32u + (r / 4) * 8u + h * 4u + (r % 4), i = iu + 64u * p;
+                    act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
+                        (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[iu * 128u + col] * sgn);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (signs) {
+        const uint32_t j = col, half = wave >> 2;
+        f16x8 hp, hn;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            hp[e] = (__builtin_popcount((uint32_t)e & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
+            hn[e] = -hp[e];
+        }
+        _Float16 *res = reinterpret_cast<_Float16 *>(lds);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            if ((uint32_t)(rb & 1) != half) continue;  // uniform per wave
+            f32x16 rot = (f32x16){};
+            const uint32_t i0 = rb * 32u + m;
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const f16x8 hb = (__builtin_popcount((16u * s8 + 8u * h) & j) & 1) ? hn : hp;
+                const f16x8 av = __builtin_bit_cast(f16x8, actc[i0 * 16u + (((uint32_t)(2 * s8) + h) ^ (i0 & 15u))]);
+                rot = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, hb, rot, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
+            }
+        }
+        __syncthreads();
+    }
+    // Global (not flat) stores: a flat access also counts as LDS traffic in the wait counters.
+    const gd_u32x4 *rows_src = reinterpret_cast<const gd_u32x4 *>(signs ? lds : lds + 32768);
+    __attribute__((address_space(1))) gd_u32x4 *og =
+        (__attribute__((address_space(1))) gd_u32x4 *)(uintptr_t)(out + (size_t)row0 * (F / 2u) + fb * 64u);
+    for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
+        const uint32_t i = idx >> 4, c = idx & 15u;
+        og[(size_t)i * (F / 8u) + c] = rows_src[i * 16u + (c ^ (i & 15u))];
+    }
+}
+
+// Down epilogue: wave w holds output columns 32 w + m of rows rb * 32 + 8 (r / 4) + 4 h + r % 4;
+// each value goes straight to out[slot of row i][eb * 256 + 32 w + m] (lanes m: 128 contiguous
+// bytes of a row). my_slot: the slot of sorted row threadIdx.x (threads < 128), passed through
+// LDS.
+template <int NRB>
+__device__ __forceinline__ void gh_down_epilogue(GhLds &sm, const f32x16 (&acc)[NRB], uint32_t my_slot,
+                                                 uint32_t wave, uint32_t m, uint32_t h, float *out, uint32_t rows,
+                                                 uint32_t eb, uint32_t E) {
+    uint32_t *slot = reinterpret_cast<uint32_t *>(&sm);
+    if (threadIdx.x < GG_TM) slot[threadIdx.x] = my_slot;
+    __syncthreads();
+    // Global (not flat) stores: a flat access also counts as LDS traffic in the wait counters.
+    __attribute__((address_space(1))) float *o =
+        (__attribute__((address_space(1))) float *)(uintptr_t)(out + eb * 256u + wave * 32u + m);
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
+            if (i < rows) o[(size_t)slot[i] * E] = acc[rb][r];
+        }
+    }
+}
