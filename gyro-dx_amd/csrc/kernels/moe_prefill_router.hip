@@ -3,33 +3,52 @@
 //   logits[t][r] = W_r[r] . x[t] (+ bias[r])          src/engine.zig:526 (kernels.matmul)
 //   xh16[t]      = H_128 (gate_signs * x[t]) per 128-block, as binary16 pairs
 //                                                      src/engine.zig:547-551
-// Group (bx, by) computes the 32 x 32 logit tile of tokens 32 bx.. and experts 32 by.. with
-// v_mfma_f32_32x32x2_f32; its four waves split K = E into quarters and their partial tiles are
-// added in wave order through LDS. The MFMA operands take one row per lane, so each wave stages
-// its own 32-wide K chunks of the 32 token rows and the 32 router rows into LDS first: direct
-// global-to-LDS loads (8 lanes per 128-byte row, whole rows per load), the 16-byte chunk q of
-// row r stored at position q ^ (r % 8), two chunks ahead in three buffers per wave; only the
-// wave's own load count is waited for, so the K loop has no barrier. Lane half h takes k + 4h
-// .. k + 4h + 3 of every 8 for both operands, so every product x[t][k] W[r][k] enters the sum
-// once. The rotation of all n * E/128 blocks is spread over every wave of the grid, eight
-// blocks per wave at a time.
-// Grid: (ceil(n / 32), ceil(n_expert / 32)); 256 threads. Requires E % 128 == 0.
+// Group (bx, by, bz) computes the 32 x 32 logit tile of tokens 32 bx.. and experts 32 by.. over
+// K range bz of S (the K split, chosen by the host so that small batches still fill the GPU)
+// with v_mfma_f32_32x32x2_f32; its waves 0..3 split the range into quarters and their partial
+// tiles are added in wave order through LDS. Range bz writes logit plane bz; the top-k kernel
+// adds the S planes in plane order. The MFMA operands take one row per lane, so each of these
+// waves stages its own 32-wide K chunks of the 32 token rows and the 32 router rows into LDS
+// first: direct global-to-LDS loads (8 lanes per 128-byte row, whole rows per load), the
+// 16-byte chunk q of row r stored at position q ^ (r % 8), two chunks ahead in three buffers per
+// wave, four chunks ahead in five buffers per wave; only the wave's own load count is waited
+// for, so the K loop has no barrier, and the operands of chunk c + 1 are read from LDS while the
+// MFMAs of chunk c run. Lane half h takes
+// k + 4h .. k + 4h + 3 of every 8 for both operands, so every product x[t][k] W[r][k] enters the
+// sum once. Waves 4..7 meanwhile rotate: all n * E/128 blocks are spread over the rotation
+// waves of the grid, eight blocks per wave at a time, so the rotation's memory traffic and VALU
+// work overlap the MFMA chains on the same SIMDs.
+// Grid: (ceil(n / 32), ceil(n_expert / 32), S); 512 threads. Requires E % (128 S) == 0.
 // Constants: 0 x_uav 1 x_off (words; rows of E floats) 2 n_tok 3 E 4 router_srv 5 router_off
 // 6 n_expert 7 bias_srv (0xffffffff: none) 8 bias_off 9 logits_uav 10 logits_off
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
 // 14 xh16_off (words) 15 x16 (1: also write the unrotated input as binary16, for the shared
-// expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words).
+// expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words) 18 S (0 or
+// 1: no split; plane z at logits_off + z n n_expert; the bias enters plane 0).
 #include "ggemm.h"
 #include "fwht.h"
 
 #define RT_WAVES 4
 #define RT_KC 32    // K per staged chunk
-#define RT_NBUF 3
+#define RT_NBUF 5    // chunks c .. c + 4 of a wave in LDS: four chunks (32 KB) in flight
 
+// 160 KB: the staging buffers of the four K waves; after its K loop a wave's partial tile
+// (4 KB, fp32) goes over its own first activation buffer.
 struct __attribute__((aligned(16))) RtLds {
     gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 128 bytes
     gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_KC / 4];
 };
+static_assert(sizeof(RtLds) == 163840, "the CU's 160 KB");
+
+// Waits until chunk c's loads have landed, with `ahead` later chunks (8 loads each) in flight.
+__device__ __forceinline__ void rt_wait(uint32_t ahead) {
+    switch (ahead) {
+        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
 
 // Stages chunk c (K = kq + 32 c ..) of this wave's 32 token rows and 32 router rows: 4 + 4
 // loads, lane l of load i carrying row 8 i + l / 8, position l % 8.
@@ -57,35 +76,78 @@ __device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16]
     d[1] = o[1];
 }
 
-GD_PIPELINE_NAMED(moe_prefill_router, 256) {
+GD_PIPELINE_NAMED(moe_prefill_router, 512) {
     __shared__ RtLds sm;
-    __shared__ float red[RT_WAVES][32 * 32];
+    float *red = reinterpret_cast<float *>(&sm.x[0][0][0]);  // red(w) at sm.x[w][0]
+    constexpr uint32_t kRedStride = sizeof(sm.x[0]) / 4u;   // floats from one wave's buffers to the next
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = a.c[2], E = a.c[3], NE = a.c[6];
     const float *X = gd_buf<const float>(a, a.c[0]) + a.c[1];
-    const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
+    const uint32_t t0 = blockIdx.x * 32u, r0 = blockIdx.y * 32u, z = blockIdx.z;
+    const uint32_t S = a.c[18] > 1u ? a.c[18] : 1u, ES = E / S;
+    const uint32_t m = lane & 31u, h = lane >> 5;
+    f32x16 acc = {};
 
-    // Router tile: start the staging of this wave's first chunks before the rotation share.
-    const uint32_t t0 = blockIdx.x * 32u, r0 = blockIdx.y * 32u;
-    const uint32_t kq = wave * (E / 4u), nc = E / 4u / RT_KC;
-    uint32_t xoff[4], woff[4];
+    if (wave < RT_WAVES) {
+        // Router tile, K quarter `wave`.
+        const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
+        const uint32_t kq = z * ES + wave * (ES / 4u), nc = ES / 4u / RT_KC;
+        uint32_t xoff[4], woff[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = (lane & 7u) ^ (r & 7u);
-        xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
-        woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
-    }
-    rt_stage(sm, wave, 0, X, W, xoff, woff, 0);
-    if (nc > 1u) rt_stage(sm, wave, 1, X, W, xoff, woff, RT_KC * 4u);
-
-    // Rotation share of this group: each wave transforms eight 128-blocks at a time, an 8-lane
-    // group per block holding 16 consecutive values per lane (gd_fwht128_x16); the blocks
-    // b = 8 (first + waves j) + lane / 8.
-    {
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = (lane & 7u) ^ (r & 7u);
+            xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
+            woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
+        }
+        for (uint32_t c = 0; c < nc && c < RT_NBUF - 1u; ++c) rt_stage(sm, wave, c, X, W, xoff, woff, c * RT_KC * 4u);
+        // Rows beyond n or n_expert were staged as copies of the last row; their operands are
+        // zeroed here.
+        const bool tv = t0 + m < n, rv = r0 + m < NE;
+        float4 xv[4], wv[4];
+        auto read_chunk = [&](uint32_t buf) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
+                xv[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
+                wv[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
+            }
+        };
+        rt_wait(min(nc - 1u, RT_NBUF - 2u));  // chunks 1 .. 3 may be in flight
+        read_chunk(0);
+        for (uint32_t c = 0; c < nc; ++c) {
+            float4 xa[4], wa[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xa[j] = tv ? xv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+                wa[j] = rv ? wv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            // Chunk c + 4 into the buffer of chunk c - 1, whose operands were read (and waited
+            // for) before the MFMAs of chunk c - 1.
+            if (c + 4u < nc) rt_stage(sm, wave, (c + 4u) % RT_NBUF, X, W, xoff, woff, (c + 4u) * RT_KC * 4u);
+            if (c + 1u < nc) {
+                rt_wait(min(nc - 2u - c, RT_NBUF - 2u));  // chunks c + 2 .. c + 4 may be in flight
+                read_chunk((c + 1u) % RT_NBUF);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].x, wa[j].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].y, wa[j].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].z, wa[j].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].w, wa[j].w, acc, 0, 0, 0);
+            }
+        }
+        // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m. The wave's
+        // buffers are free: its last LDS reads were waited for before its last MFMAs.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave * kRedStride + ((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[r];
+    } else {
+        // Rotation share of this group's waves 4..7: each wave transforms eight 128-blocks at a
+        // time, an 8-lane group per block holding 16 consecutive values per lane
+        // (gd_fwht128_x16); the blocks b = 8 (first + waves j) + lane / 8.
         const uint32_t nblk = E / 128u, total = n * nblk;
-        const uint32_t waves = gridDim.x * gridDim.y * RT_WAVES;
-        const uint32_t first = (blockIdx.y * gridDim.x + blockIdx.x) * RT_WAVES + wave;
+        const uint32_t waves = gridDim.x * gridDim.y * gridDim.z * RT_WAVES;
+        const uint32_t first = ((z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * RT_WAVES + (wave - RT_WAVES);
         const bool has_signs = a.c[11] != 0xffffffffu;
         const float *S = has_signs ? gd_buf<const float>(a, a.c[11]) + a.c[12] : nullptr;
         uint32_t *XH = gd_buf<uint32_t>(a, a.c[13]) + a.c[14];
@@ -121,50 +183,17 @@ GD_PIPELINE_NAMED(moe_prefill_router, 256) {
             }
         }
     }
-
-    // K loop over this wave's quarter. Rows beyond n or n_expert were staged as copies of the last
-    // row; their operands are zeroed here.
-    const uint32_t m = lane & 31u, h = lane >> 5;
-    const bool tv = t0 + m < n, rv = r0 + m < NE;
-    f32x16 acc = {};
-    for (uint32_t c = 0; c < nc; ++c) {
-        if (c + 1u < nc) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c + 1 may be in flight
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const uint32_t buf = c % RT_NBUF;
-        float4 xv[4], wv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
-            xv[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
-            wv[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float4 av = xv[j], bv = wv[j];
-            if (!tv) av = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (!rv) bv = make_float4(0.f, 0.f, 0.f, 0.f);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
-        }
-        // Chunk c + 2 into the buffer of chunk c - 1, whose reads completed before its MFMAs.
-        if (c + 2u < nc) rt_stage(sm, wave, (c + 2u) % RT_NBUF, X, W, xoff, woff, (c + 2u) * RT_KC * 4u);
-    }
-    // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m.
-#pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave][((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[r];
     __syncthreads();
-    const bool has_bias = a.c[7] != 0xffffffffu;
-    float *L = gd_buf<float>(a, a.c[9]) + a.c[10];
+    const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;
+    float *L = gd_buf<float>(a, a.c[9]) + a.c[10] + (size_t)z * n * NE;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t idx = tid + 256u * q, i = idx >> 5, j = idx & 31u;
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t idx = tid + 512u * q, i = idx >> 5, j = idx & 31u;
         const uint32_t t = t0 + i, r = r0 + j;
         if (t < n && r < NE) {
-            float v = red[0][idx];
+            float v = red[idx];
 #pragma unroll
-            for (int w = 1; w < RT_WAVES; ++w) v += red[w][idx];
+            for (int w = 1; w < RT_WAVES; ++w) v += red[w * kRedStride + idx];
             if (has_bias) v += gd_buf<const float>(a, a.c[7])[a.c[8] + r];
             L[(size_t)t * NE + r] = v;
         }

@@ -1,9 +1,10 @@
 // Prefill path, step 2: top-8 routing of every token, one wave per token.
 // Softmax, top-k with ties to the lower index, and the renormalised weights of
 // src/engine.zig:527-540 and :670-687, computed on the logits as route_fast.h describes.
+// The logits are the sum of S planes (the router's K split), added in plane order.
 // Grid: ceil(n / 4); 256 threads (four tokens per group). Requires n_expert <= 256, top-8.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_tok 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 weights_uav 8 weights_off.
+// 6 ids_off 7 weights_uav 8 weights_off 9 S (0 or 1: one plane) 10 plane stride (floats).
 #include "route_fast.h"
 
 GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
@@ -11,8 +12,16 @@ GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
     const uint32_t NE = a.c[2], n = a.c[3];
     const uint32_t t = blockIdx.x * 4u + wave;
     if (t >= n) return;
+    const uint32_t S = a.c[9] > 1u ? a.c[9] : 1u;
+    const float *lg = gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * NE;
     float v[4];
-    rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * NE, NE, v);
+    rf_load<4>(lg, NE, v);
+    for (uint32_t z = 1; z < S; ++z) {
+        float p[4];
+        rf_load<4>(lg + (size_t)z * a.c[10], NE, p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] += p[j];
+    }
     uint32_t ids[8];
     float wts[8];
     wave_route_fast<4, 8>(v, NE, gd_bits_f32(a.c[4]), ids, wts);

@@ -623,13 +623,19 @@ class Engine {
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
+        // K split of the router: small batches get more groups (up to 256 of 32 x 32 logit tiles),
+        // each K range writing its own logit plane.
+        const uint32_t rt_tiles = ((n + 31) / 32) * ((NE + 31) / 32);
+        uint32_t ks = 1;
+        while (rt_tiles * ks * 2 <= 256 && E % (128 * ks * 2) == 0 && ks * 2 <= 16 && (uint64_t)ks * 2 * n <= max_tok) ks *= 2;
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
-                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0},
-                             (n + 31) / 32, (NE + 31) / 32);
+                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks},
+                             (n + 31) / 32, (NE + 31) / 32, ks);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
-                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0}, (n + 3) / 4);
+                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE},
+                             (n + 3) / 4);
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
                              {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows}, 1);
         if (L.type_id == 144) {
