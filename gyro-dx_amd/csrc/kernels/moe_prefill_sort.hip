@@ -5,7 +5,8 @@
 // stable order: order_start[e] is the exclusive prefix of the expert counts and
 // route_order[order_start[e] + i] is the i-th slot, in increasing slot order, that chose e.
 // One group of 16 waves. The expert ids are first copied into LDS as 16-bit values (every
-// load issued up front). Wave w owns a contiguous run of slots. Pass 1 counts per (wave,
+// load issued up front). Wave w >= 1 owns a contiguous run of slots (wave 0 none: it ranks
+// the partial tiles meanwhile). Pass 1 counts per (wave,
 // expert) with LDS atomics; the counts become per-wave write cursors by a prefix over waves
 // then over experts; pass 2 walks each run again in slot order and places every slot at its
 // cursor plus its rank among the lanes of the same round that chose the same expert; the lanes
@@ -52,17 +53,21 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
 #pragma unroll 8
     for (uint32_t i = tid; i < n_slots; i += 1024u) id16[i] = (uint16_t)min(ids[i], NE - 1u);
     __syncthreads();
-    // Runs of whole rounds of 64 slots per wave.
-    const uint32_t per_wave = ((n_slots + SORT_WAVES * 64u - 1u) / (SORT_WAVES * 64u)) * 64u;
-    const uint32_t s0 = wave * per_wave, s1 = min(s0 + per_wave, n_slots);
+    // Runs of whole rounds of 64 slots per wave. Wave 0 ranks the partial tiles while waves
+    // 1 .. 15 place the slots, so the placement runs have no slots for wave 0.
+    const uint32_t per_wave = ((n_slots + (SORT_WAVES - 1u) * 64u - 1u) / ((SORT_WAVES - 1u) * 64u)) * 64u;
+    const uint32_t s0 = wave == 0u ? n_slots : (wave - 1u) * per_wave, s1 = min(s0 + per_wave, n_slots);
     for (uint32_t s = s0 + lane; s < s1; s += 64u) atomicAdd(&cur[wave][id16[s]], 1u);
     __syncthreads();
-    // Column prefix over waves: cur[w][e] becomes the count of e in runs before w.
-    uint32_t total = 0;
+    // Column prefix over waves, in registers: colp[w] is the count of e in runs before w.
+    uint32_t total = 0, colp[SORT_WAVES];
     if (tid < NE) {
+#pragma unroll
+        for (uint32_t w = 0; w < SORT_WAVES; ++w) colp[w] = cur[w][tid];
+#pragma unroll
         for (uint32_t w = 0; w < SORT_WAVES; ++w) {
-            const uint32_t c = cur[w][tid];
-            cur[w][tid] = total;
+            const uint32_t c = colp[w];
+            colp[w] = total;
             total += c;
         }
     }
@@ -107,8 +112,11 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
     if (tid <= NE) meta[tid] = start[tid];
     if (tid == 0) meta[1023] = tstart[NE];
     // Cursors: segment start plus the counts of earlier runs.
-    if (tid < NE)
-        for (uint32_t w = 0; w < SORT_WAVES; ++w) cur[w][tid] += start[tid];
+    if (tid < NE) {
+        const uint32_t st = start[tid];
+#pragma unroll
+        for (uint32_t w = 0; w < SORT_WAVES; ++w) cur[w][tid] = colp[w] + st;
+    }
     __syncthreads();
     // Rank of each partial tile by decreasing size, ties by expert (wave 0, before its share of
     // the placement): rank = (partial tiles larger than p) + (earlier experts of size p).
