@@ -461,10 +461,11 @@ static_assert(sizeof(GhLds) == 81920, "two groups fill the CU's 160 KB");
 
 struct GhState {
     const void *abase, *wbase;  // activation rows; the layer's slot arena
-    uint32_t roff[2], woff[2];  // per load: lane offset at sub-block / block 0
+    uint32_t roff[2], woff[2];  // per load: lane offset at sub-block / block 0 (woff: the row's first byte)
+    uint32_t wpar[2];           // per load: 1 if its row starts 2 bytes past a 4-byte boundary
     uint32_t nal, nwl;          // activation loads per sub-block (0 or 2), weight loads per block (1 or 2)
     uint32_t wave, m, h, sel, nk;
-    uint32_t wq;                // staged weight row this lane decodes
+    uint32_t wq, qpar;          // staged weight row this lane decodes, and its row's start parity
     uint32_t arow;              // byte of this lane's step-0 A chunk of rows m + 32 rb in buffer 0
 };
 
@@ -494,12 +495,14 @@ __device__ __forceinline__ uint32_t gh_chunk(uint32_t wave, uint32_t lane, int i
     row = wave * 16u + (uint32_t)i * 8u + (lane >> 3);
     return ((lane & 7u) ^ ((row >> 1) & 7u)) * 16u;
 }
-// Weight block kb of the 256 staged rows (as gg_stage_w8).
+// Weight block kb of the 256 staged rows (as gg_stage_w8). Block kb of a row starts at byte
+// 34 kb of it; with an odd block count per row, odd rows start 2 bytes past a 4-byte boundary,
+// so the 4-byte-aligned start of the block lies 2 bytes earlier when (row parity + kb) is odd.
 __device__ __forceinline__ void gh_stage_w(GhLds &sm, uint32_t buf, const GhState &t, uint32_t kb) {
     const uint32_t base = gg_lds_addr(&sm.w[0][0]) + buf * (uint32_t)sizeof(sm.w[0]);
-    const uint32_t kbo = (kb * 34u) & ~3u;
-    gg_dma16(base + gg_w8_load(t.wave, 0) * 1024u, t.wbase, t.woff[0] + kbo);
-    if (t.nwl == 2u) gg_dma16(base + gg_w8_load(t.wave, 1) * 1024u, t.wbase, t.woff[1] + kbo);
+    gg_dma16(base + gg_w8_load(t.wave, 0) * 1024u, t.wbase, t.woff[0] + kb * 34u - 2u * ((t.wpar[0] + kb) & 1u));
+    if (t.nwl == 2u)
+        gg_dma16(base + gg_w8_load(t.wave, 1) * 1024u, t.wbase, t.woff[1] + kb * 34u - 2u * ((t.wpar[1] + kb) & 1u));
 }
 // Step-0 A byte of lane (m, h) in buffer 0 (row m, chunk h).
 __device__ __forceinline__ uint32_t gh_arow(const GhLds &sm, uint32_t m, uint32_t h) {
@@ -574,7 +577,7 @@ __device__ __forceinline__ void gh_kloop(GhLds &sm, const GhState &t, f32x16 (&a
         gh_read_w(sm, kb & 1u, t.wq, wc);
         float sc;
         uint32_t q[8];
-        tq2_unpack(wc.d, (kb & 1u) != 0u, sc, q);
+        tq2_unpack(wc.d, ((t.qpar + kb) & 1u) != 0u, sc, q);
         const half2_t sc2 = {(_Float16)sc, (_Float16)sc};
         uint32_t raw[2][4], pr[2] = {0u, 0u};
         gg_gather(q, 0, t.sel, sm.book, raw[0]);

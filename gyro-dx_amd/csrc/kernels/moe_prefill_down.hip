@@ -12,7 +12,9 @@
 // in fp32 for the k-ordered combine.
 // Grid: (E / 256, max tiles); 512 threads, two groups per CU (80 KB of LDS, at most 128 VGPRs),
 // started tile by tile in the sort's longest-first order; the groups beyond the sort's tile
-// count exit. Requires TQ2_T experts, F % 256 == 0, E % 256 == 0.
+// count exit. Requires TQ2_T experts, F % 128 == 0 with F >= 256 (an odd block count per down
+// row puts odd rows 2 bytes off a 4-byte boundary; the staging and the unpack follow each row's
+// parity), E % 256 == 0.
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 act16_uav 4 act16_off (words) 5 base_lo
 // 6 base_hi 7 slot_stride 8 down_offset (bytes from the bundle start) 9 codebook_srv
 // 10 down32_uav 11 down32_off (words) 12 E 13 F.
@@ -68,7 +70,9 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_down, 512, 4) {
     for (int i = 0; i < 2; ++i) {
         const uint32_t g = gg_w8_load(wave, i) * 64u + lane, q = g / 3u, piece = g - q * 3u;
         t.woff[i] = e * a.c[7] + a.c[8] + (eb * 256u + q) * row_bytes + piece * 16u;
+        t.wpar[i] = ((eb * 256u + q) * t.nk) & 1u;  // F / 128 odd: odd rows start 2 bytes off
     }
+    t.qpar = ((eb * 256u + t.wq) * t.nk) & 1u;
     t.nwl = wave < 4u ? 2u : 1u;
     t.nal = wave < 2u * ((rows + 31u) >> 5) ? 2u : 0u;  // waves whose 16 rows lie in the tile's row blocks
     float *out = gd_buf<float>(a, a.c[10]) + a.c[11];

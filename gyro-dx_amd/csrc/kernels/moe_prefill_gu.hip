@@ -78,7 +78,9 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 4) {
     for (int i = 0; i < 2; ++i) {
         const uint32_t g = gg_w8_load(wave, i) * 64u + lane, q = g / 3u, piece = g - q * 3u;
         t.woff[i] = e * a.c[7] + (q >> 7) * proj_bytes + (fb * 128u + (q & 127u)) * row_bytes + piece * 16u;
+        t.wpar[i] = 0u;  // E / 128 is even: every row starts on a 4-byte boundary
     }
+    t.qpar = 0u;
     t.nwl = wave < 4u ? 2u : 1u;
     t.nal = wave < 2u * ((rows + 31u) >> 5) ? 2u : 0u;  // waves whose 16 rows lie in the tile's row blocks
     // Epilogue operands, loaded now so that no load of the epilogue is issued in the K loop; as

@@ -1,10 +1,12 @@
-// Prefill path, step 2: top-8 routing of every token, one wave per token.
+// Prefill path, step 2: top-U routing of every token (U = n_used <= 16), one wave per token.
 // Softmax, top-k with ties to the lower index, and the renormalised weights of
 // src/engine.zig:527-540 and :670-687, computed on the logits as route_fast.h describes.
 // The logits are the sum of S planes (the router's K split), added in plane order.
-// Grid: ceil(n / 4); 256 threads (four tokens per group). Requires n_expert <= 256, top-8.
+// Grid: ceil(n / 4); 256 threads (four tokens per group). Requires n_expert <= 256,
+// 1 <= n_used <= 16.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_tok 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 weights_uav 8 weights_off 9 S (0 or 1: one plane) 10 plane stride (floats).
+// 6 ids_off 7 weights_uav 8 weights_off 9 S (0 or 1: one plane) 10 plane stride (floats)
+// 11 n_used (0: 8, so that a caller passing 11 constants gets top-8).
 #include "route_fast.h"
 
 GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
@@ -22,18 +24,45 @@ GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] += p[j];
     }
-    uint32_t ids[8];
-    float wts[8];
-    wave_route_fast<4, 8>(v, NE, gd_bits_f32(a.c[4]), ids, wts);
-    if (lane < 8u) {
+    const uint32_t U = a.c[11] ? a.c[11] : 8u;  // uniform, <= 16
+    uint32_t ids[16];
+    float wts[16];
+    if (U == 8u) {
+        wave_route_fast<4, 8>(v, NE, gd_bits_f32(a.c[4]), ids, wts);
+    } else {
+        // Ranks 0 .. U - 1 in order, then the softmax over them in rank order (rf_weights).
+        uint64_t key[4];
+        rf_init<4>(v, NE, key);
+        float top[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if ((uint32_t)k < U) ids[k] = rf_next<4>(key, top[k]);
+        float total = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if ((uint32_t)k < U) {
+                wts[k] = expf(top[k] - top[0]);
+                total += wts[k];
+            }
+        const float inv = 1.0f / total, scale = gd_bits_f32(a.c[4]);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if ((uint32_t)k < U) {
+                float w = wts[k] * inv;
+                if (scale != 0.f && scale != 1.f) w *= scale;
+                wts[k] = w;
+            }
+    }
+    if (lane < U) {
         uint32_t id = ids[0];
         float w = wts[0];
 #pragma unroll
-        for (int j = 1; j < 8; ++j) {
+        for (int j = 1; j < 16; ++j) {
+            if ((uint32_t)j >= U) break;
             id = lane == (uint32_t)j ? ids[j] : id;
             w = lane == (uint32_t)j ? wts[j] : w;
         }
-        gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * 8u + lane] = id;
-        gd_buf<float>(a, a.c[7])[a.c[8] + t * 8u + lane] = w;
+        gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * U + lane] = id;
+        gd_buf<float>(a, a.c[7])[a.c[8] + t * U + lane] = w;
     }
 }

@@ -603,9 +603,12 @@ class Engine {
     // every such product must be finite in binary16. Uniform TQ2_T layers take moe_prefill_gu /
     // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
     // A shared expert runs as moe_prefill_shared (SF a multiple of 64).
+    // TQ2_T layers take F a multiple of 128 (an odd block count per down row is handled), the
+    // type-generic kernels a multiple of 256; top-U for U <= 16.
     bool prefill_supported(const Layer &L) const {
-        return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % 256 == 0 && U == 8 &&
-               NE <= 256 && L.max_scale * max_codebook < 65504.0f;
+        const uint32_t fq = L.type_id == 144 ? 128u : 256u;
+        return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % fq == 0 && F >= 256 && U >= 1 &&
+               U <= 16 && NE <= 256 && L.max_scale * max_codebook < 65504.0f;
     }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
@@ -616,10 +619,11 @@ class Engine {
                      uint32_t res_off = 0) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
-            throw NativeError(-1, "prefill path needs E and F multiples of 256, top-8 of <= 256 experts, a shared "
-                                  "expert (if any) of width a multiple of 64 on E <= 4096 and binary16-finite "
-                                  "scale x codebook products");
-        if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (4096 tokens of top-8)");
+            throw NativeError(-1, "prefill path needs E a multiple of 256, F a multiple of 128 (TQ2_T) or 256 (other "
+                                  "types) and at least 256, top-1 to top-16 of <= 256 experts, a shared expert (if "
+                                  "any) of width a multiple of 64 on E <= 4096 and binary16-finite scale x codebook "
+                                  "products");
+        if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (n x n_used)");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
@@ -634,7 +638,7 @@ class Engine {
                               L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks},
                              (n + 31) / 32, (NE + 31) / 32, ks);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
-                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE},
+                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U},
                              (n + 3) / 4);
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
                              {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows}, 1);

@@ -1,11 +1,12 @@
 """GPU parity of the grouped-GEMM prefill path against the CPU oracle, through the C ABI.
 
-Bar: top-k expert ids identical (tokens whose 8th/9th fp64 router probabilities lie within
-1e-5 relative are reported and excluded); the counting sort (route_order, order_start)
+Bar: top-k expert ids identical (tokens whose U-th/(U+1)-th fp64 router probabilities lie
+within 1e-5 relative are reported and excluded); the counting sort (route_order, order_start)
 identical to the oracle's whenever every token is separable; layer outputs within relative
 RMS 2e-3 and cosine 0.9999 of the oracle's fp32 results. Shapes cover the full layer with the
 Zipf-skewed router, a single token, ragged tile rows, an expert whose segment spans several
-128-row tiles, and a layer without rotations.
+128-row tiles, a layer without rotations, the real model's expert shapes (hidden 2560, F 640,
+top-10) and other odd down-row block counts and top-k widths.
 """
 import numpy as np
 import pytest
@@ -92,6 +93,20 @@ def test_prefill_hot_experts_span_tiles(oracle_mod):
     x = synth.make_tokens(42, 300, layer.E, bf16=True)
     order, start = run_case(oracle_mod, layer, x, 300, "hot experts")
     assert np.diff(start.astype(np.int64)).max() == 300
+
+
+def test_prefill_coder_shapes_top10(oracle_mod):
+    """The real model's expert shapes: hidden 2560, F 640 (five blocks per down row, so odd down
+    rows start 2 bytes off a 4-byte boundary), top-10 routing, with a Zipf-skewed router."""
+    layer = synth.make_layer(71, E=2560, F=640, n_expert=128, n_used=10, zipf=1.1)
+    run_case(oracle_mod, layer, synth.make_tokens(72, 150, layer.E, bf16=True), 160, "coder shapes")
+
+
+def test_prefill_odd_down_blocks_other_top_k(oracle_mod):
+    """F 384 (three blocks per down row) with top-6 and top-16 routing."""
+    for U, n in ((6, 53), (16, 21)):
+        layer = synth.make_layer(80 + U, E=1024, F=384, n_expert=64, n_used=U)
+        run_case(oracle_mod, layer, synth.make_tokens(90 + U, n, layer.E, bf16=True), 64, f"F 384 top-{U}")
 
 
 def test_prefill_without_rotations(oracle_mod):
