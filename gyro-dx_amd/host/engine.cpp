@@ -282,7 +282,7 @@ class Engine {
         table = dev.buffer(T * U * 24, Kind::device);
         xh = dev.buffer(T * E * f, Kind::device);
         gu = dev.buffer(T * U * 2 * F * f, Kind::device);
-        parts = E / 1024 ? E / 1024 : 1;
+        parts = (E + 1023) / 1024;  // K-parts of up to 8 blocks of the decode gate/up kernels
         gu_part = dev.buffer(parts * T * U * 2 * F * f, Kind::device);
         act = dev.buffer(T * U * F * f, Kind::device);
         down = dev.buffer(T * U * E * f, Kind::device);
@@ -551,11 +551,19 @@ class Engine {
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
+    // Uniform TQ2_T layers without a shared expert: E a multiple of 256 up to 4096, F a
+    // multiple of 128 up to 1024, top-1 to top-16 (moe_decode_gu for E a multiple of 1024 and
+    // top-8, moe_decode_gu_g otherwise; moe_decode_down for F 512, top-8 and at most two
+    // K-parts, moe_decode_down_g otherwise). Other layers: the type-generic kernels.
     bool decode_supported(const Layer &L, uint32_t n) const {
+        if (NE > 256 || n > 8) return false;
+        if (!decode_generic_types(L))
+            return E % 256 == 0 && E <= 4096 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
         // A shared expert runs fused into moe_router and moe_decode_down_x.
         const bool shared_ok = !L.SF || (L.SF <= 1024 && L.SF % 256 == 0 && E <= 2048);
-        return E % 1024 == 0 && F == 512 && U == 8 && NE <= 256 && n <= 8 && shared_ok;
+        return E % 1024 == 0 && F == 512 && U == 8 && shared_ok;
     }
+    bool decode_fast_down() const { return F == 512 && U == 8 && parts <= 2; }
     // Layers other than uniform TQ2_T without a shared expert take the type-generic kernels.
     static bool decode_generic_types(const Layer &L) { return L.type_id != 144 || L.SF; }
 
@@ -564,8 +572,10 @@ class Engine {
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
-            throw NativeError(-1, "decode path needs E % 1024 == 0, F == 512, top-8 of <= 256 experts, n <= 8, and "
-                                  "a shared expert (if any) of width <= 1024, a multiple of 256, with E <= 2048");
+            throw NativeError(-1, "decode path needs <= 256 experts and n <= 8; uniform TQ2_T layers E a multiple of "
+                                  "256 up to 4096, F a multiple of 128 up to 1024 and top-1..16; other layers E % 1024 "
+                                  "== 0, F == 512, top-8 and a shared expert (if any) of width <= 1024, a multiple "
+                                  "of 256, with E <= 2048");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
@@ -575,11 +585,11 @@ class Engine {
                               L.SF ? L.sh_gate.srv : 0u, L.SF ? sh_g.uav : 0u},
                              std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 4 + 1 : 0));
         if (!decode_generic_types(L)) {
-            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
+            dispatch_maybe_timed(bracket == 2, marks, E % 1024 == 0 && U == 8 ? "moe_decode_gu" : "moe_decode_gu_g",
                                  {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
                                   base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
                                  F / 64, 2 * parts, n * U);
-            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
+            dispatch_maybe_timed(bracket == 3, marks, decode_fast_down() ? "moe_decode_down" : "moe_decode_down_g",
                                  {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
                                   2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
                                   out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,

@@ -149,3 +149,28 @@ def test_zipf_bias_routing(oracle_mod):
         np.testing.assert_array_equal(ids, tr["route_ids"])
         assert_close(oracle_mod, ref, out, f"zipf path {path}")
     eng.close()
+
+
+@pytest.mark.parametrize("E,F,NE,U", [(2560, 640, 128, 10), (1024, 384, 64, 6), (3072, 1024, 64, 16),
+                                      (2048, 512, 64, 4)])
+def test_decode_path_other_shapes(oracle_mod, E, F, NE, U):
+    """The decode path at the real model's expert shapes (hidden 2560, F 640, top-10: a partial
+    last K-part of the gate/up kernel and moe_decode_down_g) and at other widths and top-k,
+    for 1, 3 and 8 tokens, with the residual of a stack step on the last case."""
+    L = synth.make_layer(200 + U, E=E, F=F, n_expert=NE, n_used=U)
+    ol = oracle_mod.OracleLayer(L)
+    eng = Engine(max_tok=8)
+    try:
+        eng.add_layer(L)
+        for n in (1, 3, 8):
+            x = synth.make_tokens(300 + n + U, n, E)
+            ref, tr = ol.forward(x, trace=True)
+            print(f"decode E={E} F={F} experts={NE} top-{U} n={n}", flush=True)
+            out = eng.forward(0, x, PATH_DECODE)
+            ids, w = eng.last_routes(n)
+            sep = separable(ol, x, U)
+            np.testing.assert_array_equal(ids[sep], tr["route_ids"][sep])
+            np.testing.assert_allclose(w[sep], tr["route_w"][sep], rtol=2e-5, atol=1e-7)
+            assert_close(oracle_mod, ref, out, f"decode E={E} F={F} top-{U} n={n}")
+    finally:
+        eng.close()
