@@ -101,6 +101,22 @@ def test_stack_prefill_path_and_run(oracle_mod, full_stack):
         eng.close()
 
 
+def test_stack_coder_shapes_decode_and_prefill(oracle_mod):
+    """Three layers at the real model's expert shapes (hidden 2560, F 640, top-10) through the
+    decode path (moe_decode_gu_g / moe_decode_down_g, 6 tokens) and the prefill path (48)."""
+    layers = synth.make_stack(4841, 3, E=2560, F=640, n_expert=128, n_used=10)
+    eng, ids = make_engine(layers, 48)
+    try:
+        for path, n, name in ((PATH_DECODE, 6, "decode"), (PATH_PREFILL, 48, "prefill")):
+            x = synth.make_tokens(4842 + n, n, 2560, bf16=True)
+            ref, clear = oracle_stack(oracle_mod, layers, x)
+            print(f"stack coder shapes {name}: 3 layers, {n} tokens", flush=True)
+            out = eng.forward_stack(ids, x, path)
+            check(oracle_mod, f"stack coder shapes {name}", ref, out, clear, min_clear=0.5)
+    finally:
+        eng.close()
+
+
 def test_stack_reference_path(oracle_mod):
     layers = synth.make_stack(4811, 3, E=1024, F=256, n_expert=64, n_used=4)
     layers[1].norm_weight = None  # a layer without norm weight
