@@ -14,7 +14,7 @@ BUILD = ROOT / "gyro-dx_amd" / "build"
 def declared(header, prefix):
     """Function declarations: `<API macro> <return type> <name>(`."""
     text = (ROOT / "include" / header).read_text()
-    return sorted(set(re.findall(rf"\b(?:GD|GM)_API\s+[\w ]+?\*?\s*\b({prefix}[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(rf"\b(?:GD|GM|GG)_API\s+[\w ]+?\*?\s*\b({prefix}[a-z0-9_]+)\s*\(", text)))
 
 
 def exported(lib):
@@ -25,6 +25,7 @@ def exported(lib):
 @pytest.mark.parametrize("lib,header,prefix,count", [
     ("libgyro_native.so", "gyro_native.h", "gd_", 27),
     ("libgyro_moe.so", "gyro_moe.h", "gm_", 15),
+    ("libgyro_moe.so", "gyro_gguf.h", "gg_", 12),
 ])
 def test_exports(lib, header, prefix, count):
     path = BUILD / lib

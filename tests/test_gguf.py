@@ -1,0 +1,96 @@
+"""The GGUF header reader (include/gyro_gguf.h), on the CPU: the cases of src/gguf.zig's own
+tests (expert slices of the real model's down tensor, truncation at every byte, overlapping
+ranges and overflow, duplicate keys and invalid booleans, unknown tensor types), plus metadata,
+alignment and a written file whose expert slices round-trip through gg_open."""
+import numpy as np
+import pytest
+
+from gguf_fixture import GgufBuilder
+from gyrodx import gguf
+
+
+def kind(fn):
+    with pytest.raises(gguf.GgufError) as e:
+        fn()
+    return e.value.kind
+
+
+def test_expert_slices_use_block_bytes_and_absolute_offsets():
+    """The real model's down tensor: 640 x 2560 TQ2_T weights per expert, 256 experts."""
+    f = GgufBuilder().header(1, 0).tensor("blk.0.ffn_down_exps.weight", (640, 2560, 256), 144, 0).pad()
+    payload = 435200 * 256
+    m = gguf.parse(f.bytes(), len(f.bytes()) + payload)
+    off, n = m.expert_range("blk.0.ffn_down_exps.weight", 255)
+    assert n == 435200 == 640 // 128 * 34 * 2560
+    assert off == m.data_offset + 435200 * 255
+    assert kind(lambda: m.expert_range("blk.0.ffn_down_exps.weight", 256)) == "InvalidExpert"
+    full = len(f.bytes()) + payload
+    for end in range(len(f.bytes())):
+        assert kind(lambda: gguf.parse(f.bytes()[:end], full)) == "UnexpectedEnd", end
+
+
+def test_overlapping_ranges_and_overflow():
+    f = GgufBuilder().header(2, 0).tensor("a", (32,), 0, 0).tensor("b", (32,), 0, 32).pad()
+    assert kind(lambda: gguf.parse(f.bytes(), 4096)) == "OverlappingTensors"
+    f = GgufBuilder().header(1, 0).tensor("a", (2 ** 64 - 1, 2), 0, 0).pad()
+    assert kind(lambda: gguf.parse(f.bytes(), 2 ** 64 - 1)) == "IntegerOverflow"
+
+
+def test_duplicate_keys_and_invalid_booleans():
+    f = GgufBuilder().header(0, 2)
+    for _ in range(2):
+        f.str("a").u32(4).u32(1)
+    assert kind(lambda: gguf.parse(f.pad().bytes(), 4096)) == "DuplicateKey"
+    f = GgufBuilder().header(0, 1).str("a").u32(7).u8(2).pad()
+    assert kind(lambda: gguf.parse(f.bytes(), 4096)) == "InvalidBoolean"
+
+
+def test_unknown_tensor_type_keeps_no_size():
+    f = GgufBuilder().header(1, 0).tensor("unknown", (128, 2, 4), 999, 0).pad()
+    m = gguf.parse(f.bytes(), 4096)
+    assert m.tensors()[0].byte_length is None
+    assert kind(lambda: m.expert_range("unknown", 0)) == "UnsupportedTensorType"
+
+
+def test_header_checks_and_metadata():
+    assert kind(lambda: gguf.parse(GgufBuilder().header(0, 0, magic=b"GGUX").pad().bytes(), 64)) == "BadMagic"
+    assert kind(lambda: gguf.parse(GgufBuilder().header(0, 0, version=2).pad().bytes(), 64)) == "UnsupportedVersion"
+    f = GgufBuilder().header(1, 2).kv_u32("general.alignment", 64).kv_str("general.name", "x")
+    f.tensor("t", (128, 3), 145, 64).pad(64)
+    m = gguf.parse(f.bytes(), len(f.bytes()) + 64 + 26 * 3)
+    assert m.alignment == 64 and m.data_offset % 64 == 0 and m.metadata_u64("general.alignment") == 64
+    assert m.tensor("t").byte_length == 26 * 3 and m.tensor("t").file_offset == m.data_offset + 64
+    assert kind(lambda: m.metadata_u64("general.name")) == "InvalidMetadata"
+    f = GgufBuilder().header(1, 1).kv_u32("general.alignment", 48).tensor("t", (4,), 0, 0).pad()
+    assert kind(lambda: gguf.parse(f.bytes(), 4096)) == "InvalidAlignment"
+    f = GgufBuilder().header(1, 0).tensor("t", (4,), 0, 16).pad()
+    assert kind(lambda: gguf.parse(f.bytes(), 4096)) == "InvalidAlignment"
+    assert gguf.is_expert_tensor("blk.3.ffn_up_exps.weight") and not gguf.is_expert_tensor("blk.3.ffn_up.weight")
+
+
+def test_written_file_expert_slices(tmp_path):
+    """A file with three TQ2_T expert tensors: every expert's slice read back through gg_open and
+    the mapped loader equals the bytes written."""
+    rng = np.random.default_rng(5)
+    E, F, NE = 256, 128, 3
+    mats = {"gate": rng.integers(0, 256, (NE, F, E // 128 * 34), dtype=np.uint8),
+            "up": rng.integers(0, 256, (NE, F, E // 128 * 34), dtype=np.uint8),
+            "down": rng.integers(0, 256, (NE, E, F // 128 * 34), dtype=np.uint8)}
+    f = GgufBuilder().header(3, 0)
+    off = 0
+    offs = {}
+    for p, dims in (("gate", (E, F, NE)), ("up", (E, F, NE)), ("down", (F, E, NE))):
+        offs[p] = off
+        f.tensor(f"blk.0.ffn_{p}_exps.weight", dims, 144, off)
+        off += (mats[p].nbytes + 31) // 32 * 32
+    f.pad()
+    data = bytearray(off)
+    for p in mats:
+        data[offs[p]:offs[p] + mats[p].nbytes] = mats[p].tobytes()
+    path = tmp_path / "experts.gguf"
+    path.write_bytes(f.bytes() + bytes(data))
+    got = gguf.load_layer_experts(str(path), 0)
+    assert (got["E"], got["F"], got["n_expert"]) == (E, F, NE)
+    for p in mats:
+        for e in range(NE):
+            np.testing.assert_array_equal(got[p][e], mats[p][e])
