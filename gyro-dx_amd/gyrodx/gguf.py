@@ -23,7 +23,7 @@ class GgufError(RuntimeError):
              -5: "InvalidBoolean", -6: "LimitExceeded", -7: "IntegerOverflow", -8: "InvalidAlignment",
              -9: "InvalidDimensions", -10: "DuplicateKey", -11: "DuplicateTensor", -12: "InvalidTensorRange",
              -13: "OverlappingTensors", -14: "UnsupportedTensorType", -15: "InvalidExpert",
-             -16: "InvalidMetadata", -17: "IO", -18: "NotFound"}
+             -16: "InvalidMetadata", -17: "IO", -18: "NotFound", -19: "UnsupportedGyroMetadata"}
 
     def __init__(self, code: int, what: str):
         self.code = code
@@ -57,6 +57,9 @@ def _lib() -> C.CDLL:
             "gg_expert_range": ([vp, C.c_char_p, u32, C.POINTER(u64), C.POINTER(u64)], C.c_int),
             "gg_is_expert_tensor": ([C.c_char_p], C.c_int),
             "gg_metadata_u64": ([vp, C.c_char_p, C.POINTER(u64)], C.c_int),
+            "gg_metadata_raw": ([vp, C.c_char_p, C.POINTER(u32), C.POINTER(C.POINTER(C.c_uint8)),
+                                 C.POINTER(C.c_size_t)], C.c_int),
+            "gg_validate_gyro": ([vp], C.c_int),
         }
         for name, (args, res) in sigs.items():
             f = getattr(L, name)
@@ -134,6 +137,44 @@ class Model:
         _check(_lib().gg_metadata_u64(self._h, key.encode(), C.byref(v)), f"metadata {key}")
         return v.value
 
+    def has(self, key: str) -> bool:
+        kind = C.c_uint32()
+        return _lib().gg_metadata_raw(self._h, key.encode(), C.byref(kind), None, None) == 0
+
+    def metadata(self, key: str):
+        """A metadata value: int, float, bool, str, or a list of them (one array level)."""
+        kind, raw, n = C.c_uint32(), C.POINTER(C.c_uint8)(), C.c_size_t()
+        _check(_lib().gg_metadata_raw(self._h, key.encode(), C.byref(kind), C.byref(raw), C.byref(n)),
+               f"metadata {key}")
+        b = bytes(raw[:n.value])
+        return _decode(kind.value, b, 0)[0]
+
+    def validate_gyro(self) -> None:
+        _check(_lib().gg_validate_gyro(self._h), "validate_gyro")
+
+
+_SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 10: "<Q", 11: "<q", 12: "<d"}
+
+
+def _decode(kind: int, b: bytes, pos: int):
+    """Value of GGUF type `kind` at b[pos:] (src/gguf.zig:13-17) and the position after it."""
+    import struct
+    if kind in _SCALAR:
+        fmt = _SCALAR[kind]
+        return struct.unpack_from(fmt, b, pos)[0], pos + struct.calcsize(fmt)
+    if kind == 7:
+        return b[pos] == 1, pos + 1
+    if kind == 8:
+        (n,) = struct.unpack_from("<Q", b, pos)
+        return b[pos + 8:pos + 8 + n].decode(), pos + 8 + n
+    et, n = struct.unpack_from("<IQ", b, pos)
+    pos += 12
+    out = []
+    for _ in range(n):
+        v, pos = _decode(et, b, pos)
+        out.append(v)
+    return out, pos
+
 
 def parse(prefix: bytes, file_size: int) -> Model:
     h = C.c_void_p()
@@ -176,3 +217,51 @@ def load_layer_experts(path: str, layer: int) -> dict:
         return out
     finally:
         m.close()
+
+
+def load_layer(path: str, layer: int):
+    """One MoE layer of a GGUF file as a gyrodx.synth.Layer for gm_add_layer: the routed experts
+    (load_layer_experts), the fp32 router "blk.<l>.ffn_gate_inp.weight" (E x n_expert),
+    n_used and the optional expert-weights scale from "<arch>.expert_used_count" /
+    "<arch>.expert_weights_scale" (src/model.zig:262-285), and the explicit Hadamard signs of the
+    gate and down inputs: a tensor listed in prism.hadamard.weight_names takes the run of
+    prism.hadamard.sign_values that belongs to its input width (src/model.zig:306-333). The
+    rotation metadata is validated first (src/gguf.zig:182-250)."""
+    from .synth import Layer
+    m = open_model(path)
+    try:
+        m.validate_gyro()
+        arch = m.metadata("general.architecture")
+        n_used = int(m.metadata(f"{arch}.expert_used_count"))
+        scale = float(m.metadata(f"{arch}.expert_weights_scale")) if m.has(f"{arch}.expert_weights_scale") else 0.0
+        r = m.tensor(f"blk.{layer}.ffn_gate_inp.weight")
+        if r.type_id != 0 or r.rank != 2:
+            raise GgufError(-14, r.name)
+        E, NE = r.dims
+        mm = np.memmap(path, dtype=np.uint8, mode="r")
+        router = np.frombuffer(mm[r.file_offset:r.file_offset + r.byte_length], np.float32).reshape(NE, E)
+
+        def signs(name: str, width: int):
+            if not m.has("prism.hadamard.weight_names") or name not in m.metadata("prism.hadamard.weight_names"):
+                return None
+            if m.metadata("prism.hadamard.sign_mode") != "explicit":
+                return np.ones(width, np.float32)
+            off = 0
+            values = m.metadata("prism.hadamard.sign_values")
+            for w in m.metadata("prism.hadamard.sign_widths"):
+                if w == width:
+                    return np.asarray(values[off:off + w], np.float32)
+                off += w
+            raise GgufError(-16, f"signs of width {width}")
+
+        F = m.tensor(f"blk.{layer}.ffn_down_exps.weight").dims[0]
+        gate_signs = signs(f"blk.{layer}.ffn_gate_exps.weight", E)
+        down_signs = signs(f"blk.{layer}.ffn_down_exps.weight", F)
+    finally:
+        m.close()
+    ex = load_layer_experts(path, layer)
+    if ex["E"] != E or ex["n_expert"] != NE or ex["F"] != F:
+        raise GgufError(-9, "router and expert shapes")
+    return Layer(E=E, F=ex["F"], n_expert=NE, n_used=n_used, types=ex["types"], gate=ex["gate"], up=ex["up"],
+                 down=ex["down"], router=np.ascontiguousarray(router), router_bias=None, gate_signs=gate_signs,
+                 down_signs=down_signs, expert_weights_scale=scale)

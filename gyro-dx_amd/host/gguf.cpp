@@ -212,6 +212,107 @@ void fill(const Tensor &t, gg_tensor_info *out) {
     out->byte_length = t.byte_length;
 }
 
+const Entry *entry(const gg_model *m, const char *key) {
+    for (const auto &e : m->metadata)
+        if (e.key == key) return &e;
+    return nullptr;
+}
+
+// src/gguf.zig:65-110 (Entry accessors) and :163-180 (Model.required / number / text).
+const Entry &required(const gg_model &m, const char *key) {
+    const Entry *e = entry(&m, key);
+    if (!e) throw Fail{GG_INVALID_METADATA};
+    return *e;
+}
+uint64_t number(const gg_model &m, const char *key) {
+    const Entry &e = required(m, key);
+    Cursor c{e.raw.data(), e.raw.size()};
+    switch (e.kind) {
+        case kU8: return c.num<uint8_t>();
+        case kU16: return c.num<uint16_t>();
+        case kU32: return c.num<uint32_t>();
+        case kU64: return c.num<uint64_t>();
+        default: throw Fail{GG_INVALID_METADATA};
+    }
+}
+std::string text(const Entry &e) {
+    if (e.kind != kString) throw Fail{GG_INVALID_METADATA};
+    Cursor c{e.raw.data(), e.raw.size()};
+    return c.str();
+}
+bool boolean(const Entry &e) {
+    if (e.kind != kBool || e.raw.size() != 1) throw Fail{GG_INVALID_METADATA};
+    return e.raw[0] == 1;
+}
+std::vector<std::string> strings(const Entry &e) {
+    if (e.kind != kArray) throw Fail{GG_INVALID_METADATA};
+    Cursor c{e.raw.data(), e.raw.size()};
+    if (c.tag() != kString) throw Fail{GG_INVALID_METADATA};
+    const uint64_t n = c.num<uint64_t>();
+    std::vector<std::string> out;
+    for (uint64_t i = 0; i < n; ++i) out.push_back(c.str());
+    return out;
+}
+std::vector<int32_t> ints32(const Entry &e) {
+    if (e.kind != kArray) throw Fail{GG_INVALID_METADATA};
+    Cursor c{e.raw.data(), e.raw.size()};
+    if (c.tag() != kI32) throw Fail{GG_INVALID_METADATA};
+    const uint64_t n = c.num<uint64_t>();
+    std::vector<int32_t> out;
+    for (uint64_t i = 0; i < n; ++i) out.push_back(c.num<int32_t>());
+    return out;
+}
+
+// src/gguf.zig:182-250.
+void validate_gyro(const gg_model &m) {
+    bool has_gyro = false;
+    for (const auto &t : m.tensors) has_gyro |= t.type_id >= 144 && t.type_id <= 151;
+    if (!has_gyro) return;
+    if (number(m, "agention.trellis.state_bits") != 15) throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    if (number(m, "prism.hadamard.version") != 1) throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    const uint64_t b = number(m, "prism.hadamard.block_size");
+    if (b == 0 || b > 65536 || (b & (b - 1))) throw Fail{GG_INVALID_METADATA};
+    if (text(required(m, "prism.hadamard.transform")) != "normalized-sylvester-walsh-hadamard")
+        throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    if (text(required(m, "prism.hadamard.axis")) != "input-last-dimension") throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    const std::string mode = text(required(m, "prism.hadamard.sign_mode"));
+    const bool expl = mode == "explicit";
+    if (!expl && mode != "identity") throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    const std::vector<std::string> names = strings(required(m, "prism.hadamard.weight_names"));
+    if (names.empty()) throw Fail{GG_INVALID_METADATA};
+    const std::vector<int32_t> widths = expl ? ints32(required(m, "prism.hadamard.sign_widths")) : std::vector<int32_t>{};
+    uint64_t sum = 0;
+    for (size_t i = 0; i < widths.size(); ++i) {
+        const int32_t w = widths[i];
+        if (w <= 0 || (uint64_t)w % b) throw Fail{GG_INVALID_METADATA};
+        for (size_t j = 0; j < i; ++j)
+            if (widths[j] == w) throw Fail{GG_INVALID_METADATA};
+        sum = add(sum, (uint64_t)w);
+    }
+    if (expl) {
+        const std::vector<int32_t> signs = ints32(required(m, "prism.hadamard.sign_values"));
+        if (signs.size() != sum) throw Fail{GG_INVALID_METADATA};
+        for (int32_t v : signs)
+            if (v != 1 && v != -1) throw Fail{GG_INVALID_METADATA};
+    } else if (entry(&m, "prism.hadamard.sign_widths") || entry(&m, "prism.hadamard.sign_values")) {
+        throw Fail{GG_INVALID_METADATA};
+    }
+    std::unordered_set<std::string> seen;
+    for (const auto &name : names) {
+        if (!seen.insert(name).second) throw Fail{GG_INVALID_METADATA};
+        const Tensor *t = find(&m, name.c_str());
+        if (!t || t->dims[0] % b) throw Fail{GG_INVALID_METADATA};
+        if (expl && std::find(widths.begin(), widths.end(), (int32_t)t->dims[0]) == widths.end())
+            throw Fail{GG_INVALID_METADATA};
+    }
+    for (const char *key : {"prism.hadamard.gdn_v_grouped", "prism.hadamard.tied_output"}) {
+        const Entry *e = entry(&m, key);
+        if (e && boolean(*e)) throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+    }
+    if (const Entry *e = entry(&m, "prism.hadamard.inverse_weight_names"))
+        if (!strings(*e).empty()) throw Fail{GG_UNSUPPORTED_GYRO_METADATA};
+}
+
 bool ends_with(const std::string &s, const char *suffix) {
     const size_t n = std::strlen(suffix);
     return s.size() >= n && s.compare(s.size() - n, n, suffix) == 0;
@@ -308,6 +409,25 @@ int gg_metadata_u64(const gg_model *m, const char *key, uint64_t *out) {
         }
     }
     return GG_NOT_FOUND;
+}
+
+int gg_metadata_raw(const gg_model *m, const char *key, uint32_t *kind, const uint8_t **raw, size_t *len) {
+    const Entry *e = m && key ? entry(m, key) : nullptr;
+    if (!e) return GG_NOT_FOUND;
+    if (kind) *kind = e->kind;
+    if (raw) *raw = e->raw.data();
+    if (len) *len = e->raw.size();
+    return GG_OK;
+}
+
+int gg_validate_gyro(const gg_model *m) {
+    if (!m) return GG_INVALID_METADATA;
+    try {
+        validate_gyro(*m);
+    } catch (const Fail &f) {
+        return f.code;
+    }
+    return GG_OK;
 }
 
 }  // extern "C"

@@ -39,6 +39,7 @@ enum gg_error {
     GG_INVALID_METADATA = -16,
     GG_IO = -17, /* the file could not be opened or read (gg_open only) */
     GG_NOT_FOUND = -18,
+    GG_UNSUPPORTED_GYRO_METADATA = -19,
 };
 
 typedef struct gg_model gg_model;
@@ -76,6 +77,15 @@ GG_API int gg_expert_range(const gg_model *m, const char *name, uint32_t expert,
 GG_API int gg_is_expert_tensor(const char *name);
 /* src/gguf.zig:70-77 (Entry.unsigned): an unsigned integer metadata value. */
 GG_API int gg_metadata_u64(const gg_model *m, const char *key, uint64_t *out);
+
+/* A metadata entry's value type (src/gguf.zig:13-17) and its raw value bytes (for arrays: the
+ * element type, the count and the elements), owned by the model. */
+GG_API int gg_metadata_raw(const gg_model *m, const char *key, uint32_t *kind, const uint8_t **raw, size_t *len);
+/* src/gguf.zig:182-250 (Model.validateGyro): the released version-1 rotation metadata of a file
+ * holding Gyro tensors (Trellis state bits 15, normalized Sylvester Walsh-Hadamard blocks along
+ * the input's last dimension, explicit or identity signs, every listed tensor present with a
+ * width the signs cover). 0, GG_INVALID_METADATA or GG_UNSUPPORTED_GYRO_METADATA. */
+GG_API int gg_validate_gyro(const gg_model *m);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,26 @@ class GgufBuilder:
     def kv_str(self, key, v):
         return self.str(key).u32(8).str(v)
 
+    def kv_f32(self, key, v):
+        self.str(key).u32(6)
+        self.b += struct.pack("<f", v)
+        return self
+
+    def kv_bool(self, key, v):
+        return self.str(key).u32(7).u8(1 if v else 0)
+
+    def kv_i32s(self, key, vals):
+        self.str(key).u32(9).u32(5).u64(len(vals))
+        for v in vals:
+            self.b += struct.pack("<i", int(v))
+        return self
+
+    def kv_strs(self, key, vals):
+        self.str(key).u32(9).u32(8).u64(len(vals))
+        for v in vals:
+            self.str(v)
+        return self
+
     def tensor(self, name, dims, type_id, offset):
         self.str(name).u32(len(dims))
         for d in dims:
@@ -48,3 +68,43 @@ class GgufBuilder:
 
     def bytes(self):
         return bytes(self.b)
+
+
+def write_layer_file(path, L, arch="gyrotest"):
+    """One MoE layer as a GGUF file: blk.0.ffn_gate_inp.weight (fp32 router, dims (E, n_expert)),
+    blk.0.ffn_{gate,up,down}_exps.weight (Gyro experts), the expert counts and scale under
+    `arch`, and the released rotation metadata with explicit signs for widths E (gate, up) and
+    F (down)."""
+    import numpy as np
+    ty = int(L.types[0, 0])
+    names = [f"blk.0.ffn_{p}_exps.weight" for p in ("gate", "up", "down")]
+    kv = [("general.alignment", "u32", 32), ("general.architecture", "str", arch),
+          (f"{arch}.expert_count", "u32", L.n_expert), (f"{arch}.expert_used_count", "u32", L.n_used),
+          ("agention.trellis.state_bits", "u32", 15), ("prism.hadamard.version", "u32", 1),
+          ("prism.hadamard.block_size", "u32", 128),
+          ("prism.hadamard.transform", "str", "normalized-sylvester-walsh-hadamard"),
+          ("prism.hadamard.axis", "str", "input-last-dimension"), ("prism.hadamard.sign_mode", "str", "explicit"),
+          ("prism.hadamard.weight_names", "strs", [names[0], names[1], names[2]]),
+          ("prism.hadamard.sign_widths", "i32s", [L.E, L.F]),
+          ("prism.hadamard.sign_values", "i32s", list(L.gate_signs.astype(int)) + list(L.down_signs.astype(int)))]
+    if L.expert_weights_scale:
+        kv.append((f"{arch}.expert_weights_scale", "f32", L.expert_weights_scale))
+    f = GgufBuilder().header(4, len(kv))
+    for key, kind, v in kv:
+        {"u32": f.kv_u32, "str": f.kv_str, "strs": f.kv_strs, "i32s": f.kv_i32s, "f32": f.kv_f32}[kind](key, v)
+    blobs = [("blk.0.ffn_gate_inp.weight", (L.E, L.n_expert), 0, np.ascontiguousarray(L.router, np.float32)),
+             (names[0], (L.E, L.F, L.n_expert), ty, np.stack(L.gate)),
+             (names[1], (L.E, L.F, L.n_expert), ty, np.stack(L.up)),
+             (names[2], (L.F, L.E, L.n_expert), ty, np.stack(L.down))]
+    off, offs = 0, []
+    for name, dims, t, arr in blobs:
+        f.tensor(name, dims, t, off)
+        offs.append(off)
+        off += (arr.nbytes + 31) // 32 * 32
+    f.pad()
+    data = bytearray(off)
+    for (_, _, _, arr), o in zip(blobs, offs):
+        data[o:o + arr.nbytes] = arr.tobytes()
+    with open(path, "wb") as fh:
+        fh.write(f.bytes())
+        fh.write(bytes(data))

@@ -1,7 +1,8 @@
 """The GGUF header reader (include/gyro_gguf.h), on the CPU: the cases of src/gguf.zig's own
 tests (expert slices of the real model's down tensor, truncation at every byte, overlapping
 ranges and overflow, duplicate keys and invalid booleans, unknown tensor types), plus metadata,
-alignment and a written file whose expert slices round-trip through gg_open."""
+alignment, a written file whose expert slices round-trip through gg_open, and the rotation
+metadata check of src/gguf.zig:182-250."""
 import numpy as np
 import pytest
 
@@ -94,3 +95,52 @@ def test_written_file_expert_slices(tmp_path):
     for p in mats:
         for e in range(NE):
             np.testing.assert_array_equal(got[p][e], mats[p][e])
+
+
+def gyro_meta(f, names, widths, signs, **over):
+    kv = {"agention.trellis.state_bits": ("u32", 15), "prism.hadamard.version": ("u32", 1),
+          "prism.hadamard.block_size": ("u32", 128),
+          "prism.hadamard.transform": ("str", "normalized-sylvester-walsh-hadamard"),
+          "prism.hadamard.axis": ("str", "input-last-dimension"), "prism.hadamard.sign_mode": ("str", "explicit"),
+          "prism.hadamard.weight_names": ("strs", names), "prism.hadamard.sign_widths": ("i32s", widths),
+          "prism.hadamard.sign_values": ("i32s", signs)}
+    kv.update(over)
+    kv = {k: v for k, v in kv.items() if v is not None}
+    return kv
+
+
+def gyro_file(**over):
+    kv = gyro_meta(None, ["w"], [128], [1, -1] * 64, **over)
+    f = GgufBuilder().header(1, len(kv))
+    for k, (kind, v) in kv.items():
+        {"u32": f.kv_u32, "str": f.kv_str, "strs": f.kv_strs, "i32s": f.kv_i32s, "bool": f.kv_bool}[kind](k, v)
+    f.tensor("w", (128, 4), 144, 0).pad()
+    return gguf.parse(f.bytes(), len(f.bytes()) + 4 * 34)
+
+
+def test_validate_gyro_metadata():
+    """src/gguf.zig:182-250: the released version-1 rotation metadata is accepted; each departure
+    is refused with the reference's error kind."""
+    gyro_file().validate_gyro()
+    assert kind(lambda: gyro_file(**{"agention.trellis.state_bits": ("u32", 16)}).validate_gyro()) == "UnsupportedGyroMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.block_size": ("u32", 96)}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.axis": ("str", "output")}).validate_gyro()) == "UnsupportedGyroMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.sign_values": ("i32s", [1, 0] * 64)}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.sign_values": ("i32s", [1] * 127)}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.weight_names": ("strs", ["w", "w"])}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.weight_names": ("strs", ["missing"])}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.sign_widths": ("i32s", [256]),
+                                     "prism.hadamard.sign_values": ("i32s", [1] * 256)}).validate_gyro()) == "InvalidMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.sign_mode": ("str", "identity")}).validate_gyro()) == "InvalidMetadata"
+    gyro_file(**{"prism.hadamard.sign_mode": ("str", "identity"), "prism.hadamard.sign_widths": None,
+                 "prism.hadamard.sign_values": None}).validate_gyro()
+    assert kind(lambda: gyro_file(**{"prism.hadamard.tied_output": ("bool", True)}).validate_gyro()) == "UnsupportedGyroMetadata"
+    assert kind(lambda: gyro_file(**{"prism.hadamard.transform": None}).validate_gyro()) == "InvalidMetadata"
+
+
+def test_metadata_values():
+    m = gyro_file()
+    assert m.metadata("prism.hadamard.weight_names") == ["w"]
+    assert m.metadata("prism.hadamard.sign_values")[:4] == [1, -1, 1, -1]
+    assert m.metadata("prism.hadamard.axis") == "input-last-dimension"
+    assert m.has("prism.hadamard.version") and not m.has("nope")
