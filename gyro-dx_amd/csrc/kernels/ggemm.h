@@ -229,7 +229,8 @@ __device__ __forceinline__ void gx_gather_piece(const uint32_t (&w)[gyro_nw<ID>(
 struct GxState {
     const void *xbase;                   // activation rows
     const void *wb[2];                   // matrix of each of this wave's weight loads
-    uint32_t roff[4], woff[2], wbb[2];   // per load: lane offset at block 0, block bytes
+    uint32_t roff[4], woff[2], wbb[2];   // per load: lane offset at block 0 (the row's first byte), block bytes
+    uint32_t wpar[2], qpar;              // row start parity (2 bytes past a 4-byte boundary) per load, decode row
     uint32_t nwl;                        // weight loads per block of this wave (1 or 2)
     uint32_t nal;                        // activation loads per block of this wave (0 or 4)
     uint32_t wave, m, h, nk;
@@ -242,12 +243,14 @@ __device__ __forceinline__ void gx_sync(const GxState &t, uint32_t kb) { gg_sync
 
 // Stages K block kb into buffer buf: the wave's activation loads (if any), then its weight loads w and
 // (nwl == 2) w + 8 at LDS byte 1024 L of the weight buffer; block kb of a row starts at its
-// matrix row's byte (kb BB) & ~3.
+// row's byte kb BB (every BB is 2 mod 4), whose 4-byte-aligned start lies 2 bytes earlier when the
+// row's start parity plus kb is odd.
 __device__ __forceinline__ void gx_stage(GxLds &sm, uint32_t buf, const GxState &t, uint32_t kb) {
     if (t.nal) gg_stage_a8(sm, buf, t.wave, t.xbase, t.roff, kb);
     const uint32_t base = gg_lds_addr(&sm.w[buf][0]);
-    gg_dma16(base + t.wave * 1024u, t.wb[0], t.woff[0] + ((kb * t.wbb[0]) & ~3u));
-    if (t.nwl == 2u) gg_dma16(base + (t.wave + 8u) * 1024u, t.wb[1], t.woff[1] + ((kb * t.wbb[1]) & ~3u));
+    gg_dma16(base + t.wave * 1024u, t.wb[0], t.woff[0] + kb * t.wbb[0] - 2u * ((t.wpar[0] + kb) & 1u));
+    if (t.nwl == 2u)
+        gg_dma16(base + (t.wave + 8u) * 1024u, t.wb[1], t.woff[1] + kb * t.wbb[1] - 2u * ((t.wpar[1] + kb) & 1u));
 }
 
 // K block kb from buffer BUF for NRB 32-row blocks with blocks of Gyro type ID, in the software
@@ -270,11 +273,11 @@ __device__ __forceinline__ void gx_step(GxLds &sm, const GxState &t, uint32_t kb
     uint32_t w[NW], raw[2][4], pr[2] = {0u, 0u};  // gathers of even and odd steps, two steps ahead
     const uint32_t sel = gg_sel(t.h);
     if constexpr (ID == 144) {
-        tq2_unpack(d, (kb & 1u) != 0u, sc, w);
+        tq2_unpack(d, ((t.qpar + kb) & 1u) != 0u, sc, w);
         gg_gather(w, 0, sel, sm.book, raw[0]);
         gg_gather(w, 1, sel, sm.book, raw[1]);
     } else {
-        gyro_unpack<ID>(d, (kb & 1u) != 0u, sc, w);
+        gyro_unpack<ID>(d, ((t.qpar + kb) & 1u) != 0u, sc, w);
         gx_half_stream<ID>(w, t.h);
 #pragma unroll
         for (int s0 = 0; s0 < 2; ++s0) {

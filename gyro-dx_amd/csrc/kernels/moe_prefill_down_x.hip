@@ -70,7 +70,9 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_down_x, 512, 2) {
         t.wb[i] = down;
         t.wbb[i] = bb;
         t.woff[i] = (eb * 256u + r) * row_bytes + piece * 16u;
+        t.wpar[i] = ((eb * 256u + r) * t.nk) & 1u;  // F / 128 odd: odd rows start 2 bytes off
     }
+    t.qpar = ((eb * 256u + wave * 32u + t.m) * t.nk) & 1u;
     __syncthreads();  // codebook and slot numbers
     t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
     gx_stage(sm, 0, t, 0);

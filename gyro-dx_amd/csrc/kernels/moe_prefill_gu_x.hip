@@ -84,7 +84,9 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu_x, 512, 2) {
         t.wb[i] = reinterpret_cast<const void *>(is_up ? upm : gate);
         t.wbb[i] = bb;
         t.woff[i] = (fb * 128u + r) * ((E / 128u) * bb) + piece * 16u;
+        t.wpar[i] = 0u;  // E / 128 is even: every row starts on a 4-byte boundary
     }
+    t.qpar = 0u;
     t.nal = gg_a_loads(wave, (rows + 31u) >> 5);
     gx_stage(sm, 0, t, 0);
     if (t.nk > 1u) gx_stage(sm, 1, t, 1);

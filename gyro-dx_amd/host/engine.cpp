@@ -613,11 +613,9 @@ class Engine {
     // every such product must be finite in binary16. Uniform TQ2_T layers take moe_prefill_gu /
     // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
     // A shared expert runs as moe_prefill_shared (SF a multiple of 64).
-    // TQ2_T layers take F a multiple of 128 (an odd block count per down row is handled), the
-    // type-generic kernels a multiple of 256; top-U for U <= 16.
+    // F a multiple of 128 (an odd block count per down row is handled), top-U for U <= 16.
     bool prefill_supported(const Layer &L) const {
-        const uint32_t fq = L.type_id == 144 ? 128u : 256u;
-        return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % fq == 0 && F >= 256 && U >= 1 &&
+        return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % 128 == 0 && F >= 256 && U >= 1 &&
                U <= 16 && NE <= 256 && L.max_scale * max_codebook < 65504.0f;
     }
 
@@ -629,8 +627,7 @@ class Engine {
                      uint32_t res_off = 0) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
-            throw NativeError(-1, "prefill path needs E a multiple of 256, F a multiple of 128 (TQ2_T) or 256 (other "
-                                  "types) and at least 256, top-1 to top-16 of <= 256 experts, a shared expert (if "
+            throw NativeError(-1, "prefill path needs E a multiple of 256, F a multiple of 128 and at least 256, top-1 to top-16 of <= 256 experts, a shared expert (if "
                                   "any) of width a multiple of 64 on E <= 4096 and binary16-finite scale x codebook "
                                   "products");
         if (n * U > 32768u) throw NativeError(-1, "prefill calls take at most 32768 token slots (n x n_used)");

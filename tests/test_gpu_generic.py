@@ -97,6 +97,18 @@ def test_prefill_path_uniform_other_types(oracle_mod, type_id):
     check(oracle_mod, layer, synth.make_tokens(141 + type_id, 200, layer.E), PATH_PREFILL, f"prefill type {type_id}")
 
 
+@pytest.mark.parametrize("type_id,E,F,NE,U", [(148, 2560, 640, 64, 10), (0, 1024, 384, 64, 6)])
+def test_prefill_path_generic_types_odd_down_blocks(oracle_mod, type_id, E, F, NE, U):
+    """The type-generic prefill GEMMs with an odd block count per down row (F 640 and 384: odd
+    rows start 2 bytes off a 4-byte boundary) and other top-k widths: a uniform 64-step type at
+    the real model's hidden 2560 / F 640 / top-10, and mixed types (type_id 0) at F 384, top-6."""
+    from gyrodx.engine import PATH_PREFILL
+    kw = dict(mixed_types=True) if type_id == 0 else dict(type_id=type_id)
+    layer = synth.make_layer(160 + U, E=E, F=F, n_expert=NE, n_used=U, **kw)
+    check(oracle_mod, layer, synth.make_tokens(161 + U, 90, layer.E), PATH_PREFILL,
+          f"prefill type {type_id or 'mixed'} E={E} F={F} top-{U}")
+
+
 def test_prefill_refuses_fp16_overflowing_scales_any_type():
     """A block scale of any Gyro type whose products with the codebook overflow binary16 makes the
     prefill path refuse the layer."""
