@@ -559,10 +559,12 @@ class Engine {
         if (NE > 256 || n > 8) return false;
         if (!decode_generic_types(L))
             return E % 256 == 0 && E <= 4096 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
-        // A shared expert runs fused into moe_router and moe_decode_down_x.
-        const bool shared_ok = !L.SF || (L.SF <= 1024 && L.SF % 256 == 0 && E <= 2048);
-        return E % 1024 == 0 && F == 512 && U == 8 && shared_ok;
+        // A shared expert runs fused into moe_router and moe_decode_down_x (hidden 2048-class
+        // shapes); other shapes take moe_decode_gu_xg / moe_decode_down_xg without one.
+        if (decode_generic_tuned()) return !L.SF || (L.SF <= 1024 && L.SF % 256 == 0 && E <= 2048);
+        return !L.SF && E % 256 == 0 && E <= 4096 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
     }
+    bool decode_generic_tuned() const { return E % 1024 == 0 && F == 512 && U == 8; }
     bool decode_fast_down() const { return F == 512 && U == 8 && parts <= 2; }
     // Layers other than uniform TQ2_T without a shared expert take the type-generic kernels.
     static bool decode_generic_types(const Layer &L) { return L.type_id != 144 || L.SF; }
@@ -572,10 +574,10 @@ class Engine {
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
         const Layer &L = layers.at(il);
         if (!decode_supported(L, n))
-            throw NativeError(-1, "decode path needs <= 256 experts and n <= 8; uniform TQ2_T layers E a multiple of "
-                                  "256 up to 4096, F a multiple of 128 up to 1024 and top-1..16; other layers E % 1024 "
-                                  "== 0, F == 512, top-8 and a shared expert (if any) of width <= 1024, a multiple "
-                                  "of 256, with E <= 2048");
+            throw NativeError(-1, "decode path needs <= 256 experts, n <= 8, E a multiple of 256 up to 4096, F a "
+                                  "multiple of 128 up to 1024 and top-1..16; a shared expert (on a layer of another "
+                                  "type than uniform TQ2_T) needs E % 1024 == 0, F == 512, top-8, width <= 1024, "
+                                  "a multiple of 256, and E <= 2048");
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
@@ -597,10 +599,18 @@ class Engine {
                                  E / 8, n);
             return;
         }
-        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_x",
+        dispatch_maybe_timed(bracket == 2, marks, decode_generic_tuned() ? "moe_decode_gu_x" : "moe_decode_gu_xg",
                              {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
                               L.xtab.srv, codebook.srv, gu_part.uav, 0, E, F, n},
                              F / 64, 2 * parts, n * U);
+        if (!decode_generic_tuned()) {
+            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_xg",
+                                 {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
+                                  L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
+                                  st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
+                                 E / 8, n);
+            return;
+        }
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
                              {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
