@@ -1,5 +1,5 @@
 // Matrix-vector products for up to 8 token rows: y[t][r] = act(scale * W[r] . x[t]) (+= y with
-// mode 1). Replaces mv_f32 and mv_bf16 of shaders/engine/mv.hlsl:4-54,123-182 with the same
+// mode 1). Replaces mv_f32, mv_bf16 and mv_q8 of shaders/engine/mv.hlsl:4-92,123-182 with the same
 // constants (C): 0 w_srv, 1 w_off (bytes), 2 rows, 3 cols, 4 x_uav, 5 x_off, 6 x_stride,
 // 7 n_tok, 8 y_uav, 9 y_off, 10 y_stride, 11 mode, 12 act, 13 scale (fp32 bits), 14 row_bytes,
 // 15 rows_per_wave.
@@ -13,7 +13,11 @@
 #define MV_MAX_TOK 8
 #define MV_STAGED 16384
 
-template <bool BF16>
+// Row formats: fp32; bf16; Q8_0 repacked as `cols` int8 quants followed by cols / 32 binary16
+// scales (q8_repack), row_bytes = cols + cols / 16.
+enum { MV_F32 = 0, MV_BF16 = 1, MV_Q8 = 2 };
+
+template <int KIND>
 __device__ __forceinline__ void mv_body(const GdArgs &a) {
     __shared__ float gx[MV_STAGED];
     const uint32_t rows = a.c[2], cols = a.c[3], n_tok = a.c[7] < MV_MAX_TOK ? a.c[7] : MV_MAX_TOK;
@@ -33,7 +37,8 @@ __device__ __forceinline__ void mv_body(const GdArgs &a) {
         }
         __syncthreads();
     }
-    constexpr uint32_t per = BF16 ? 8u : 4u;  // values per lane per step
+    // Values per lane per step: 16 bytes of the row (a Q8 lane's 16 quants lie in one 32-block).
+    constexpr uint32_t per = KIND == MV_Q8 ? 16u : KIND == MV_BF16 ? 8u : 4u;
     for (uint32_t half = 0; half < 2; ++half) {
         const uint32_t ref_wave = wave * 2u + half;
         for (uint32_t rr = 0; rr < rpw; ++rr) {
@@ -45,7 +50,16 @@ __device__ __forceinline__ void mv_body(const GdArgs &a) {
             const uint8_t *wr = W + (size_t)row * row_bytes;
             for (uint32_t c = lane * per; c < cols; c += 64u * per) {
                 float v[per];
-                if (BF16) {
+                if (KIND == MV_Q8) {
+                    const uint4 raw = *reinterpret_cast<const uint4 *>(wr + c);
+                    const float d = gd_half(*reinterpret_cast<const uint16_t *>(wr + cols + (c / 32u) * 2u));
+                    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b)
+                            v[4 * j + b] = d * (float)((int32_t)(w4[j] << (24 - 8 * b)) >> 24);
+                } else if (KIND == MV_BF16) {
                     const uint4 raw = *reinterpret_cast<const uint4 *>(wr + c * 2u);
                     const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll

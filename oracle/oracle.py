@@ -237,3 +237,27 @@ def cosine(ref, cand) -> float:
     cand = np.asarray(cand, dtype=np.float64).ravel()
     na, nb = float(np.dot(ref, ref)), float(np.dot(cand, cand))
     return float(np.dot(ref, cand)) / (na * nb) ** 0.5 if na > 0 and nb > 0 else 1.0
+
+
+def q8_0_decode_rows(src: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Q8_0 rows (34-byte blocks: binary16 scale d, 32 int8 quants q) to fp32, w = d * q
+    (src/kernels.zig:107-120, decodeRow of type_q8_0)."""
+    b = np.ascontiguousarray(src, np.uint8).reshape(rows, cols // 32, 34)
+    d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
+    q = b[:, :, 2:].view(np.int8).astype(np.float32)
+    return (d * q).reshape(rows, cols)
+
+
+def q8_repack(src: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The device layout of shaders/engine/mv.hlsl:94-119: per row the cols int8 quants, then the
+    cols / 32 binary16 scales; row bytes cols + cols / 16."""
+    b = np.ascontiguousarray(src, np.uint8).reshape(rows, cols // 32, 34)
+    return np.concatenate([b[:, :, 2:].reshape(rows, cols), b[:, :, :2].reshape(rows, cols // 16)], axis=1)
+
+
+def q8_repacked_decode(packed: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """fp32 weights of repacked Q8_0 rows (mv.hlsl:64-76: d of block c / 32 times the quant)."""
+    p = np.ascontiguousarray(packed, np.uint8).reshape(rows, cols + cols // 16)
+    q = p[:, :cols].view(np.int8).astype(np.float32)
+    d = p[:, cols:].copy().view(np.float16).astype(np.float32)
+    return q * np.repeat(d, 32, axis=1)

@@ -54,7 +54,7 @@ def test_struct_layouts():
 
 def test_kernels_built():
     kernels = {p.stem for p in (BUILD / "kernels").glob("*.co")}
-    reference = {"mv_f32", "mv_bf16", "moe_route", "moe_resolve", "moe_gyro", "moe_act", "rotate128",
+    reference = {"mv_f32", "mv_bf16", "mv_q8", "q8_repack", "moe_route", "moe_resolve", "moe_gyro", "moe_act", "rotate128",
                  "moe_combine", "ew", "gyro_decode", "linalg_smoke", "moe_gyro_x"}
     fast = {"moe_router", "moe_decode_gu", "moe_decode_down", "moe_dequant", "moe_prefill_router",
             "moe_prefill_topk", "moe_prefill_sort", "moe_prefill_gu", "moe_prefill_down", "moe_prefill_combine",
