@@ -80,6 +80,7 @@ def write_layer_file(path, L, arch="gyrotest"):
     names = [f"blk.0.ffn_{p}_exps.weight" for p in ("gate", "up", "down")]
     kv = [("general.alignment", "u32", 32), ("general.architecture", "str", arch),
           (f"{arch}.expert_count", "u32", L.n_expert), (f"{arch}.expert_used_count", "u32", L.n_used),
+          (f"{arch}.block_count", "u32", 1),
           ("agention.trellis.state_bits", "u32", 15), ("prism.hadamard.version", "u32", 1),
           ("prism.hadamard.block_size", "u32", 128),
           ("prism.hadamard.transform", "str", "normalized-sylvester-walsh-hadamard"),
