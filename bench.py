@@ -361,6 +361,68 @@ def mixed_bench(args):
     return res
 
 
+def coder_bench(args):
+    """The real model's routed-expert shape (hidden 2560, 256 experts, top-10, F 640) in TQ2_T
+    (decode on moe_decode_gu_g / moe_decode_down_g) and in a 64-step type, GGUF 148 (decode on
+    moe_decode_gu_xg / moe_decode_down_xg): batch-1 decode over cycled layer copies, a
+    1024-token prefill, per-kernel times, and parity of 16 decode tokens with the oracle."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from gyrodx import synth
+    from gyrodx.engine import PATH_DECODE, PATH_PREFILL, Engine
+
+    cE, cF, cNE, cU = 2560, 640, 256, 10
+    out = {}
+    for type_id, kernels in ((144, ("moe_decode_gu_g", "moe_decode_down_g")),
+                             (148, ("moe_decode_gu_xg", "moe_decode_down_xg"))):
+        layer = synth.make_layer(args.seed + type_id, E=cE, F=cF, n_expert=cNE, n_used=cU, type_id=type_id)
+        eng = Engine(max_tok=PREFILL_TOKENS)
+        ids = [eng.add_layer(layer) for _ in range(args.copies)]
+        steps = args.mixed_steps
+        x = synth.make_tokens(args.seed + type_id + 1, steps + 16, E=cE)
+        eng.set_tokens(x)
+        eng.run(PATH_DECODE, 1, 16, ids, first=0)
+        dev_ms, wall_ms, _ = eng.run(PATH_DECODE, 1, steps, ids, first=16)
+        gpu = eng.read_outputs(steps + 16)[16:]
+        kus = {}
+        for name, br in (("router", 1), (kernels[0], 2), (kernels[1], 3)):
+            kus[name] = round(eng.run(PATH_DECODE, 1, steps, ids, bracket=br, first=16)[2], 3)
+        expert_bytes = []
+        for t in range(32):
+            eng.forward(ids[0], x[16 + t:17 + t], PATH_DECODE)
+            r, _ = eng.last_routes(1)
+            expert_bytes.append(sum(layer.expert_bytes(int(e)) for e in r[0]))
+        step_s = wall_ms / steps * 1e-3
+        per_tok = float(np.mean(expert_bytes)) + cNE * cE * 4
+        rec = {"decode": {"tok_s": round(1.0 / step_s, 1), "us_per_token": round(step_s * 1e6, 2),
+                          "kernel_us": kus, "bytes_per_token": int(per_tok),
+                          "hbm_gbs": round(per_tok / step_s / 1e9, 1),
+                          "roofline": {"bound": "hbm", "frac": round(per_tok / step_s / 1e9 / HBM_PEAK_GBS, 4)}}}
+        calls = 8
+        xp = synth.make_tokens(args.seed + type_id + 2, PREFILL_TOKENS * calls, E=cE, bf16=True)
+        eng.set_tokens(xp)
+        eng.run(PATH_PREFILL, PREFILL_TOKENS, 2, ids, first=0)
+        pdev, pwall, _ = eng.run(PATH_PREFILL, PREFILL_TOKENS, calls, ids, first=0)
+        flops = PREFILL_TOKENS * cU * 3 * 2 * cE * cF
+        dev_s = pdev / calls * 1e-3
+        pus = {}
+        for name, br in (("router", 1), ("topk", 4), ("sort", 5), ("gate/up", 2), ("down", 3), ("combine", 6)):
+            pus[name] = round(eng.run(PATH_PREFILL, PREFILL_TOKENS, calls, ids, bracket=br, first=0)[2], 3)
+        rec["prefill"] = {"tokens": PREFILL_TOKENS, "calls": calls, "tok_s": round(PREFILL_TOKENS * calls / pwall * 1e3, 1),
+                          "device_us_per_call": round(dev_s * 1e6, 2), "kernel_us": pus, "flops_per_call": flops,
+                          "roofline": {"bound": "mfma", "frac": round(flops / dev_s / 1e12 / MFMA_PEAK_TFLOPS, 4)}}
+        eng.close()
+        if not args.no_cpu:
+            ol = oracle.OracleLayer(layer)
+            ref = ol.forward(x[16:32], threads=cpu_threads())
+            rec["parity"] = {"decode_tokens": 16, "rel_rms": oracle.rel_rms(ref, gpu[:16]),
+                             "cosine": oracle.cosine(ref, gpu[:16])}
+        out[f"type_{type_id}"] = rec
+        print(f"coder shape, type {type_id}: {json.dumps(rec)}", file=sys.stderr, flush=True)
+    return {"workload": f"routed experts at hidden {cE}, {cNE} experts, top-{cU}, F {cF}; "
+                        f"{args.copies} layer copies cycled", **out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -379,6 +441,8 @@ def main() -> int:
     ap.add_argument("--mixed", action="store_true",
                     help="the mixed-quant layer with the shared expert, printed as its own JSON line")
     ap.add_argument("--mixed-steps", type=int, default=500)
+    ap.add_argument("--coder", action="store_true",
+                    help="the real model's expert shape (2560 / 640 / top-10) in TQ2_T and GGUF 148; prints its own JSON line")
     ap.add_argument("--stack-batches", default="1,8,32,64,4096", help="sweep points of --stack (of 1,8,32,64,4096)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
@@ -397,6 +461,9 @@ def main() -> int:
         return 0
     if args.mixed:
         print(json.dumps({"mixed": mixed_bench(args)}), flush=True)
+        return 0
+    if args.coder:
+        print(json.dumps({"coder": coder_bench(args)}), flush=True)
         return 0
     layer = synth.make_layer(args.seed)
     if args.prefill_only:
