@@ -49,17 +49,36 @@ def compile_runtime() -> str:
     return out.name
 
 
+# Host sources compiled as HIP: engine.cpp defines the device scratch array of the
+# no-allocation entry point (its only device code). The others are plain C++.
+HIP_HOST_SOURCES = {"engine.cpp"}
+
+
 def compile_host() -> str:
     out = BUILD / "libgyro_moe.so"
     srcs = sorted((HERE / "host").glob("*.cpp"))
     if not srcs:
         return "(no host sources)"
-    cmd = ["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wno-unused-parameter",
-           "-I", str(ROOT / "include"), "-I", str(HERE / "host"), "-o", str(out), *map(str, srcs),
-           f"-L{BUILD}", "-lgyro_native", "-Wl,-rpath,$ORIGIN"]
+    objdir = BUILD / "host_obj"
+    objdir.mkdir(parents=True, exist_ok=True)
+    inc = ["-I", str(ROOT / "include"), "-I", str(HERE / "host")]
+    objs = []
+    for src in srcs:
+        obj = objdir / (src.stem + ".o")
+        if src.name in HIP_HOST_SOURCES:
+            cmd = [HIPCC, f"--offload-arch={ARCH}", "-x", "hip", "-O2", "-fPIC", "-std=c++17", "-Wall",
+                   "-Wno-unused-parameter", *NO_PACKED, *inc, "-c", "-o", str(obj), str(src)]
+        else:
+            cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-parameter", *inc, "-c", "-o", str(obj),
+                   str(src)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"host {src.name}:\n{r.stderr}")
+        objs.append(str(obj))
+    cmd = [HIPCC, "-shared", "-fPIC", "-o", str(out), *objs, f"-L{BUILD}", "-lgyro_native", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"host:\n{r.stderr}")
+        raise RuntimeError(f"host link:\n{r.stderr}")
     return out.name
 
 

@@ -112,6 +112,7 @@ struct gd_buffer {
     uint64_t bytes = 0;
     uint64_t padded = 0;
     bool host_kind = false;
+    bool external = false;  // gd_wrap_memory: the caller owns the memory
     uint32_t srv_index = UINT32_MAX;
     uint32_t uav_index = UINT32_MAX;
     uint64_t last_storage = 0;
@@ -765,6 +766,48 @@ extern "C" gd_result gd_dispatch_timed(gd_context *c, gd_pipeline *p, const uint
     return launch(c, p, c->table, constants, count, x, y, z, c->compute, c->ts_pool[first], c->ts_pool[second]);
 }
 
+extern "C" gd_result gd_dispatch_on(gd_context *c, gd_pipeline *p, const uint32_t *constants, uint32_t count,
+                                    uint32_t x, uint32_t y, uint32_t z, void *stream) {
+    if (!c || !p || p->owner != c || count > kMaxConstants || (count && !constants) || !x || !y || !z ||
+        x > 65535 || y > 65535 || z > 65535)
+        return kInvalidArg;
+    GD_HIP(hipSetDevice(c->device));
+    return launch(c, p, c->table, constants, count, x, y, z, stream ? (hipStream_t)stream : c->compute);
+}
+
+extern "C" gd_result gd_wrap_memory(gd_context *c, void *device_address, uint64_t bytes, gd_buffer **out,
+                                    gd_buffer_info *info) {
+    if (!c || !out || !info || bytes > (uint64_t(1) << 32)) return kInvalidArg;
+    *out = nullptr;
+    *info = {};
+    try {
+        auto b = std::make_unique<gd_buffer>();
+        b->owner = c;
+        b->bytes = bytes;
+        b->padded = bytes;
+        b->external = true;
+        b->device = device_address;
+        b->srv_index = c->alloc_index();
+        b->uav_index = c->alloc_index();
+        if (b->srv_index == UINT32_MAX || b->uav_index == UINT32_MAX) {
+            if (b->srv_index != UINT32_MAX) c->table_free.push_back(b->srv_index);
+            if (b->uav_index != UINT32_MAX) c->table_free.push_back(b->uav_index);
+            return kOutOfMemory;
+        }
+        GD_HIP(hipSetDevice(c->device));
+        GD_TRY(c->set_index(b->srv_index, device_address));
+        GD_TRY(c->set_index(b->uav_index, device_address));
+        info->srv_index = b->srv_index;
+        info->uav_index = b->uav_index;
+        info->gpu_address = (uint64_t)(uintptr_t)device_address;
+        info->allocated_bytes = bytes;
+        c->buffers.push_back(b.get());
+        *out = b.release();
+        return kOk;
+    }
+    GD_CATCH
+}
+
 extern "C" gd_result gd_barrier(gd_context *c) {
     if (!c || !c->recording) return kInvalidArg;
     return kOk;  // the compute stream executes dispatches in order
@@ -828,10 +871,12 @@ extern "C" gd_result gd_release_buffer(gd_context *c, gd_buffer *b, uint32_t tim
         c->set_index(b->uav_index, nullptr);
         c->table_free.push_back(b->uav_index);
     }
-    if (b->host_kind)
+    if (b->external) {
+    } else if (b->host_kind) {
         hipHostFree(b->host);
-    else
+    } else {
         hipFree(b->device);
+    }
     c->buffers.erase(std::find(c->buffers.begin(), c->buffers.end(), b));
     delete b;
     return kOk;
@@ -858,10 +903,12 @@ extern "C" gd_result gd_destroy(gd_context *c, uint32_t timeout) {
         delete p;
     }
     for (gd_buffer *b : c->buffers) {
-        if (b->host_kind)
+        if (b->external) {
+        } else if (b->host_kind) {
             hipHostFree(b->host);
-        else
+        } else {
             hipFree(b->device);
+        }
         delete b;
     }
     for (gd_file *f : c->files) {

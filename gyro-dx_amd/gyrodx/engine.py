@@ -51,6 +51,7 @@ def lib() -> C.CDLL:
         L.gm_forward_stack.argtypes = [vp, C.POINTER(u32), u32, u32, f32p, u32, f32p]
         L.gm_run_stack.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
                                    C.POINTER(C.c_double)]
+        L.gm_forward_decode_noalloc.argtypes = [vp, u32, vp, u32, vp, vp]
         _lib = L
     return _lib
 
@@ -180,6 +181,13 @@ class Engine:
         self._check(lib().gm_run_stack(self._h, path, batch, calls, first, arr, len(layers), C.byref(dev),
                                        C.byref(wall)), "gm_run_stack")
         return dev.value, wall.value
+
+    def forward_decode_noalloc(self, layer: int, x_ptr: int, n: int, out_ptr: int, stream: int = 0):
+        """Decode-path forward of n <= 8 tokens between device buffers (addresses x_ptr, out_ptr),
+        queued on the hipStream_t `stream` (0: the engine's compute stream); allocates nothing and
+        does not wait."""
+        self._check(lib().gm_forward_decode_noalloc(self._h, layer, x_ptr, n, out_ptr, stream or None),
+                    "gm_forward_decode_noalloc")
 
     def read_outputs(self, n: int) -> np.ndarray:
         out = np.empty((n, self.E), np.float32)

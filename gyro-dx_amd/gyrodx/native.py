@@ -19,8 +19,9 @@ SYMBOLS = [
     "gd_create_resource", "gd_create_pipeline", "gd_release_pipeline", "gd_begin", "gd_dispatch",
     "gd_barrier", "gd_timestamp", "gd_submit", "gd_wait_compute", "gd_read_timestamps",
     "gd_queue_wait_storage", "gd_read_ranges_after", "gd_release_buffer", "gd_release_file", "gd_destroy",
-    # Extension without a counterpart in the reference ABI (timed dispatch for profiling).
-    "gd_dispatch_timed",
+    # Extensions without a counterpart in the reference ABI: timed dispatch for profiling, and the
+    # stream launch and caller-memory table entries of the MoE engine's no-allocation entry point.
+    "gd_dispatch_timed", "gd_dispatch_on", "gd_wrap_memory",
 ]
 
 
@@ -87,6 +88,8 @@ def lib() -> C.CDLL:
             "gd_release_file": [vp, vp, u32],
             "gd_destroy": [vp, u32],
             "gd_dispatch_timed": [vp, vp, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(u32)],
+            "gd_dispatch_on": [vp, vp, C.POINTER(u32), u32, u32, u32, u32, vp],
+            "gd_wrap_memory": [vp, vp, u64, C.POINTER(vp), C.POINTER(BufferInfo)],
         }
         for name, args in sig.items():
             f = getattr(L, name)

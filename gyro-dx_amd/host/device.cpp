@@ -47,6 +47,19 @@ Buffer Device::buffer(uint64_t bytes, Kind kind) {
     return b;
 }
 
+Buffer Device::wrap(void *device_address, uint64_t bytes) {
+    gd_buffer *handle = nullptr;
+    gd_buffer_info info{};
+    check(gd_wrap_memory(ctx, device_address, bytes, &handle, &info), "gd_wrap_memory");
+    Buffer b;
+    b.handle = handle;
+    b.srv = info.srv_index;
+    b.uav = info.uav_index;
+    b.bytes = bytes;
+    b.gpu = info.gpu_address;
+    return b;
+}
+
 void Device::release(Buffer &b) {
     if (b.handle) gd_release_buffer(ctx, b.handle, kTimeoutMs);
     b = Buffer{};

@@ -43,6 +43,8 @@ class Device {
     void init(uint32_t adapter);  // src/gpu.zig:41-53
     void deinit();
     Buffer buffer(uint64_t bytes, Kind kind);  // src/gpu.zig:68-75
+    // Table entries for memory owned elsewhere (gd_wrap_memory); release frees the entries only.
+    Buffer wrap(void *device_address, uint64_t bytes);
     void release(Buffer &b);
     gd_pipeline *pipeline(const std::vector<uint8_t> &code);  // src/gpu.zig:81-85
     void begin();

@@ -1,7 +1,12 @@
 // MoE layer engine above the gyro_native ABI: resident experts in slot arenas, the reference
 // dispatch sequence of src/gpu_engine.zig:1052-1119, and the MI355X decode and grouped-GEMM
 // paths. C entry points are declared in include/gyro_moe.h.
+//
+// This file is compiled as HIP source for one reason: it defines the device array `scratch`
+// that the no-allocation decode entry point (gm_forward_decode_noalloc) uses for its
+// intermediate buffers. Every kernel still comes from the pipelines in the kernel directory.
 #include <dirent.h>
+#include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <chrono>
@@ -10,12 +15,19 @@
 #include <cstring>
 #include <fstream>
 #include <map>
+#include <initializer_list>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "device.h"
 #include "gyro_moe.h"
+
+// Intermediate buffers of gm_forward_decode_noalloc: router logits, routes, the rotated input,
+// the gate/up partials and the shared expert's rows. One copy per GPU, alive until the process
+// ends; every no-allocation call on a GPU shares it, so calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t scratch[GM_NOALLOC_SCRATCH_BYTES];
 
 namespace gyro {
 namespace {
@@ -152,7 +164,42 @@ std::vector<uint8_t> read_file(const std::string &path) {
     return std::vector<uint8_t>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
 }
 
+// Device address of `scratch` on each GPU, looked up once per device with that device current.
+// In host code the array's name is only a stand-in for the symbol; kernels get this address.
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_ptr[kMaxDevices] = {};
+
+void *scratch_address(uint32_t device) {
+    if (device >= (uint32_t)kMaxDevices) throw NativeError(-1, "device ordinal out of range for the scratch table");
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[device]) {
+        hipError_t rc = hipSetDevice((int)device);
+        if (rc != hipSuccess) throw NativeError(-1, std::string("hipSetDevice: ") + hipGetErrorString(rc));
+        void *p = nullptr;
+        rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (rc != hipSuccess || !p)
+            throw NativeError(-1, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(rc));
+        scratch_ptr[device] = p;
+    }
+    return scratch_ptr[device];
+}
+
+// Fixed regions of the scratch array: the shared expert's rows (n <= 8 tokens x 2 SF <= 2048
+// floats) and gate dots come first, at their own table entries (moe_router takes them without
+// an offset); the per-call buffers follow from kNoallocBase.
+constexpr uint64_t kNoallocShH = 0, kNoallocShHBytes = 64u << 10;
+constexpr uint64_t kNoallocShG = kNoallocShHBytes, kNoallocShGBytes = 256;
+constexpr uint64_t kNoallocBase = 128u << 10;
+static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocBase, "scratch regions overlap");
+
 }  // namespace
+
+// Table indices (and word offsets) of the intermediate buffers of the decode path.
+struct DecodeBufs {
+    uint32_t logits, logits_off, ids, ids_off, weights, weights_off, xh, xh_off, gu, gu_off;
+    uint32_t sh_h, sh_g;  // shared expert rows and gate dots (offset 0)
+};
 
 // Residual stream of a stack step: the layer input is normalised by the layer's RMSNorm inside
 // the path's first kernel, and the path's last kernel adds res to its output.
@@ -164,7 +211,11 @@ struct StackStep {
 class Engine {
   public:
     Device dev;
-    std::map<std::string, gd_pipeline *> pipes;
+    std::map<std::string, gd_pipeline *, std::less<>> pipes;
+    // Direct launches (no recording) on a caller's stream, for gm_forward_decode_noalloc.
+    bool direct = false;
+    void *direct_stream = nullptr;
+    Buffer na_base, na_shh, na_shg, na_x, na_out;  // table entries into `scratch` and for the caller's x, out
     std::string error;
     uint32_t max_tok = 0;
     uint32_t E = 0, F = 0, NE = 0, U = 0;
@@ -193,16 +244,25 @@ class Engine {
         return it->second;
     }
 
+    void dispatch_words(const char *name, const uint32_t *c, uint32_t count, uint32_t x, uint32_t y, uint32_t z) {
+        if (direct)
+            check(gd_dispatch_on(dev.ctx, pipe(name), c, count, x, y, z, direct_stream), "gd_dispatch_on");
+        else
+            dev.dispatch(pipe(name), c, count, x, y, z);
+    }
     void dispatch(const char *name, const std::vector<uint32_t> &c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
-        dev.dispatch(pipe(name), c.data(), (uint32_t)c.size(), x, y, z);
+        dispatch_words(name, c.data(), (uint32_t)c.size(), x, y, z);
+    }
+    void dispatch(const char *name, std::initializer_list<uint32_t> c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
+        dispatch_words(name, c.begin(), (uint32_t)c.size(), x, y, z);
     }
 
     // Dispatch that records its own start and end timestamps when `timed` is set (their
     // indices are appended to marks).
     void dispatch_maybe_timed(bool timed, std::vector<uint32_t> *marks, const char *name,
-                              const std::vector<uint32_t> &c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
+                              std::initializer_list<uint32_t> c, uint32_t x, uint32_t y = 1, uint32_t z = 1) {
         if (timed && marks) {
-            const uint32_t first = dev.dispatch_timed(pipe(name), c.data(), (uint32_t)c.size(), x, y, z);
+            const uint32_t first = dev.dispatch_timed(pipe(name), c.begin(), (uint32_t)c.size(), x, y, z);
             marks->push_back(first);
             marks->push_back(first + 1);
         } else {
@@ -271,6 +331,19 @@ class Engine {
             std::memcpy(&h, book.data() + 2 * i, 2);
             max_codebook = std::max(max_codebook, std::fabs(half_to_float(h)));
         }
+        // Table entries of the no-allocation entry point: into this GPU's scratch array, and two
+        // whose addresses each call sets (the caller's input and output).
+        uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter));
+        na_base = dev.wrap(sp, GM_NOALLOC_SCRATCH_BYTES);
+        na_shh = dev.wrap(sp + kNoallocShH, kNoallocShHBytes);
+        na_shg = dev.wrap(sp + kNoallocShG, kNoallocShGBytes);
+        na_x = dev.wrap(nullptr, 0);
+        na_out = dev.wrap(nullptr, 0);
+    }
+
+    // The decode path's own intermediate buffers.
+    DecodeBufs engine_bufs() const {
+        return {router_out.uav, 0, ids.uav, 0, weights.uav, 0, xh.uav, 0, gu_part.uav, 0, sh_h.uav, sh_g.uav};
     }
 
     void allocate_activations() {
@@ -571,8 +644,10 @@ class Engine {
 
     // MI355X decode path: router + rotation, routed gate/up, down + combine.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
-                    int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {}) {
+                    int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {},
+                    const DecodeBufs *bufs = nullptr) {
         const Layer &L = layers.at(il);
+        const DecodeBufs B = bufs ? *bufs : engine_bufs();
         if (!decode_supported(L, n))
             throw NativeError(-1, "decode path needs <= 256 experts, n <= 8, E a multiple of 256 up to 4096, F a "
                                   "multiple of 128 up to 1024 and top-1..16; a shared expert (on a layer of another "
@@ -581,18 +656,18 @@ class Engine {
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
-                              router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
+                              B.logits, B.logits_off, L.has_gate_signs ? L.signs.srv : kNone, 0, B.xh, B.xh_off,
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
-                              bits(L.norm_eps), 2 * L.SF, L.SF ? L.sh_gu.srv : 0u, L.SF ? sh_h.uav : 0u,
-                              L.SF ? L.sh_gate.srv : 0u, L.SF ? sh_g.uav : 0u},
+                              bits(L.norm_eps), 2 * L.SF, L.SF ? L.sh_gu.srv : 0u, L.SF ? B.sh_h : 0u,
+                              L.SF ? L.sh_gate.srv : 0u, L.SF ? B.sh_g : 0u},
                              std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 4 + 1 : 0));
         if (!decode_generic_types(L)) {
             dispatch_maybe_timed(bracket == 2, marks, E % 1024 == 0 && U == 8 ? "moe_decode_gu" : "moe_decode_gu_g",
-                                 {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
-                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, gu_part.uav, 0, E, F, n},
+                                 {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
+                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n},
                                  F / 64, 2 * parts, n * U);
             dispatch_maybe_timed(bracket == 3, marks, decode_fast_down() ? "moe_decode_down" : "moe_decode_down_g",
-                                 {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, base_lo, base_hi, slot_stride,
+                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
                                   2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
                                   out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
                                   st.res_off},
@@ -600,22 +675,22 @@ class Engine {
             return;
         }
         dispatch_maybe_timed(bracket == 2, marks, decode_generic_tuned() ? "moe_decode_gu_x" : "moe_decode_gu_xg",
-                             {router_out.uav, 0, NE, U, bits(L.scale), ids.uav, 0, weights.uav, 0, xh.uav, 0,
-                              L.xtab.srv, codebook.srv, gu_part.uav, 0, E, F, n},
+                             {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
+                              L.xtab.srv, codebook.srv, B.gu, B.gu_off, E, F, n},
                              F / 64, 2 * parts, n * U);
         if (!decode_generic_tuned()) {
             dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_xg",
-                                 {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
+                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
                                   L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
                                   st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
                                  E / 8, n);
             return;
         }
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
-                             {gu_part.uav, 0, ids.uav, 0, weights.uav, 0, L.xtab.srv, 0, 0, 0, codebook.srv,
+                             {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
-                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, sh_h.uav, 0,
-                              sh_g.uav, 0, L.SF ? L.sh_down.srv : 0u, L.SF},
+                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, B.sh_h, 0,
+                              B.sh_g, 0, L.SF ? L.sh_down.srv : 0u, L.SF},
                              E / 16, n);
     }
 
@@ -770,6 +845,46 @@ class Engine {
         stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
         dev.wait(dev.submit());
         check(gd_readback(dev.ctx, x_in.handle, 0, n * E * 4, y, kTimeoutMs), "gd_readback");
+    }
+
+    // gm_forward_decode_noalloc: the decode path on device-resident x and y, its intermediate
+    // buffers carved out of this GPU's scratch array (256-byte aligned, word offsets), queued on
+    // `stream`. Nothing is allocated, copied or waited for.
+    void forward_decode_noalloc(uint32_t il, const float *x, uint32_t n, float *y, void *stream) {
+        if (n == 0 || n > 8) throw NativeError(-1, "gm_forward_decode_noalloc takes 1 to 8 tokens");
+        const Layer &L = layers.at(il);
+        if (!decode_supported(L, n)) throw NativeError(-1, "the layer is not on the decode path");
+        uint64_t at = kNoallocBase;
+        auto take = [&at](uint64_t bytes) {
+            const uint64_t off = at;
+            at = (at + bytes + 255) & ~uint64_t(255);
+            return (uint32_t)(off / 4);
+        };
+        DecodeBufs B;
+        B.logits = B.ids = B.weights = B.xh = B.gu = na_base.uav;
+        B.logits_off = take((uint64_t)n * NE * 4);
+        B.ids_off = take((uint64_t)n * U * 4);
+        B.weights_off = take((uint64_t)n * U * 4);
+        B.xh_off = take((uint64_t)n * E * 2);
+        B.gu_off = take((uint64_t)parts * n * U * 2 * F * 4);
+        B.sh_h = na_shh.uav;
+        B.sh_g = na_shg.uav;
+        if (at > GM_NOALLOC_SCRATCH_BYTES || (uint64_t)n * 2 * L.SF * 4 > kNoallocShHBytes ||
+            (uint64_t)n * 4 > kNoallocShGBytes)
+            throw NativeError(-1, "the layer's decode buffers exceed the GM_NOALLOC_SCRATCH_BYTES scratch array");
+        direct = true;
+        direct_stream = stream;
+        struct Restore {
+            Engine *e;
+            ~Restore() {
+                e->direct = false;
+                e->direct_stream = nullptr;
+            }
+        } restore{this};
+        const uint64_t xa = (uint64_t)(uintptr_t)x, ya = (uint64_t)(uintptr_t)y;
+        dispatch("gd_table_set",
+                 {2u, na_x.uav, (uint32_t)xa, (uint32_t)(xa >> 32), na_out.uav, (uint32_t)ya, (uint32_t)(ya >> 32)}, 1);
+        ffn_decode(il, n, na_x.uav, 0, na_out.uav, 0, 0, nullptr, StackStep{}, &B);
     }
 
     void forward(uint32_t il, uint32_t path, const float *x, uint32_t n, float *y) {
@@ -979,6 +1094,12 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
     });
+}
+
+extern "C" int gm_forward_decode_noalloc(gm_engine *g, uint32_t layer, const float *x, uint32_t n, float *out,
+                                         void *stream) {
+    if (!x || !out) return -1;
+    return guarded(g, [&] { g->e.forward_decode_noalloc(layer, x, n, out, stream); });
 }
 
 extern "C" int gm_read_outputs(gm_engine *g, float *y, uint32_t n_total) {

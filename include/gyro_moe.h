@@ -113,6 +113,23 @@ GM_API int gm_run_stack(gm_engine *e, uint32_t path, uint32_t batch, uint32_t ca
 /* Reads outputs[n_total][E] written by gm_run or gm_run_stack. */
 GM_API int gm_read_outputs(gm_engine *e, float *out, uint32_t n_total);
 
+/* Size of the device array that gm_forward_decode_noalloc keeps its intermediate buffers in
+ * (one per GPU, held until the process ends). */
+#define GM_NOALLOC_SCRATCH_BYTES (5u << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The GM_PATH_DECODE forward
+ * of gm_forward on n <= 8 tokens, with x[n][E] and out[n][E] in device memory, queued on
+ * `stream` (a hipStream_t of the engine's device; NULL: the engine's compute stream) without
+ * waiting for it. It calls no hipMalloc / hipFree and no memset or copy: router logits, routes,
+ * the rotated input, the gate/up partials and the shared expert's rows live in a fixed device
+ * array of GM_NOALLOC_SCRATCH_BYTES per GPU, and a small kernel points two table entries at x and
+ * out. A layer shape whose buffers exceed that array is refused with an error. Every call on one
+ * GPU shares the array and those two entries: calls that overlap on one GPU race, so a caller
+ * serialises them (one stream, or its own ordering). Results equal gm_forward's bit for bit. */
+GM_API int gm_forward_decode_noalloc(gm_engine *e, uint32_t layer, const float *x, uint32_t n, float *out,
+                                     void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -163,6 +163,18 @@ GD_API gd_result gd_destroy(gd_context *context, uint32_t timeout_ms);
 GD_API gd_result gd_dispatch_timed(gd_context *context, gd_pipeline *pipeline, const uint32_t *constants,
     uint32_t constant_count, uint32_t groups_x, uint32_t groups_y, uint32_t groups_z, uint32_t *out_index);
 
+/* Extension with no counterpart in the reference ABI, for callers that run outside a recording
+ * (the MoE engine's no-allocation entry point): launches at once on `stream`, a hipStream_t of
+ * the context's device (NULL: the context's compute stream), with the checks of gd_dispatch but
+ * no gd_begin / gd_submit bracket and no ticket. */
+GD_API gd_result gd_dispatch_on(gd_context *context, gd_pipeline *pipeline, const uint32_t *constants,
+    uint32_t constant_count, uint32_t groups_x, uint32_t groups_y, uint32_t groups_z, void *stream);
+/* Extension with no counterpart in the reference ABI: gives memory the caller owns (device
+ * address, may be NULL until a kernel writes the entry) SRV and UAV table indices, as
+ * gd_create_resource does for memory it allocates. gd_release_buffer frees the indices only. */
+GD_API gd_result gd_wrap_memory(gd_context *context, void *device_address, uint64_t bytes,
+    gd_buffer **out_buffer, gd_buffer_info *out_info);
+
 #ifdef __cplusplus
 }
 #endif
