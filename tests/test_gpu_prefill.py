@@ -59,10 +59,15 @@ def run_case(oracle_mod, layer, x, max_tok, what):
         print(f"{what}: {int((~sep).sum())} near-tie tokens excluded", flush=True)
         np.testing.assert_array_equal(ids[sep], tr["route_ids"][sep])
         np.testing.assert_allclose(w[sep], tr["route_w"][sep], rtol=2e-5, atol=1e-7)
+        order, start = eng.last_sort(n)
         if sep.all():
-            order, start = eng.last_sort(n)
             np.testing.assert_array_equal(start, tr["order_start"])
             np.testing.assert_array_equal(order, tr["route_order"])
+        # Whatever the ties, the sort is the stable counting sort of the routes the GPU chose
+        # (src/engine.zig:553-564).
+        flat = ids.reshape(-1).astype(np.int64)
+        np.testing.assert_array_equal(start, np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=layer.n_expert))]))
+        np.testing.assert_array_equal(order, np.argsort(flat, kind="stable"))
         check_tiles(eng.last_tiles(), tr["order_start"] if sep.all() else eng.last_sort(n)[1])
         r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
         print(f"{what}: rel_rms={r:.3e} cosine={c:.8f}", flush=True)
@@ -79,6 +84,25 @@ def test_prefill_full_layer_zipf(oracle_mod):
     order, start = run_case(oracle_mod, layer, x, 256, "full zipf")
     counts = np.diff(start.astype(np.int64))
     assert counts.max() > 128  # at least one expert spans several tiles
+
+
+@pytest.mark.timeout(600)
+def test_prefill_config3_1024_tokens(oracle_mod):
+    """The prefill configuration itself: 1024 bf16 tokens through the Zipf(1.1)-biased layer."""
+    layer = synth.make_layer(20261201, zipf=1.1)
+    x = synth.make_tokens(20261203, 1024, bf16=True)
+    order, start = run_case(oracle_mod, layer, x, 1024, "config 3, 1024 tokens")
+    assert len(order) == 8192
+
+
+@pytest.mark.timeout(900)
+def test_prefill_4096_tokens(oracle_mod):
+    """The stack configuration's 4096-token prefill on one layer: 32,768 slots, the largest call
+    the sort and tile list accept (n x n_used <= 32768)."""
+    layer = synth.make_layer(4910, zipf=1.1)
+    x = synth.make_tokens(4911, 4096, bf16=True)
+    eng_tiles = run_case(oracle_mod, layer, x, 4096, "4096 tokens")
+    assert len(eng_tiles[0]) == 32768
 
 
 def test_prefill_single_and_ragged(oracle_mod):
