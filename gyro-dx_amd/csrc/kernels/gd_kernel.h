@@ -139,5 +139,13 @@ __device__ __forceinline__ gd_gu32x4 *gd_global4(const uint32_t *p) { return (gd
 // accesses across it.
 __device__ __forceinline__ void gd_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Activation range guard: an activation rounded to binary16 must be finite and at most 65504 in
+// magnitude (false for NaN and infinities). A kernel that rounds one outside stores 1 to the
+// flag word at table index `flag` (0: no flag); the host reads it and recomputes on the fp32 path.
+__device__ __forceinline__ bool gd_half_ok(float v) { return __builtin_fabsf(v) <= 65504.0f; }
+__device__ __forceinline__ void gd_range_flag(const uint64_t *table, uint32_t flag, bool bad) {
+    if (flag && bad) reinterpret_cast<uint32_t *>(table[flag])[0] = 1u;
+}
+
 // 1 / sqrt(128) rounded to binary32, the normalisation of a 128-point Walsh-Hadamard block.
 #define GD_INV_SQRT128 0.0883883461356163f

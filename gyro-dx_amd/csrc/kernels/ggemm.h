@@ -354,7 +354,8 @@ __device__ __forceinline__ void gx_run(GxLds &sm, const GxState &t, uint32_t typ
 template <class LDS, int NRB>
 __device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
                                                uint32_t h, const float *signs, uint32_t *out, uint32_t row0,
-                                               uint32_t rows, uint32_t fb, uint32_t F) {
+                                               uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
+    bool bad = false;  // a tile row's activation outside the binary16 range
     const bool up = wave >= 4u;
     const uint32_t cq = wave & 3u, col = cq * 32u + m;
     float *ubuf = reinterpret_cast<float *>(&sm.a[0][0]);
@@ -373,8 +374,9 @@ __device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB]
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
-                act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
-                    (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[i * 128u + col] * sgn);
+                const float v = gd_silu_rcp(acc[rb][r]) * ubuf[i * 128u + col] * sgn;
+                bad |= i < rows && !gd_half_ok(v);
+                act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] = (_Float16)v;
             }
         }
     }
@@ -400,11 +402,14 @@ __device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB]
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
-                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
+                const float v = rot[r] * GD_INV_SQRT128;
+                bad |= i < rows && !gd_half_ok(v);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)v;
             }
         }
         __syncthreads();
     }
+    if (flag && bad) *flag = 1u;
     const gd_u32x4 *rows_src = signs ? &sm.a[0][0] : &sm.a[2][0];
     for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
         const uint32_t i = idx >> 4, c = idx & 15u;
@@ -623,7 +628,8 @@ __device__ __forceinline__ void gh_prologue(GhLds &sm, const GhState &t) {
 template <int NRB>
 __device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
                                                uint32_t h, bool signs, float sgn, uint32_t *out, uint32_t row0,
-                                               uint32_t rows, uint32_t fb, uint32_t F) {
+                                               uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
+    bool bad = false;  // a tile row's activation outside the binary16 range
     uint8_t *lds = reinterpret_cast<uint8_t *>(&sm);
     float *ubuf = reinterpret_cast<float *>(lds);
     _Float16 *act = reinterpret_cast<_Float16 *>(lds + 32768);
@@ -646,8 +652,9 @@ __device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NR
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t iu = (rb - 2 * p) * 32u + (r / 4) * 8u + h * 4u + (r % 4), i = iu + 64u * p;
-                    act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] =
-                        (_Float16)(gd_silu_rcp(acc[rb][r]) * ubuf[iu * 128u + col] * sgn);
+                    const float v = gd_silu_rcp(acc[rb][r]) * ubuf[iu * 128u + col] * sgn;
+                    bad |= i < rows && !gd_half_ok(v);
+                    act[i * 128u + ((((col >> 3) ^ (i & 15u)) << 3) | (col & 7u))] = (_Float16)v;
                 }
             }
         }
@@ -676,11 +683,14 @@ __device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NR
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = rb * 32u + (r / 4) * 8u + h * 4u + (r % 4);
-                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)(rot[r] * GD_INV_SQRT128);
+                const float v = rot[r] * GD_INV_SQRT128;
+                bad |= i < rows && !gd_half_ok(v);
+                res[i * 128u + ((((j >> 3) ^ (i & 15u)) << 3) | (j & 7u))] = (_Float16)v;
             }
         }
         __syncthreads();
     }
+    if (flag && bad) *flag = 1u;
     // Global (not flat) stores: a flat access also counts as LDS traffic in the wait counters.
     const gd_u32x4 *rows_src = reinterpret_cast<const gd_u32x4 *>(signs ? lds : lds + 32768);
     __attribute__((address_space(1))) gd_u32x4 *og =

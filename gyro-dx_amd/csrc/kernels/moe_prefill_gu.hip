@@ -22,18 +22,19 @@
 // groups start tile by tile in the sort's longest-first order, all column blocks of a tile
 // together; the groups beyond the sort's tile count exit.
 // Requires TQ2_T experts, E % 256 == 0 (rows start at 4-byte boundaries, an even block count
-// of at least 2), F % 128 == 0, |xh|, |act| < 65504.
+// of at least 2), F % 128 == 0, activations within the binary16 range (checked: the range flag).
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 xh16_uav 4 xh16_off (words) 5 base_lo
 // 6 base_hi 7 slot_stride 8 proj_bytes 9 codebook_srv 10 signs_srv (0xffffffff: none)
-// 11 signs_off 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used.
+// 11 signs_off 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used 17 range flag (1: word 1022
+// of meta is set to 1 when an activation of a tile row leaves the binary16 range; 0: none).
 #include "ggemm.h"
 
 template <int NRB>
 __device__ __forceinline__ void gu_tile(GhLds &sm, const GhState &t, bool signs, float sgn, uint32_t *out,
-                                        uint32_t row0, uint32_t rows, uint32_t fb, uint32_t F) {
+                                        uint32_t row0, uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
     f32x16 acc[NRB];
     gh_kloop<NRB>(sm, t, acc);
-    gh_gu_epilogue<NRB>(sm, acc, t.wave, t.m, t.h, signs, sgn, out, row0, rows, fb, F);
+    gh_gu_epilogue<NRB>(sm, acc, t.wave, t.m, t.h, signs, sgn, out, row0, rows, fb, F, flag);
 }
 
 GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 4) {
@@ -90,13 +91,15 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu, 512, 4) {
                                                            [a.c[11] + fb * 128u + (wave & 3u) * 32u + t.m])
                                         : 1.0f;
     uint32_t *out = gd_buf<uint32_t>(a, a.c[12]) + a.c[13];
+    uint32_t *flag = a.c[17] ? const_cast<uint32_t *>(meta) + 1022u : nullptr;
     gh_settle(out, F);
+    gh_settle(flag, rows);
     __syncthreads();  // codebook
     gh_prologue(sm, t);
     switch ((rows + 31u) >> 5) {
-        case 1: gu_tile<1>(sm, t, signs, sgn, out, row0, rows, fb, F); break;
-        case 2: gu_tile<2>(sm, t, signs, sgn, out, row0, rows, fb, F); break;
-        case 3: gu_tile<3>(sm, t, signs, sgn, out, row0, rows, fb, F); break;
-        default: gu_tile<4>(sm, t, signs, sgn, out, row0, rows, fb, F); break;
+        case 1: gu_tile<1>(sm, t, signs, sgn, out, row0, rows, fb, F, flag); break;
+        case 2: gu_tile<2>(sm, t, signs, sgn, out, row0, rows, fb, F, flag); break;
+        case 3: gu_tile<3>(sm, t, signs, sgn, out, row0, rows, fb, F, flag); break;
+        default: gu_tile<4>(sm, t, signs, sgn, out, row0, rows, fb, F, flag); break;
     }
 }

@@ -15,19 +15,20 @@
 // K loop, B-operand decode and epilogue as the TQ2_T kernel (ggemm.h); the fp16 products
 // scale x codebook stay finite: the host checks every layer's scales.
 // Grid: (F / 128, max tiles); 512 threads, one group per CU (152.5 KB of LDS).
-// Requires Gyro types 144..151, E % 256 == 0, F % 128 == 0, |xh|, |act| < 65504.
+// Requires Gyro types 144..151, E % 256 == 0, F % 128 == 0, activations within the binary16 range (checked: the range flag).
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 xh16_uav 4 xh16_off (words) 5 xtab_srv
 // 6 codebook_srv 7 signs_srv (0xffffffff: none) 8 signs_off 9 act16_uav 10 act16_off (words)
-// 11 E 12 F 13 n_used.
+// 11 E 12 F 13 n_used 14 range flag (1: word 1022 of meta is set to 1 when an activation of a
+// tile row leaves the binary16 range; 0: none).
 #include "ggemm.h"
 
 template <int NRB>
 __device__ __forceinline__ void gux_tile(GxLds &sm, const GxState &t, uint32_t type, const GdArgs &a, uint32_t row0,
-                                         uint32_t rows, uint32_t fb, uint32_t F) {
+                                         uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
     f32x16 acc[NRB];
     gx_run<NRB>(sm, t, type, acc);
     const float *signs = a.c[7] != 0xffffffffu ? gd_buf<const float>(a, a.c[7]) + a.c[8] : nullptr;
-    gg_gu_epilogue(sm, acc, t.wave, t.m, t.h, signs, gd_buf<uint32_t>(a, a.c[9]) + a.c[10], row0, rows, fb, F);
+    gg_gu_epilogue(sm, acc, t.wave, t.m, t.h, signs, gd_buf<uint32_t>(a, a.c[9]) + a.c[10], row0, rows, fb, F, flag);
 }
 
 GD_PIPELINE_NAMED_OCC(moe_prefill_gu_x, 512, 2) {
@@ -91,10 +92,11 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gu_x, 512, 2) {
     gx_stage(sm, 0, t, 0);
     if (t.nk > 1u) gx_stage(sm, 1, t, 1);
     const uint32_t type = wave < 4u ? tg : tu;
+    uint32_t *flag = a.c[14] ? const_cast<uint32_t *>(meta) + 1022u : nullptr;
     switch ((rows + 31u) >> 5) {
-        case 1: gux_tile<1>(sm, t, type, a, row0, rows, fb, F); break;
-        case 2: gux_tile<2>(sm, t, type, a, row0, rows, fb, F); break;
-        case 3: gux_tile<3>(sm, t, type, a, row0, rows, fb, F); break;
-        default: gux_tile<4>(sm, t, type, a, row0, rows, fb, F); break;
+        case 1: gux_tile<1>(sm, t, type, a, row0, rows, fb, F, flag); break;
+        case 2: gux_tile<2>(sm, t, type, a, row0, rows, fb, F, flag); break;
+        case 3: gux_tile<3>(sm, t, type, a, row0, rows, fb, F, flag); break;
+        default: gux_tile<4>(sm, t, type, a, row0, rows, fb, F, flag); break;
     }
 }

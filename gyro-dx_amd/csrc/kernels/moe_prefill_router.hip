@@ -24,7 +24,9 @@
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
 // 14 xh16_off (words) 15 x16 (1: also write the unrotated input as binary16, for the shared
 // expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words) 18 S (0 or
-// 1: no split; plane z at logits_off + z n n_expert; the bias enters plane 0).
+// 1: no split; plane z at logits_off + z n n_expert; the bias enters plane 0) 19 range flag
+// (table index of a word set to 1 when a value written as binary16 is outside its range; 0:
+// none).
 #include "ggemm.h"
 #include "fwht.h"
 
@@ -62,11 +64,12 @@ __device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf,
     for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
 }
 
-// Sixteen values as binary16 pairs (32 bytes) at dst.
-__device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16]) {
+// Sixteen values as binary16 pairs (32 bytes) at dst; `bad` records a value outside the range.
+__device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16], bool &bad) {
     gd_u32x4 o[2];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+        bad |= !gd_half_ok(v[2 * j]) || !gd_half_ok(v[2 * j + 1]);
         const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
         const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
         o[j >> 2][j & 3] = h0 | (h1 << 16);
@@ -152,6 +155,7 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
         const float *S = has_signs ? gd_buf<const float>(a, a.c[11]) + a.c[12] : nullptr;
         uint32_t *XH = gd_buf<uint32_t>(a, a.c[13]) + a.c[14];
         const uint32_t l8 = lane & 7u;
+        bool bad = false;
         for (uint32_t g = first; g * 8u < total; g += waves) {
             const uint32_t b = g * 8u + (lane >> 3);
             if (b < total) {
@@ -163,7 +167,7 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
                     const float4 f = src[q];
                     v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
                 }
-                if (a.c[15]) rt_store_h16(gd_buf<uint32_t>(a, a.c[16]) + a.c[17] + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v);
+                if (a.c[15]) rt_store_h16(gd_buf<uint32_t>(a, a.c[16]) + a.c[17] + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v, bad);
                 if (has_signs) {
                     const float4 *sg = reinterpret_cast<const float4 *>(S + i);
 #pragma unroll
@@ -179,9 +183,10 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
 #pragma unroll
                     for (int j = 0; j < 16; ++j) v[j] *= GD_INV_SQRT128;
                 }
-                rt_store_h16(XH + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v);
+                rt_store_h16(XH + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v, bad);
             }
         }
+        gd_range_flag(a.table, a.c[19], bad);
     }
     __syncthreads();
     const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;

@@ -20,7 +20,8 @@
 // Constants: 0 mode 1 a_uav 2 a_off (words) 3 lda (values per A row) 4 w_srv 5 w_off (words)
 // 6 K 7 out_uav 8 out_off (words) 9 n_tok 10 up_row0 (mode 0: first up row, = SF) 11 scale0
 // (fp32 bits: 2^-k of the gate or the down matrix) 12 scale1 (the up matrix) 13 ldo (values per
-// output row).
+// output row) 14 range flag (mode 0: table index of a word set to 1 when a SwiGLU value of a token
+// row leaves the binary16 range; 0: none).
 #include "ggemm.h"
 
 #define SH_TM 64
@@ -128,13 +129,17 @@ GD_PIPELINE_NAMED(moe_prefill_shared, 256) {
         }
         __syncthreads();
         if (wave < 2u) {
+            bool bad = false;
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t i = rbase + (r / 4) * 8u + (r % 4), c = 32u * j + m;
-                    ab[i * 64u + c] = (_Float16)(gd_silu_rcp(acc[j][r] * sg) * ub[i * 64u + c]);
+                    const float v = gd_silu_rcp(acc[j][r] * sg) * ub[i * 64u + c];
+                    bad |= t0 + i < n && !gd_half_ok(v);
+                    ab[i * 64u + c] = (_Float16)v;
                 }
+            gd_range_flag(a.table, a.c[14], bad);
         }
         __syncthreads();
         uint32_t *out = gd_buf<uint32_t>(a, a.c[7]) + a.c[8];

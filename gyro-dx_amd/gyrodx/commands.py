@@ -26,8 +26,9 @@ TIMEOUT_MS = 30000
 # src/gyro.zig:32-41: type id -> (bits per step k, steps per block, block bytes).
 TYPES = {144: (8, 32, 34), 145: (6, 32, 26), 146: (7, 32, 30), 147: (5, 64, 42), 148: (6, 64, 50),
          149: (7, 64, 58), 150: (5, 32, 22), 151: (4, 32, 18)}
-TYPE_NAMES = {144: "TQ2_T", 145: "GYRO_K6_S32", 146: "GYRO_K7_S32", 147: "GYRO_K5_S64", 148: "GYRO_K6_S64",
-              149: "GYRO_K7_S64", 150: "GYRO_K5_S32", 151: "GYRO_K4_S32"}
+# The type table's names (src/gyro.zig:33-40), printed by validateGyro as info.name.
+TYPE_NAMES = {144: "TQ2_T", 145: "TQK6", 146: "TQK7", 147: "TQP5", 148: "TQP6", 149: "TQP7", 150: "TQK5",
+              151: "TQK4"}
 EDGE_SCALES = (0, 0x8000, 1, 0x8001, 0x3FF, 0x83FF, 0x400, 0x8400, 0x3C00, 0xBC00, 0x7BFF, 0xFBFF)
 
 

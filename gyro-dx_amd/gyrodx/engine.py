@@ -18,7 +18,11 @@ class LayerDesc(C.Structure):
                 ("down_signs", C.c_void_p), ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
                 ("types", C.c_void_p), ("SF", C.c_uint32), ("sh_gate", C.c_void_p), ("sh_up", C.c_void_p),
                 ("sh_down", C.c_void_p), ("sh_gate_inp", C.c_void_p), ("norm_weight", C.c_void_p),
-                ("norm_eps", C.c_float)]
+                ("norm_eps", C.c_float), ("sh_type", C.c_uint32)]
+
+
+# GGML type of a shared expert's matrices (src/kernels.zig:7-10) -> the engine's gm_layer_desc code.
+SHARED_KIND = {30: 0, 8: 1, 0: 2}
 
 
 _lib = None
@@ -111,7 +115,7 @@ class Engine:
                       SF=layer.SF, sh_gate=ptr(layer.sh_gate), sh_up=ptr(layer.sh_up), sh_down=ptr(layer.sh_down),
                       sh_gate_inp=ptr(None if layer.sh_gate_inp is None else np.asarray(layer.sh_gate_inp, np.float32)),
                       norm_weight=ptr(None if layer.norm_weight is None else np.asarray(layer.norm_weight, np.float32)),
-                      norm_eps=layer.norm_eps)
+                      norm_eps=layer.norm_eps, sh_type=SHARED_KIND[getattr(layer, "sh_type", 30)] if layer.SF else 0)
         idx = C.c_uint32()
         self._check(lib().gm_add_layer(self._h, C.byref(d), C.byref(idx)), "gm_add_layer")
         self.E, self.U, self.n_expert = layer.E, layer.n_used, layer.n_expert

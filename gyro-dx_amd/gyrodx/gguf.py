@@ -23,12 +23,23 @@ class GgufError(RuntimeError):
              -5: "InvalidBoolean", -6: "LimitExceeded", -7: "IntegerOverflow", -8: "InvalidAlignment",
              -9: "InvalidDimensions", -10: "DuplicateKey", -11: "DuplicateTensor", -12: "InvalidTensorRange",
              -13: "OverlappingTensors", -14: "UnsupportedTensorType", -15: "InvalidExpert",
-             -16: "InvalidMetadata", -17: "IO", -18: "NotFound", -19: "UnsupportedGyroMetadata"}
+             -16: "InvalidMetadata", -17: "IO", -18: "NotFound", -19: "UnsupportedGyroMetadata",
+             -20: "OutOfMemory"}
 
     def __init__(self, code: int, what: str):
         self.code = code
         self.kind = self.NAMES.get(code, str(code))
         super().__init__(f"{what}: {self.kind}")
+
+
+class UnsupportedConfiguration(GgufError):
+    """A well-formed file the model loader refuses (error.UnsupportedConfiguration of
+    src/model.zig and src/gpu_engine.zig)."""
+
+    def __init__(self, what: str):
+        RuntimeError.__init__(self, f"{what}: UnsupportedConfiguration")
+        self.code = -21
+        self.kind = "UnsupportedConfiguration"
 
 
 class TensorInfo(C.Structure):
@@ -126,6 +137,10 @@ class Model:
         _check(_lib().gg_find_tensor(self._h, name.encode(), C.byref(t)), f"tensor {name}")
         return self._conv(t)
 
+    def has_tensor(self, name: str) -> bool:
+        t = TensorInfo()
+        return _lib().gg_find_tensor(self._h, name.encode(), C.byref(t)) == 0
+
     def expert_range(self, name: str, expert: int) -> tuple[int, int]:
         off, n = C.c_uint64(), C.c_uint64()
         _check(_lib().gg_expert_range(self._h, name.encode(), expert, C.byref(off), C.byref(n)),
@@ -219,6 +234,23 @@ def load_layer_experts(path: str, layer: int) -> dict:
         m.close()
 
 
+def _rotation(m: "Model"):
+    """The released rotation metadata as the model loader reads it (src/model.zig:299-323): the
+    listed weight names, the sign widths and values; the block size must be 128
+    (src/model.zig:312) and every listed name an expert projection (src/model.zig:421-429)."""
+    for key in ("prism.hadamard.weight_names", "prism.hadamard.sign_widths", "prism.hadamard.sign_values",
+                "prism.hadamard.block_size"):
+        if not m.has(key):
+            raise GgufError(-18, key)
+    if int(m.metadata("prism.hadamard.block_size")) != 128:
+        raise UnsupportedConfiguration("prism.hadamard.block_size must be 128")
+    names = list(m.metadata("prism.hadamard.weight_names"))
+    for n in names:
+        if not n.endswith((".ffn_gate_exps.weight", ".ffn_up_exps.weight", ".ffn_down_exps.weight")):
+            raise UnsupportedConfiguration(f"prism.hadamard lists {n}, which this graph does not rotate")
+    return names, list(m.metadata("prism.hadamard.sign_widths")), list(m.metadata("prism.hadamard.sign_values"))
+
+
 def load_layer(path: str, layer: int):
     """One MoE layer of a GGUF file as a gyrodx.synth.Layer for gm_add_layer: the routed experts
     (load_layer_experts), the fp32 router "blk.<l>.ffn_gate_inp.weight" (E x n_expert),
@@ -226,11 +258,17 @@ def load_layer(path: str, layer: int):
     "<arch>.expert_weights_scale" (src/model.zig:262-285), and the explicit Hadamard signs of the
     gate and down inputs: a tensor listed in prism.hadamard.weight_names takes the run of
     prism.hadamard.sign_values that belongs to its input width (src/model.zig:306-333). The
-    rotation metadata is validated first (src/gguf.zig:182-250)."""
+    rotation metadata is validated first (src/gguf.zig:182-250), and refused as the loaders refuse
+    it: a block size other than 128 (src/model.zig:312), a listed tensor that is not an expert
+    projection (src/model.zig:421-429), or up-projection signs that are not the gate's
+    (src/gpu_engine.zig:404). The shared expert, when the file has one
+    ("blk.<l>.ffn_{gate,up,down}_shexp.weight" in bf16, Q8_0 or fp32, and the fp32
+    "blk.<l>.ffn_gate_inp_shexp.weight", src/model.zig:413-416), is read as well."""
     from .synth import Layer
     m = open_model(path)
     try:
         m.validate_gyro()
+        names, widths, values = _rotation(m)
         arch = m.metadata("general.architecture")
         n_used = int(m.metadata(f"{arch}.expert_used_count"))
         scale = float(m.metadata(f"{arch}.expert_weights_scale")) if m.has(f"{arch}.expert_weights_scale") else 0.0
@@ -242,26 +280,70 @@ def load_layer(path: str, layer: int):
         router = np.frombuffer(mm[r.file_offset:r.file_offset + r.byte_length], np.float32).reshape(NE, E)
 
         def signs(name: str, width: int):
-            if not m.has("prism.hadamard.weight_names") or name not in m.metadata("prism.hadamard.weight_names"):
+            """(offset into sign_values, signs) of a listed tensor, None when it is not listed."""
+            if name not in names:
                 return None
-            if m.metadata("prism.hadamard.sign_mode") != "explicit":
-                return np.ones(width, np.float32)
             off = 0
-            values = m.metadata("prism.hadamard.sign_values")
-            for w in m.metadata("prism.hadamard.sign_widths"):
+            for w in widths:
                 if w == width:
-                    return np.asarray(values[off:off + w], np.float32)
+                    return off, np.asarray(values[off:off + w], np.float32)
                 off += w
-            raise GgufError(-16, f"signs of width {width}")
+            raise UnsupportedConfiguration(f"no signs of width {width} for {name}")
 
         F = m.tensor(f"blk.{layer}.ffn_down_exps.weight").dims[0]
-        gate_signs = signs(f"blk.{layer}.ffn_gate_exps.weight", E)
-        down_signs = signs(f"blk.{layer}.ffn_down_exps.weight", F)
+        gs = signs(f"blk.{layer}.ffn_gate_exps.weight", E)
+        us = signs(f"blk.{layer}.ffn_up_exps.weight", E)
+        ds = signs(f"blk.{layer}.ffn_down_exps.weight", F)
+        # The gate and up products share one rotated input (src/gpu_engine.zig:404).
+        if us is not None and (gs is None or us[0] != gs[0]):
+            raise UnsupportedConfiguration("up-projection signs differ from the gate's")
+        shared = _shared_expert(m, mm, layer, E)
     finally:
         m.close()
     ex = load_layer_experts(path, layer)
     if ex["E"] != E or ex["n_expert"] != NE or ex["F"] != F:
         raise GgufError(-9, "router and expert shapes")
-    return Layer(E=E, F=ex["F"], n_expert=NE, n_used=n_used, types=ex["types"], gate=ex["gate"], up=ex["up"],
-                 down=ex["down"], router=np.ascontiguousarray(router), router_bias=None, gate_signs=gate_signs,
-                 down_signs=down_signs, expert_weights_scale=scale)
+    L = Layer(E=E, F=ex["F"], n_expert=NE, n_used=n_used, types=ex["types"], gate=ex["gate"], up=ex["up"],
+              down=ex["down"], router=np.ascontiguousarray(router), router_bias=None,
+              gate_signs=None if gs is None else gs[1], down_signs=None if ds is None else ds[1],
+              expert_weights_scale=scale)
+    if shared is not None:
+        L.SF, L.sh_type, L.sh_gate, L.sh_up, L.sh_down, L.sh_gate_inp = shared
+    return L
+
+
+# GGML tensor types of the shared expert's matrices that the engine accepts (src/kernels.zig:7-10)
+# and their row bytes for `cols` columns.
+SHARED_TYPES = {0: lambda c: c * 4, 30: lambda c: c * 2, 8: lambda c: c // 32 * 34}
+
+
+def _shared_expert(m: "Model", mm, layer: int, E: int):
+    """(SF, type, gate, up, down, gate_inp) of the layer's shared expert, or None when the file
+    has none: gate and up [SF rows of E columns], down [E rows of SF columns] as raw row bytes of
+    one GGML type (fp32, bf16 or Q8_0), gate_inp fp32 [E]."""
+    names = [f"blk.{layer}.ffn_{p}_shexp.weight" for p in ("gate", "up", "down")]
+    if not all(m.has_tensor(n) for n in names):
+        return None
+    ts = [m.tensor(n) for n in names]
+    ty = ts[0].type_id
+    if any(t.type_id != ty or t.rank != 2 for t in ts) or ty not in SHARED_TYPES:
+        raise GgufError(-14, names[0])
+    if ts[0].dims[0] != E or ts[1].dims != ts[0].dims:
+        raise GgufError(-9, "shared expert gate/up shape")
+    SF = ts[0].dims[1]
+    if ts[2].dims != (SF, E):
+        raise GgufError(-9, "shared expert down shape")
+    if ty == 8 and (E % 32 or SF % 32):
+        raise GgufError(-9, "Q8_0 rows need a multiple of 32 columns")
+
+    def rows(t, n_rows, cols):
+        rb = SHARED_TYPES[ty](cols)
+        if t.byte_length != n_rows * rb:
+            raise GgufError(-9, t.name)
+        return np.array(mm[t.file_offset:t.file_offset + t.byte_length]).reshape(n_rows, rb)
+
+    gi = m.tensor(f"blk.{layer}.ffn_gate_inp_shexp.weight")
+    if gi.type_id != 0 or gi.rank != 1 or gi.dims[0] != E:
+        raise GgufError(-14, gi.name)
+    gate_inp = np.frombuffer(mm[gi.file_offset:gi.file_offset + gi.byte_length], np.float32).copy()
+    return SF, ty, rows(ts[0], SF, E), rows(ts[1], SF, E), rows(ts[2], E, SF), gate_inp

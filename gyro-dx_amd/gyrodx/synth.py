@@ -8,7 +8,8 @@ are [n_expert * F rows][E columns] and down is [n_expert * E rows][F columns], e
 sequence of Gyro blocks (src/gyro.zig:70-76). Block scales are drawn as uniform binary16 bit
 patterns whose magnitude lies in [2^-8, 2^-3) with a random sign; the trellis stream bytes are
 uniform random. Router weights are N(0, 0.02) fp32, activations N(0, 1), Hadamard signs
-uniform +-1 (src/model.zig:305-330).
+uniform +-1 (src/model.zig:305-330). An optional shared expert has N(0, 0.02) weights stored as
+bf16, Q8_0 (per-32-block binary16 scale max|w| / 127, int8 quants) or fp32.
 """
 from __future__ import annotations
 
@@ -74,9 +75,10 @@ class Layer:
     down_signs: np.ndarray | None  # [F] fp32
     expert_weights_scale: float = 0.0
     SF: int = 0
-    sh_gate: np.ndarray | None = None  # [SF, E] bf16 bits
+    sh_type: int = 30                  # GGML type of the shared matrices: 30 bf16, 8 Q8_0, 0 fp32
+    sh_gate: np.ndarray | None = None  # [SF, row bytes(E)] (bf16: [SF, E] uint16 bits)
     sh_up: np.ndarray | None = None
-    sh_down: np.ndarray | None = None  # [E, SF] bf16 bits
+    sh_down: np.ndarray | None = None  # [E, row bytes(SF)] (bf16: [E, SF] uint16 bits)
     sh_gate_inp: np.ndarray | None = None  # [E] fp32
     norm_weight: np.ndarray | None = None  # [E] fp32, RMSNorm of the layer's input in a stack
     norm_eps: float = 1e-6
@@ -111,9 +113,24 @@ def zipf_bias(seed: int, n_expert: int, s: float = 1.1, factor: float = 1.0) -> 
     return bias.astype(np.float32)
 
 
+def q8_0_quantize(w: np.ndarray) -> np.ndarray:
+    """fp32 rows [rows, cols] to GGUF Q8_0 rows [rows, cols / 32 * 34]: per 32-block a binary16
+    scale d = max|w| / 127 and int8 quants round(w / d)."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    d = (np.abs(b).max(axis=2) / 127.0).astype(np.float16)
+    df = d.astype(np.float32)
+    q = np.clip(np.rint(np.divide(b, df[:, :, None], out=np.zeros_like(b), where=df[:, :, None] != 0)),
+                -127, 127).astype(np.int8)
+    out = np.empty((rows, cols // 32, 34), np.uint8)
+    out[:, :, :2] = d.view(np.uint8).reshape(rows, cols // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(rows, cols // 32 * 34)
+
+
 def make_layer(seed: int, E: int = 2048, F: int = 512, n_expert: int = 256, n_used: int = 8,
                type_id: int | None = TQ2_T, mixed_types: bool = False, zipf: float | None = None,
-               zipf_factor: float = 1.0, signs: bool = True, SF: int = 0) -> Layer:
+               zipf_factor: float = 1.0, signs: bool = True, SF: int = 0, sh_type: int = 30) -> Layer:
     if mixed_types:
         types = rng(seed, STREAM_TYPES).choice(np.array(sorted(TYPES), dtype=np.uint32),
                                                size=(n_expert, 3))
@@ -138,10 +155,13 @@ def make_layer(seed: int, E: int = 2048, F: int = 512, n_expert: int = 256, n_us
         def bf16(a):
             u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
             return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        conv = {30: bf16, 8: q8_0_quantize,
+                0: lambda a: np.ascontiguousarray(a, np.float32).view(np.uint8).reshape(a.shape[0], -1)}[sh_type]
         layer.SF = SF
-        layer.sh_gate = bf16(sh.standard_normal((SF, E)) * 0.02)
-        layer.sh_up = bf16(sh.standard_normal((SF, E)) * 0.02)
-        layer.sh_down = bf16(sh.standard_normal((E, SF)) * 0.02)
+        layer.sh_type = sh_type
+        layer.sh_gate = conv((sh.standard_normal((SF, E)) * 0.02).astype(np.float32))
+        layer.sh_up = conv((sh.standard_normal((SF, E)) * 0.02).astype(np.float32))
+        layer.sh_down = conv((sh.standard_normal((E, SF)) * 0.02).astype(np.float32))
         layer.sh_gate_inp = (sh.standard_normal(E) * 0.02).astype(np.float32)
     return layer
 

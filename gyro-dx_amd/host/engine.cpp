@@ -74,7 +74,9 @@ struct Layer {
     uint64_t base = 0;        // device address of expert 0's bundle; expert e at base + e * stride
     float max_scale = 0;      // largest |block scale| over the layer's experts
     uint32_t SF = 0;          // shared expert width (0: none)
-    Buffer sh_gu, sh_down, sh_gate;  // bf16 [2 SF][E] (gate rows, then up rows), [E][SF]; fp32 [E]
+    uint32_t sh_kind = GM_SHARED_BF16;  // row format of the shared matrices on the device
+    uint32_t sh_row_e = 0, sh_row_f = 0;  // device row bytes of the gate/up rows (E columns), down rows (SF)
+    Buffer sh_gu, sh_down, sh_gate;  // [2 SF] rows (gate, then up), [E] rows, in the mv kernels' format; fp32 [E]
     Buffer sh_gu16, sh_down16;       // binary16 copies x 2^k per matrix (prefill path)
     float sh_unscale[3] = {1, 1, 1}; // 2^-k of the gate, up and down copies
     Buffer norm;                     // fp32 [E] RMSNorm weight of the layer's input in a stack
@@ -142,21 +144,56 @@ uint16_t float_to_half(float f) {
     return sign | (uint16_t)(eb << 10) | (uint16_t)(r & 0x3ffu);
 }
 
-// Binary16 copy of n bf16 values times 2^k, k chosen so that the largest finite |value| lands in
-// [2^14, 2^15) (every bf16 value whose scaled magnitude is a normal binary16 converts exactly:
-// bf16 carries 8 significant bits, binary16 11). Returns 2^-k.
-float bf16_to_scaled_half(const uint16_t *src, size_t n, std::vector<uint16_t> &dst) {
+// Binary16 copy of n fp32 values times 2^k, k chosen so that the largest finite |value| lands in
+// [2^14, 2^15): every bf16 value whose scaled magnitude is a normal binary16 converts exactly (bf16
+// carries 8 significant bits, binary16 11); Q8_0 and fp32 weights round to nearest even.
+// Returns 2^-k.
+float floats_to_scaled_half(const float *src, size_t n, std::vector<uint16_t> &dst) {
     float mx = 0;
     for (size_t i = 0; i < n; ++i) {
-        const float v = std::fabs(bf16_to_float(src[i]));
+        const float v = std::fabs(src[i]);
         if (v == v && v != INFINITY) mx = std::max(mx, v);
     }
     int ex = 0;
     if (mx > 0) std::frexp(mx, &ex);  // mx < 2^ex
     const int k = mx > 0 ? 15 - ex : 0;
     dst.resize(n);
-    for (size_t i = 0; i < n; ++i) dst[i] = float_to_half(std::ldexp(bf16_to_float(src[i]), k));
+    for (size_t i = 0; i < n; ++i) dst[i] = float_to_half(std::ldexp(src[i], k));
     return std::ldexp(1.0f, -k);
+}
+
+// Shared-expert row formats: bytes of a source row of `cols` values (as gm_layer_desc gives it)
+// and of a device row (what mv_bf16 / mv_q8 / mv_f32 read; Q8_0 repacked by q8_repack).
+uint64_t shared_src_row(uint32_t kind, uint64_t cols) {
+    return kind == GM_SHARED_Q8_0 ? cols / 32 * 34 : kind == GM_SHARED_F32 ? cols * 4 : cols * 2;
+}
+uint64_t shared_dev_row(uint32_t kind, uint64_t cols) {
+    return kind == GM_SHARED_Q8_0 ? cols + cols / 16 : kind == GM_SHARED_F32 ? cols * 4 : cols * 2;
+}
+// fp32 values of rows x cols source rows of a shared matrix (Q8_0: d * q, exact in fp32).
+void shared_to_floats(uint32_t kind, const void *src, uint64_t rows, uint64_t cols, std::vector<float> &out) {
+    out.resize(rows * cols);
+    const uint8_t *p = static_cast<const uint8_t *>(src);
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint8_t *row = p + r * shared_src_row(kind, cols);
+        float *o = out.data() + r * cols;
+        if (kind == GM_SHARED_F32) {
+            std::memcpy(o, row, cols * 4);
+        } else if (kind == GM_SHARED_BF16) {
+            for (uint64_t i = 0; i < cols; ++i) {
+                uint16_t b;
+                std::memcpy(&b, row + 2 * i, 2);
+                o[i] = bf16_to_float(b);
+            }
+        } else {
+            for (uint64_t blk = 0; blk < cols / 32; ++blk) {
+                uint16_t h;
+                std::memcpy(&h, row + blk * 34, 2);
+                const float dscale = half_to_float(h);
+                for (uint64_t j = 0; j < 32; ++j) o[blk * 32 + j] = dscale * (float)(int8_t)row[blk * 34 + 2 + j];
+            }
+        }
+    }
 }
 
 std::vector<uint8_t> read_file(const std::string &path) {
@@ -195,10 +232,18 @@ static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocBase, "scratch regions o
 
 }  // namespace
 
+// Table indices and word offsets of the shared expert's intermediate buffers: the gate and up
+// rows h [n][2 SF], the SwiGLU a [n][SF], the output o [n][E], the gate dots g [n] and, on the
+// decode path, the gated output s [n][E].
+struct SharedBufs {
+    uint32_t h, h_off, a, a_off, o, o_off, g, g_off, s, s_off;
+};
+
 // Table indices (and word offsets) of the intermediate buffers of the decode path.
 struct DecodeBufs {
     uint32_t logits, logits_off, ids, ids_off, weights, weights_off, xh, xh_off, gu, gu_off;
-    uint32_t sh_h, sh_g;  // shared expert rows and gate dots (offset 0)
+    uint32_t sh_h, sh_g;  // the fused shared expert's rows and gate dots (offset 0)
+    SharedBufs shared;    // the shared expert outside the fused kernels
 };
 
 // Residual stream of a stack step: the layer input is normalised by the layer's RMSNorm inside
@@ -228,7 +273,13 @@ class Engine {
     Buffer staging, codebook, zeros;
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
     Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
+    // Activation range guard: word 0 of range_flag (set by moe_router, moe_prefill_router and
+    // moe_prefill_shared) and word kMetaRangeFlag of meta (set by the prefill gate/up GEMMs) become
+    // 1 when an activation rounded to binary16 is outside its range.
+    Buffer range_flag;
+    static constexpr uint32_t kMetaRangeFlag = 1022;
     Buffer sh_h, sh_a, sh_o, sh_g;  // shared expert: [T][2 SF], [T][SF], [T][E], [T]
+    Buffer sh_s;                    // decode path: sigmoid(g . x) * shared output (+ stream) [T][E]
     Buffer x16;                     // prefill shared expert: the unrotated input [T][E] binary16
     uint32_t sh_width = 0;          // SF the shared buffers are sized for
     Buffer tokens, outputs;
@@ -331,6 +382,8 @@ class Engine {
             std::memcpy(&h, book.data() + 2 * i, 2);
             max_codebook = std::max(max_codebook, std::fabs(half_to_float(h)));
         }
+        range_flag = dev.buffer(256, Kind::device);
+        fill_zero(range_flag);
         // Table entries of the no-allocation entry point: into this GPU's scratch array, and two
         // whose addresses each call sets (the caller's input and output).
         uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter));
@@ -343,7 +396,8 @@ class Engine {
 
     // The decode path's own intermediate buffers.
     DecodeBufs engine_bufs() const {
-        return {router_out.uav, 0, ids.uav, 0, weights.uav, 0, xh.uav, 0, gu_part.uav, 0, sh_h.uav, sh_g.uav};
+        return {router_out.uav, 0, ids.uav, 0, weights.uav, 0, xh.uav, 0, gu_part.uav, 0, sh_h.uav, sh_g.uav,
+                engine_shared()};
     }
 
     void allocate_activations() {
@@ -363,6 +417,7 @@ class Engine {
         hn = dev.buffer(T * E * f, Kind::device);
         order = dev.buffer(T * U * 4, Kind::device);
         meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
+        fill_zero(meta);
         // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
         Buffer z = dev.buffer(T * E * f, Kind::device);
         fill_zero(z);
@@ -374,6 +429,16 @@ class Engine {
     // adds at most one partial tile.
     uint32_t max_tiles(uint32_t n) const {
         return (n * U + kTileRows - 1) / kTileRows + std::min(NE, n * U);
+    }
+
+    // q8_repack of rows x cols GGUF Q8_0 rows at the start of src into dst (row_bytes per row).
+    void repack_q8(const Buffer &src, uint64_t rows, uint64_t cols, const Buffer &dst, uint32_t row_bytes) {
+        const uint64_t blocks = rows * (cols / 32);
+        const uint32_t groups = (uint32_t)((blocks + 255) / 256);
+        dev.begin();
+        dispatch("q8_repack", {src.srv, 0, (uint32_t)rows, (uint32_t)cols, 0, 0, 0, 0, dst.uav, 0, 0, 0, 0, 0, row_bytes, 0},
+                 std::min(groups, 65535u), (groups + 65534) / 65535);
+        dev.wait(dev.submit());
     }
 
     uint32_t add_layer(const gm_layer_desc &d) {
@@ -476,34 +541,58 @@ class Engine {
         L.norm_eps = d.norm_eps;
         if (d.SF) {
             if (!d.sh_gate || !d.sh_up || !d.sh_down || !d.sh_gate_inp) throw NativeError(-1, "shared expert weights missing");
+            if (d.sh_type > GM_SHARED_F32) throw NativeError(-1, "unknown shared expert row format");
+            if (d.SF % 64 || E % 64) throw NativeError(-1, "the shared expert needs E and SF multiples of 64");
             L.SF = d.SF;
-            const uint64_t half = (uint64_t)d.SF * E * 2;
-            if (half % 4) throw NativeError(-1, "shared expert shape must be word aligned");
-            L.sh_gu = dev.buffer(2 * half, Kind::device);
-            upload(L.sh_gu, 0, d.sh_gate, half);
-            upload(L.sh_gu, half, d.sh_up, half);
-            L.sh_down = dev.buffer(half, Kind::device);
-            upload(L.sh_down, 0, d.sh_down, half);
+            L.sh_kind = d.sh_type;
+            const uint64_t SF = d.SF, kind = d.sh_type;
+            const uint64_t src_e = shared_src_row(kind, E), src_f = shared_src_row(kind, SF);
+            L.sh_row_e = (uint32_t)shared_dev_row(kind, E);
+            L.sh_row_f = (uint32_t)shared_dev_row(kind, SF);
+            L.sh_gu = dev.buffer(2 * SF * L.sh_row_e, Kind::device);
+            L.sh_down = dev.buffer((uint64_t)E * L.sh_row_f, Kind::device);
+            if (kind == GM_SHARED_Q8_0) {
+                // Raw GGUF blocks into a temporary buffer, then q8_repack into the mv_q8 layout
+                // (src/gpu_engine.zig:289-306).
+                Buffer raw = dev.buffer(std::max(2 * SF * src_e, (uint64_t)E * src_f), Kind::device);
+                upload(raw, 0, d.sh_gate, SF * src_e);
+                upload(raw, SF * src_e, d.sh_up, SF * src_e);
+                repack_q8(raw, 2 * SF, E, L.sh_gu, L.sh_row_e);
+                upload(raw, 0, d.sh_down, (uint64_t)E * src_f);
+                repack_q8(raw, E, SF, L.sh_down, L.sh_row_f);
+                dev.release(raw);
+            } else {
+                upload(L.sh_gu, 0, d.sh_gate, SF * src_e);
+                upload(L.sh_gu, SF * src_e, d.sh_up, SF * src_e);
+                upload(L.sh_down, 0, d.sh_down, (uint64_t)E * src_f);
+            }
             L.sh_gate = dev.buffer((uint64_t)E * 4, Kind::device);
             upload(L.sh_gate, 0, d.sh_gate_inp, (uint64_t)E * 4);
+            // Binary16 copies for the prefill GEMMs, each matrix scaled by its own power of two.
+            const uint64_t half = SF * E * 2;
+            std::vector<float> fl;
             std::vector<uint16_t> h16;
             L.sh_gu16 = dev.buffer(2 * half, Kind::device);
-            L.sh_unscale[0] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_gate), half / 2, h16);
+            shared_to_floats(kind, d.sh_gate, SF, E, fl);
+            L.sh_unscale[0] = floats_to_scaled_half(fl.data(), fl.size(), h16);
             upload(L.sh_gu16, 0, h16.data(), half);
-            L.sh_unscale[1] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_up), half / 2, h16);
+            shared_to_floats(kind, d.sh_up, SF, E, fl);
+            L.sh_unscale[1] = floats_to_scaled_half(fl.data(), fl.size(), h16);
             upload(L.sh_gu16, half, h16.data(), half);
             L.sh_down16 = dev.buffer(half, Kind::device);
-            L.sh_unscale[2] = bf16_to_scaled_half(static_cast<const uint16_t *>(d.sh_down), half / 2, h16);
+            shared_to_floats(kind, d.sh_down, E, SF, fl);
+            L.sh_unscale[2] = floats_to_scaled_half(fl.data(), fl.size(), h16);
             upload(L.sh_down16, 0, h16.data(), half);
             if (!x16.handle) x16 = dev.buffer((uint64_t)max_tok * E * 2, Kind::device);
             if (d.SF > sh_width) {
-                for (Buffer *b : {&sh_h, &sh_a, &sh_o, &sh_g})
+                for (Buffer *b : {&sh_h, &sh_a, &sh_o, &sh_g, &sh_s})
                     if (b->handle) dev.release(*b);
                 const uint64_t T = max_tok;
                 sh_h = dev.buffer(T * 2 * d.SF * 4, Kind::device);
                 sh_a = dev.buffer(T * d.SF * 4, Kind::device);
                 sh_o = dev.buffer(T * E * 4, Kind::device);
                 sh_g = dev.buffer(T * 4, Kind::device);
+                sh_s = dev.buffer(T * E * 4, Kind::device);
                 sh_width = d.SF;
             }
         }
@@ -555,7 +644,7 @@ class Engine {
         dev.barrier();
         uint32_t sh = sh_zero.uav, shg = sh_zero.uav;  // no shared expert: sigmoid(0) * 0
         if (L.SF) {
-            shared_expert(L, n, x_uav, x_off);
+            shared_expert(L, n, x_uav, x_off, engine_shared());
             sh = sh_o.uav;
             shg = sh_g.uav;
         }
@@ -580,14 +669,21 @@ class Engine {
         }
     }
 
-    // Shared expert of src/engine.zig:644-653 on the unrotated input (sh_o = W_d (silu(W_g x) *
-    // W_u x), sh_g = g . x), in the reference's kernels: mv_bf16, ew SwiGLU, mv_bf16, mv_f32.
-    void shared_expert(const Layer &L, uint32_t n, uint32_t x_uav, uint32_t x_off) {
+    // Shared expert of src/engine.zig:644-653 on the unrotated input, in the reference's kernels
+    // (src/gpu_engine.zig:1061-1074): the gate and up rows by the mv kernel of the row format
+    // (mv_bf16, mv_q8, mv_f32) into h, the ew SwiGLU into a, the down rows into o = W_d (silu(W_g x)
+    // * W_u x), and g = g_sh . x by mv_f32. Buffers are (table index, word offset) pairs.
+    SharedBufs engine_shared() const { return {sh_h.uav, 0, sh_a.uav, 0, sh_o.uav, 0, sh_g.uav, 0, sh_s.uav, 0}; }
+    static const char *mv_kernel(uint32_t kind) {
+        return kind == GM_SHARED_Q8_0 ? "mv_q8" : kind == GM_SHARED_F32 ? "mv_f32" : "mv_bf16";
+    }
+    void shared_expert(const Layer &L, uint32_t n, uint32_t x_uav, uint32_t x_off, const SharedBufs &S) {
         const uint32_t SF = L.SF;
-        mv("mv_bf16", L.sh_gu.srv, 2 * SF, E, E * 2, x_uav, x_off, E, n, sh_h.uav, 0, 2 * SF);
-        dispatch("ew", {sh_h.uav, 0, 2 * SF, sh_h.uav, SF, 2 * SF, sh_a.uav, 0, SF, SF, n, 0}, (SF * n + 255) / 256);
-        mv("mv_bf16", L.sh_down.srv, E, SF, SF * 2, sh_a.uav, 0, SF, n, sh_o.uav, 0, E);
-        mv("mv_f32", L.sh_gate.srv, 1, E, E * 4, x_uav, x_off, E, n, sh_g.uav, 0, 1);
+        const char *k = mv_kernel(L.sh_kind);
+        mv(k, L.sh_gu.srv, 2 * SF, E, L.sh_row_e, x_uav, x_off, E, n, S.h, S.h_off, 2 * SF);
+        dispatch("ew", {S.h, S.h_off, 2 * SF, S.h, S.h_off + SF, 2 * SF, S.a, S.a_off, SF, SF, n, 0}, (SF * n + 255) / 256);
+        mv(k, L.sh_down.srv, E, SF, L.sh_row_f, S.a, S.a_off, SF, n, S.o, S.o_off, E);
+        mv("mv_f32", L.sh_gate.srv, 1, E, E * 4, x_uav, x_off, E, n, S.g, S.g_off, 1);
     }
 
     // Any layer (mixed Gyro types, optional shared expert), in the reference's dispatch style:
@@ -617,30 +713,36 @@ class Engine {
                  (E + 31) / 32, n_slots, 1);
         uint32_t sh = sh_zero.uav, shg = sh_zero.uav;
         if (L.SF) {
-            shared_expert(L, n, x_uav, x_off);
+            shared_expert(L, n, x_uav, x_off, engine_shared());
             sh = sh_o.uav;
             shg = sh_g.uav;
         }
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
-    // Uniform TQ2_T layers without a shared expert: E a multiple of 256 up to 4096, F a
-    // multiple of 128 up to 1024, top-1 to top-16 (moe_decode_gu for E a multiple of 1024 and
-    // top-8, moe_decode_gu_g otherwise; moe_decode_down for F 512, top-8 and at most two
-    // K-parts, moe_decode_down_g otherwise). Other layers: the type-generic kernels.
+    // Routed experts: uniform TQ2_T layers take moe_decode_gu (E a multiple of 1024, top-8) or
+    // moe_decode_gu_g (E a multiple of 256 up to 4096, F a multiple of 128 up to 1024, top-1..16),
+    // and moe_decode_down (F 512, top-8, at most two K-parts) or moe_decode_down_g; other layers
+    // the type-generic kernels (_x for E a multiple of 1024, F 512, top-8; _xg otherwise).
+    // Shared expert: a bf16 one of width <= 1024 (a multiple of 256) on E <= 2048 at the _x shapes
+    // runs fused into moe_router and moe_decode_down_x; any other (bf16, Q8_0 or fp32, any width
+    // a multiple of 64) runs in the mv kernels first and enters the down kernel as its residual
+    // input, sigmoid(g . x) * W_d (silu(W_g x) * W_u x).
     bool decode_supported(const Layer &L, uint32_t n) const {
-        if (NE > 256 || n > 8) return false;
-        if (!decode_generic_types(L))
-            return E % 256 == 0 && E <= 4096 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
-        // A shared expert runs fused into moe_router and moe_decode_down_x (hidden 2048-class
-        // shapes); other shapes take moe_decode_gu_xg / moe_decode_down_xg without one.
-        if (decode_generic_tuned()) return !L.SF || (L.SF <= 1024 && L.SF % 256 == 0 && E <= 2048);
-        return !L.SF && E % 256 == 0 && E <= 4096 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
+        if (NE > 256 || n > 8 || E > 4096) return false;
+        if (decode_fused_shared(L)) return true;
+        const bool general = E % 256 == 0 && F % 128 == 0 && F <= 1024 && U >= 1 && U <= 16;
+        if (L.type_id == 144) return general;
+        return decode_generic_tuned() || general;
     }
     bool decode_generic_tuned() const { return E % 1024 == 0 && F == 512 && U == 8; }
     bool decode_fast_down() const { return F == 512 && U == 8 && parts <= 2; }
-    // Layers other than uniform TQ2_T without a shared expert take the type-generic kernels.
-    static bool decode_generic_types(const Layer &L) { return L.type_id != 144 || L.SF; }
+    bool decode_fused_shared(const Layer &L) const {
+        return L.SF && L.sh_kind == GM_SHARED_BF16 && decode_generic_tuned() && L.SF <= 1024 && L.SF % 256 == 0 &&
+               E <= 2048;
+    }
+    // Layers other than uniform TQ2_T (or with the fused shared expert) take the type-generic kernels.
+    bool decode_generic_types(const Layer &L) const { return L.type_id != 144 || decode_fused_shared(L); }
 
     // MI355X decode path: router + rotation, routed gate/up, down + combine.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
@@ -650,17 +752,29 @@ class Engine {
         const DecodeBufs B = bufs ? *bufs : engine_bufs();
         if (!decode_supported(L, n))
             throw NativeError(-1, "decode path needs <= 256 experts, n <= 8, E a multiple of 256 up to 4096, F a "
-                                  "multiple of 128 up to 1024 and top-1..16; a shared expert (on a layer of another "
-                                  "type than uniform TQ2_T) needs E % 1024 == 0, F == 512, top-8, width <= 1024, "
-                                  "a multiple of 256, and E <= 2048");
+                                  "multiple of 128 up to 1024 and top-1..16 (or, for other than uniform TQ2_T "
+                                  "experts, E a multiple of 1024 with F 512 and top-8)");
+        const bool fused_sh = decode_fused_shared(L);
+        if (L.SF && !fused_sh) {
+            // The shared expert first; its gated output (plus a stack's stream) is the residual
+            // input of the down kernel.
+            const SharedBufs &S = B.shared;
+            shared_expert(L, n, x_uav, x_off, S);
+            dispatch("ew", {S.o, S.o_off, E, S.g, S.g_off, 1, S.s, S.s_off, E, E, n, 4}, (E * n + 255) / 256);
+            if (st.res_uav != kNone)
+                dispatch("ew", {S.s, S.s_off, E, st.res_uav, st.res_off, E, S.s, S.s_off, E, E, n, 2}, (E * n + 255) / 256);
+            st.res_uav = S.s;
+            st.res_off = S.s_off;
+        }
+        const uint32_t rsf = fused_sh ? L.SF : 0u;  // shared rows computed inside moe_router
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
                               B.logits, B.logits_off, L.has_gate_signs ? L.signs.srv : kNone, 0, B.xh, B.xh_off,
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
-                              bits(L.norm_eps), 2 * L.SF, L.SF ? L.sh_gu.srv : 0u, L.SF ? B.sh_h : 0u,
-                              L.SF ? L.sh_gate.srv : 0u, L.SF ? B.sh_g : 0u},
-                             std::max(NE, E / 128) + (L.SF ? 2 * L.SF / 4 + 1 : 0));
+                              bits(L.norm_eps), 2 * rsf, rsf ? L.sh_gu.srv : 0u, rsf ? B.sh_h : 0u,
+                              rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u, flag_uav()},
+                             std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
         if (!decode_generic_types(L)) {
             dispatch_maybe_timed(bracket == 2, marks, E % 1024 == 0 && U == 8 ? "moe_decode_gu" : "moe_decode_gu_g",
                                  {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
@@ -689,8 +803,8 @@ class Engine {
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
                              {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
-                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, L.SF ? 1u : 0u, B.sh_h, 0,
-                              B.sh_g, 0, L.SF ? L.sh_down.srv : 0u, L.SF},
+                              st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, rsf ? 1u : 0u, B.sh_h, 0,
+                              B.sh_g, 0, rsf ? L.sh_down.srv : 0u, rsf},
                              E / 16, n);
     }
 
@@ -727,7 +841,7 @@ class Engine {
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
-                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks},
+                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks, flag_uav()},
                              (n + 31) / 32, (NE + 31) / 32, ks);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U},
@@ -737,7 +851,7 @@ class Engine {
         if (L.type_id == 144) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
                                  {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
-                                  codebook.srv, signs, E, act.uav, 0, E, F, U},
+                                  codebook.srv, signs, E, act.uav, 0, E, F, U, 1u},
                                  F / 128, tiles);
             dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down",
                                  {meta.uav, order.uav, 0, act.uav, 0, base_lo, base_hi, slot_stride, 2 * L.gate_bytes,
@@ -746,7 +860,7 @@ class Engine {
         } else {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu_x",
                                  {meta.uav, order.uav, 0, xh.uav, 0, L.xtab.srv, codebook.srv, signs, E, act.uav, 0, E,
-                                  F, U},
+                                  F, U, 1u},
                                  F / 128, tiles);
             dispatch_maybe_timed(bracket == 3, marks, "moe_prefill_down_x",
                                  {meta.uav, order.uav, 0, act.uav, 0, L.xtab.srv, codebook.srv, down.uav, 0, E, F},
@@ -758,7 +872,7 @@ class Engine {
             const uint32_t tt = (n + 63) / 64;
             dispatch_maybe_timed(bracket == 7, marks, "moe_prefill_shared",
                                  {0, x16.uav, 0, E, L.sh_gu16.srv, 0, E, sh_a.uav, 0, n, L.SF, bits(L.sh_unscale[0]),
-                                  bits(L.sh_unscale[1]), L.SF},
+                                  bits(L.sh_unscale[1]), L.SF, flag_uav()},
                                  L.SF / 64, tt);
             dispatch_maybe_timed(bracket == 8, marks, "moe_prefill_shared",
                                  {1, sh_a.uav, 0, L.SF, L.sh_down16.srv, 0, L.SF, sh_o.uav, 0, n, 0,
@@ -837,6 +951,10 @@ class Engine {
             if (list[l] >= layers.size()) throw NativeError(-1, "layer index out of range");
     }
 
+    // A fast path (decode, prefill) whose activations left the binary16 range is recomputed on
+    // the generic path, which keeps them in fp32.
+    static bool fast_path(uint32_t path) { return path == GM_PATH_DECODE || path == GM_PATH_PREFILL; }
+
     void forward_stack(const uint32_t *list, uint32_t n_layers, uint32_t path, const float *x, uint32_t n, float *y) {
         if (n == 0 || n > max_tok) throw NativeError(-1, "token count exceeds max_tok");
         check_stack(list, n_layers);
@@ -844,8 +962,30 @@ class Engine {
         dev.begin();
         stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
         dev.wait(dev.submit());
+        if (fast_path(path) && take_range_flag()) {
+            upload(x_in, 0, x, (uint64_t)n * E * 4);
+            dev.begin();
+            stack(list, n_layers, GM_PATH_GENERIC, n, x_in.uav, 0, x_in.uav, 0);
+            dev.wait(dev.submit());
+        }
         check(gd_readback(dev.ctx, x_in.handle, 0, n * E * 4, y, kTimeoutMs), "gd_readback");
     }
+
+    // Reads and clears the activation range flags; true when a fast-path kernel rounded an
+    // activation outside the binary16 range since the last call.
+    bool take_range_flag() {
+        uint32_t f = 0, g = 0;
+        check(gd_readback(dev.ctx, range_flag.handle, 0, 4, &f, kTimeoutMs), "gd_readback");
+        if (meta.handle) check(gd_readback(dev.ctx, meta.handle, kMetaRangeFlag * 4, 4, &g, kTimeoutMs), "gd_readback");
+        if (!f && !g) return false;
+        const uint32_t zero = 0;
+        upload(range_flag, 0, &zero, 4);
+        if (meta.handle) upload(meta, kMetaRangeFlag * 4, &zero, 4);
+        return true;
+    }
+    // The flag's table index for kernels of the fast paths (none on direct launches, whose
+    // callers do not read it).
+    uint32_t flag_uav() const { return direct ? 0u : range_flag.uav; }
 
     // gm_forward_decode_noalloc: the decode path on device-resident x and y, its intermediate
     // buffers carved out of this GPU's scratch array (256-byte aligned, word offsets), queued on
@@ -869,8 +1009,18 @@ class Engine {
         B.gu_off = take((uint64_t)parts * n * U * 2 * F * 4);
         B.sh_h = na_shh.uav;
         B.sh_g = na_shg.uav;
-        if (at > GM_NOALLOC_SCRATCH_BYTES || (uint64_t)n * 2 * L.SF * 4 > kNoallocShHBytes ||
-            (uint64_t)n * 4 > kNoallocShGBytes)
+        B.shared = {};
+        if (L.SF && !decode_fused_shared(L)) {
+            SharedBufs &S = B.shared;
+            S.h = S.a = S.o = S.g = S.s = na_base.uav;
+            S.h_off = take((uint64_t)n * 2 * L.SF * 4);
+            S.a_off = take((uint64_t)n * L.SF * 4);
+            S.o_off = take((uint64_t)n * E * 4);
+            S.g_off = take((uint64_t)n * 4);
+            S.s_off = take((uint64_t)n * E * 4);
+        }
+        if (at > GM_NOALLOC_SCRATCH_BYTES ||
+            (decode_fused_shared(L) && ((uint64_t)n * 2 * L.SF * 4 > kNoallocShHBytes || (uint64_t)n * 4 > kNoallocShGBytes)))
             throw NativeError(-1, "the layer's decode buffers exceed the GM_NOALLOC_SCRATCH_BYTES scratch array");
         direct = true;
         direct_stream = stream;
@@ -893,6 +1043,11 @@ class Engine {
         dev.begin();
         ffn(path, il, n, x_in.uav, 0, out.uav, 0);
         dev.wait(dev.submit());
+        if (fast_path(path) && take_range_flag()) {
+            dev.begin();
+            ffn(GM_PATH_GENERIC, il, n, x_in.uav, 0, out.uav, 0);
+            dev.wait(dev.submit());
+        }
         check(gd_readback(dev.ctx, out.handle, 0, n * E * 4, y, kTimeoutMs), "gd_readback");
     }
 };
@@ -1057,6 +1212,9 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
         if (bracket_us) *bracket_us = br_n ? br / (double)br_n : 0.0;
+        if (Engine::fast_path(path) && e.take_range_flag())
+            throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
+                                        "are invalid (gm_forward recomputes such calls on GM_PATH_GENERIC)");
     });
 }
 
@@ -1093,6 +1251,9 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         }
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
+        if (Engine::fast_path(path) && e.take_range_flag())
+            throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
+                                        "are invalid (gm_forward_stack recomputes such calls on GM_PATH_GENERIC)");
     });
 }
 

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <unordered_set>
 #include <vector>
@@ -302,7 +303,9 @@ void validate_gyro(const gg_model &m) {
         if (!seen.insert(name).second) throw Fail{GG_INVALID_METADATA};
         const Tensor *t = find(&m, name.c_str());
         if (!t || t->dims[0] % b) throw Fail{GG_INVALID_METADATA};
-        if (expl && std::find(widths.begin(), widths.end(), (int32_t)t->dims[0]) == widths.end())
+        // Widths compare as u64 with the tensor's first dimension (src/gguf.zig:237).
+        if (expl && std::none_of(widths.begin(), widths.end(),
+                                 [&](int32_t w) { return (uint64_t)w == t->dims[0]; }))
             throw Fail{GG_INVALID_METADATA};
     }
     for (const char *key : {"prism.hadamard.gdn_v_grouped", "prism.hadamard.tied_output"}) {
@@ -318,25 +321,21 @@ bool ends_with(const std::string &s, const char *suffix) {
     return s.size() >= n && s.compare(s.size() - n, n, suffix) == 0;
 }
 
-}  // namespace
-
-extern "C" {
-
-int gg_parse(const uint8_t *prefix, size_t prefix_len, uint64_t file_size, gg_model **out) {
-    if (!out || (!prefix && prefix_len)) return GG_INVALID_METADATA;
-    *out = nullptr;
-    auto *m = new gg_model;
+// No C++ exception crosses the C boundary: allocation failures (std::bad_alloc, and the
+// length errors of containers asked to grow past their limits) return GG_OUT_OF_MEMORY, the
+// reference's allocator error.
+template <typename Fn>
+int guarded(Fn fn) {
     try {
-        parse(prefix, prefix_len, file_size, *m);
+        return fn();
     } catch (const Fail &f) {
-        delete m;
         return f.code;
+    } catch (...) {
+        return GG_OUT_OF_MEMORY;
     }
-    *out = m;
-    return GG_OK;
 }
 
-int gg_open(const char *path, gg_model **out) {
+int gg_open_impl(const char *path, gg_model **out) {
     if (!out) return GG_INVALID_METADATA;
     *out = nullptr;
     FILE *f = std::fopen(path, "rb");
@@ -353,6 +352,25 @@ int gg_open(const char *path, gg_model **out) {
     std::fclose(f);
     if (got != prefix.size()) return GG_IO;
     return gg_parse(prefix.data(), prefix.size(), (uint64_t)size, out);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gg_parse(const uint8_t *prefix, size_t prefix_len, uint64_t file_size, gg_model **out) {
+    if (!out || (!prefix && prefix_len)) return GG_INVALID_METADATA;
+    *out = nullptr;
+    return guarded([&] {
+        std::unique_ptr<gg_model> m(new gg_model);
+        parse(prefix, prefix_len, file_size, *m);
+        *out = m.release();
+        return (int)GG_OK;
+    });
+}
+
+int gg_open(const char *path, gg_model **out) {
+    return guarded([&] { return gg_open_impl(path, out); });
 }
 
 void gg_free(gg_model *m) { delete m; }
@@ -391,9 +409,12 @@ int gg_expert_range(const gg_model *m, const char *name, uint32_t expert, uint64
 
 int gg_is_expert_tensor(const char *name) {
     if (!name) return 0;
-    const std::string s(name);
-    return ends_with(s, ".ffn_gate_exps.weight") || ends_with(s, ".ffn_up_exps.weight") ||
-           ends_with(s, ".ffn_down_exps.weight");
+    const size_t n = std::strlen(name);
+    for (const char *suffix : {".ffn_gate_exps.weight", ".ffn_up_exps.weight", ".ffn_down_exps.weight"}) {
+        const size_t k = std::strlen(suffix);
+        if (n >= k && std::memcmp(name + n - k, suffix, k) == 0) return 1;
+    }
+    return 0;
 }
 
 int gg_metadata_u64(const gg_model *m, const char *key, uint64_t *out) {
@@ -422,12 +443,10 @@ int gg_metadata_raw(const gg_model *m, const char *key, uint32_t *kind, const ui
 
 int gg_validate_gyro(const gg_model *m) {
     if (!m) return GG_INVALID_METADATA;
-    try {
+    return guarded([&] {
         validate_gyro(*m);
-    } catch (const Fail &f) {
-        return f.code;
-    }
-    return GG_OK;
+        return (int)GG_OK;
+    });
 }
 
 }  // extern "C"

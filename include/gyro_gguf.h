@@ -40,6 +40,7 @@ enum gg_error {
     GG_IO = -17, /* the file could not be opened or read (gg_open only) */
     GG_NOT_FOUND = -18,
     GG_UNSUPPORTED_GYRO_METADATA = -19,
+    GG_OUT_OF_MEMORY = -20, /* an allocation failed (the reference's allocator error) */
 };
 
 typedef struct gg_model gg_model;

@@ -48,19 +48,26 @@ typedef struct gm_layer_desc {
     const uint8_t *const *up;
     const uint8_t *const *down;
     const uint32_t *types;
-    /* Optional shared SwiGLU expert (src/engine.zig:644-653), SF = 0 for none: bf16 gate and up
-     * [SF][E], down [E][SF], and the fp32 gate input [E]: out += sigmoid(g . x) * W_d (silu(W_g x)
-     * * W_u x) on the unrotated input x. */
+    /* Optional shared SwiGLU expert (src/engine.zig:644-653), SF = 0 for none: gate and up [SF]
+     * rows of E columns, down [E] rows of SF columns, in the row format sh_type names (bf16; GGUF
+     * Q8_0 blocks; fp32), and the fp32 gate input [E]: out += sigmoid(g . x) * W_d (silu(W_g x)
+     * * W_u x) on the unrotated input x. E and SF must be multiples of 64. */
     uint32_t SF;
-    const uint16_t *sh_gate;
-    const uint16_t *sh_up;
-    const uint16_t *sh_down;
+    const void *sh_gate;
+    const void *sh_up;
+    const void *sh_down;
     const float *sh_gate_inp;
     /* RMSNorm applied to this layer's input inside a stack (gm_forward_stack, gm_run_stack): fp32
      * weight [E] or NULL (no weight), and eps (src/kernels.zig:281-291). */
     const float *norm_weight;
     float norm_eps;
+    /* Row format of the shared expert's matrices: GM_SHARED_BF16 (default), GM_SHARED_Q8_0
+     * (34-byte blocks of a binary16 scale and 32 int8 quants, repacked at upload as
+     * src/gpu_engine.zig:289-306 does) or GM_SHARED_F32. */
+    uint32_t sh_type;
 } gm_layer_desc;
+
+enum { GM_SHARED_BF16 = 0, GM_SHARED_Q8_0 = 1, GM_SHARED_F32 = 2 };
 
 /* Creates an engine on device `adapter`, loading every <name>.co pipeline in kernel_dir.
  * max_tok bounds the tokens of one gm_forward/gm_run call (the reference uses passes of 64). */

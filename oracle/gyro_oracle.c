@@ -224,6 +224,43 @@ float go_dot_bf16(const uint16_t *row, const float *x, size_t n) {
 /* src/kernels.zig:253-261. */
 float go_dot_dense(const float *a, const float *b, size_t n) { return go_dot_f32(a, b, n); }
 
+/* dotQ8, src/kernels.zig:107-120: per 32-block, d * (sum of q * x) (the block sum in 8 lanes). */
+static float dot_q8(const uint8_t *row, const float *x, size_t n) {
+    float total = 0;
+    for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *block = row + b * 34;
+        const float d = go_fp16_to_fp32((uint16_t)(block[0] | (block[1] << 8)));
+        float acc[8] = {0};
+        for (size_t i = 0; i < 32; i += 8)
+            for (int l = 0; l < 8; ++l) acc[l] += (float)(int8_t)block[2 + i + l] * x[b * 32 + i + l];
+        total += d * (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])));
+    }
+    return total;
+}
+
+size_t go_dense_row_bytes(uint32_t type_id, size_t cols) {
+    switch (type_id) {
+        case 0: return cols * 4;
+        case 30: return cols * 2;
+        case 8: return cols % 32 ? 0 : cols / 32 * 34;
+        default: return 0;
+    }
+}
+
+
+/* fp32 value i of a dense row (decodeRow, src/kernels.zig:213-235, for the dense types). */
+static float dense_value(uint32_t type_id, const void *row, size_t i) {
+    switch (type_id) {
+        case 0: return ((const float *)row)[i];
+        case 30: return bf16_to_f32(((const uint16_t *)row)[i]);
+        case 8: {
+            const uint8_t *block = (const uint8_t *)row + (i / 32) * 34;
+            return go_fp16_to_fp32((uint16_t)(block[0] | (block[1] << 8))) * (float)(int8_t)block[2 + i % 32];
+        }
+        default: return 0;
+    }
+}
+
 /* src/kernels.zig:136-159: one block of 128 values in the stored basis. */
 static void decode_block(const type_row *t, const uint8_t *block, float out[128]) {
     float scale = go_fp16_to_fp32((uint16_t)(block[0] | (block[1] << 8)));
@@ -284,10 +321,19 @@ static float dot_gyro_generic(const type_row *t, const uint8_t *row, const float
     return total;
 }
 
-/* src/kernels.zig:201-210 (Gyro types only on this path). */
+/* src/kernels.zig:201-210: the dense types of the shared expert (fp32, bf16, Q8_0) and the Gyro
+ * types; 0 for any other type. */
 float go_dot_row(uint32_t type_id, const uint8_t *row, const float *x, size_t cols) {
-    if (type_id == 144) return dot_tq2(row, x, cols);
-    return dot_gyro_generic(find_type(type_id), row, x, cols);
+    switch (type_id) {
+        case 0: return go_dot_f32((const float *)(const void *)row, x, cols);
+        case 30: return go_dot_bf16((const uint16_t *)(const void *)row, x, cols);
+        case 8: return dot_q8(row, x, cols);
+        case 144: return dot_tq2(row, x, cols);
+        default: {
+            const type_row *t = find_type(type_id);
+            return t ? dot_gyro_generic(t, row, x, cols) : 0.0f;
+        }
+    }
 }
 
 /* src/kernels.zig:213-235 (Gyro types). */
@@ -461,7 +507,8 @@ typedef struct ffn_ctx {
     const uint32_t *starts;
     const float *y_in;   /* matmul input for the shared expert */
     float *y_out;
-    const uint16_t *mat;
+    const uint8_t *mat;
+    uint32_t mat_type;
     size_t mat_rows, mat_cols;
 } ffn_ctx;
 
@@ -477,14 +524,15 @@ static void router_range(void *c_, size_t start, size_t end) {
         }
 }
 
-/* kernels.matmul for a bf16 matrix: one decoded row reused for every token
- * (src/kernels.zig:244-250 matvecRange). */
-static void bf16_range(void *c_, size_t start, size_t end) {
+/* kernels.matmul for a dense matrix of the shared expert, one row at a time for every token
+ * (src/kernels.zig:244-250 matvecRange, dotRow per row). */
+static void dense_range(void *c_, size_t start, size_t end) {
     ffn_ctx *c = (ffn_ctx *)c_;
+    const size_t rb = go_dense_row_bytes(c->mat_type, c->mat_cols);
     for (size_t r = start; r < end; ++r)
         for (size_t t = 0; t < c->n; ++t)
             c->y_out[t * c->mat_rows + r] =
-                go_dot_bf16(c->mat + r * c->mat_cols, c->y_in + t * c->mat_cols, c->mat_cols);
+                go_dot_row(c->mat_type, c->mat + r * rb, c->y_in + t * c->mat_cols, c->mat_cols);
 }
 
 /* Phase 1, src/engine.zig:568-602: one task per (expert, row) of gate and up. */
@@ -555,6 +603,9 @@ static int check_layer(const go_layer *l) {
     for (uint32_t e = 0; e < l->n_expert; ++e)
         if (!find_type(l->gate_type[e]) || !find_type(l->up_type[e]) || !find_type(l->down_type[e]))
             return GO_UNSUPPORTED_TYPE;
+    if (l->SF && (!l->sh_gate || !l->sh_up || !l->sh_down || !go_dense_row_bytes(l->sh_type, l->E) ||
+                  !go_dense_row_bytes(l->sh_type, l->SF)))
+        return GO_UNSUPPORTED_TYPE;
     if (!g_codebook_ready) return GO_INVALID_SOURCE_LENGTH;
     return GO_OK;
 }
@@ -652,19 +703,20 @@ int go_moe_ffn(const go_layer *l, const float *x, size_t n, float *out, go_trace
         c.y_in = x;
         c.mat_cols = E;
         c.mat_rows = SF;
-        c.mat = l->sh_gate;
+        c.mat_type = l->sh_type;
+        c.mat = (const uint8_t *)l->sh_gate;
         c.y_out = sg;
-        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, bf16_range);
-        c.mat = l->sh_up;
+        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, dense_range);
+        c.mat = (const uint8_t *)l->sh_up;
         c.y_out = su;
-        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, bf16_range);
+        pool_run(pool_ptr, SF, chunk_for(pool_ptr, SF, 8), &c, dense_range);
         for (size_t i = 0; i < n * SF; ++i) sg[i] = go_silu(sg[i]) * su[i];
         c.y_in = sg;
         c.mat_cols = SF;
         c.mat_rows = E;
-        c.mat = l->sh_down;
+        c.mat = (const uint8_t *)l->sh_down;
         c.y_out = sd;
-        pool_run(pool_ptr, E, chunk_for(pool_ptr, E, 8), &c, bf16_range);
+        pool_run(pool_ptr, E, chunk_for(pool_ptr, E, 8), &c, dense_range);
         for (size_t t = 0; t < n; ++t) {
             float gate = l->sh_gate_inp ? go_sigmoid(go_dot_dense(l->sh_gate_inp, x + t * E, E))
                                         : l->sh_gate_const;
@@ -765,11 +817,13 @@ int go_moe_dense_f64(const go_layer *l, const float *x, size_t n, const uint32_t
         if (l->SF) {
             const size_t SF = l->SF;
             double *sg = (double *)malloc(SF * sizeof(double));
+            const size_t rbe = go_dense_row_bytes(l->sh_type, E), rbf = go_dense_row_bytes(l->sh_type, SF);
             for (size_t r = 0; r < SF; ++r) {
                 double s1 = 0, s2 = 0;
+                const uint8_t *gr = (const uint8_t *)l->sh_gate + r * rbe, *ur = (const uint8_t *)l->sh_up + r * rbe;
                 for (size_t i = 0; i < E; ++i) {
-                    s1 += (double)bf16_to_f32(l->sh_gate[r * E + i]) * (double)x[t * E + i];
-                    s2 += (double)bf16_to_f32(l->sh_up[r * E + i]) * (double)x[t * E + i];
+                    s1 += (double)dense_value(l->sh_type, gr, i) * (double)x[t * E + i];
+                    s2 += (double)dense_value(l->sh_type, ur, i) * (double)x[t * E + i];
                 }
                 sg[r] = silu64(s1) * s2;
             }
@@ -783,7 +837,8 @@ int go_moe_dense_f64(const go_layer *l, const float *x, size_t n, const uint32_t
             }
             for (size_t r = 0; r < E; ++r) {
                 double s = 0;
-                for (size_t i = 0; i < SF; ++i) s += (double)bf16_to_f32(l->sh_down[r * SF + i]) * sg[i];
+                const uint8_t *dr = (const uint8_t *)l->sh_down + r * rbf;
+                for (size_t i = 0; i < SF; ++i) s += (double)dense_value(l->sh_type, dr, i) * sg[i];
                 o[r] += gate * s;
             }
             free(sg);

@@ -88,11 +88,15 @@ float go_sigmoid(float x);                                                      
 float go_dot_f32(const float *row, const float *x, size_t n);                    /* :72-84 */
 float go_dot_bf16(const uint16_t *row, const float *x, size_t n);                /* :86-105 */
 float go_dot_dense(const float *a, const float *b, size_t n);                    /* :253-261 */
-float go_dot_row(uint32_t type_id, const uint8_t *row, const float *x, size_t cols); /* :201-210 */
+/* :201-210; also the dense types fp32 (0), bf16 (30) and Q8_0 (8, dotQ8 :107-120) */
+float go_dot_row(uint32_t type_id, const uint8_t *row, const float *x, size_t cols);
 void go_decode_row_fast(uint32_t type_id, const uint8_t *row, float *out, size_t cols); /* :213-235 */
 void go_rms_norm(float *out, const float *x, const float *w, size_t n, float eps);  /* :281-291 */
 /* src/engine.zig:670-687: top-k by value, ties to the lower index. */
 void go_topk(const float *values, size_t n, uint32_t *ids, float *weights, size_t k);
+
+/* Row bytes of those types (src/kernels.zig:56-67); 0 for other types or bad widths. */
+size_t go_dense_row_bytes(uint32_t type_id, size_t cols);
 
 /* One MoE layer as src/engine.zig:520-653 computes it. Expert matrices: per expert and
  * projection, a pointer to its packed rows and its type id (144..151), so a layer may mix
@@ -109,12 +113,14 @@ typedef struct go_layer {
     const uint32_t *gate_type, *up_type, *down_type; /* [n_expert] */
     const float *gate_signs;      /* [E] or NULL */
     const float *down_signs;      /* [F] or NULL */
-    /* Shared expert (optional, bf16 weights): SF = 0 disables it. */
+    /* Shared expert (optional): SF = 0 disables it. Rows in the GGML type sh_type: 0 fp32,
+     * 30 bf16, 8 Q8_0 (src/kernels.zig:7-10, rowBytes :56-67). */
     uint32_t SF;
-    const uint16_t *sh_gate, *sh_up; /* [SF][E] bf16 */
-    const uint16_t *sh_down;         /* [E][SF] bf16 */
-    const float *sh_gate_inp;        /* [E] fp32 */
-    float sh_gate_const;             /* used when sh_gate_inp is NULL: gate = this value */
+    const void *sh_gate, *sh_up; /* [SF] rows of E columns */
+    const void *sh_down;         /* [E] rows of SF columns */
+    const float *sh_gate_inp;    /* [E] fp32 */
+    float sh_gate_const;         /* used when sh_gate_inp is NULL: gate = this value */
+    uint32_t sh_type;
 } go_layer;
 
 /* Optional intermediate outputs of go_moe_ffn (any pointer may be NULL). */

@@ -110,7 +110,7 @@ class _GoLayer(C.Structure):
         ("gate_signs", C.c_void_p), ("down_signs", C.c_void_p),
         ("SF", C.c_uint32),
         ("sh_gate", C.c_void_p), ("sh_up", C.c_void_p), ("sh_down", C.c_void_p),
-        ("sh_gate_inp", C.c_void_p), ("sh_gate_const", C.c_float),
+        ("sh_gate_inp", C.c_void_p), ("sh_gate_const", C.c_float), ("sh_type", C.c_uint32),
     ]
 
 
@@ -156,6 +156,7 @@ class OracleLayer:
         s.sh_gate, s.sh_up, s.sh_down = ptr(L.sh_gate), ptr(L.sh_up), ptr(L.sh_down)
         s.sh_gate_inp = ptr(L.sh_gate_inp)
         s.sh_gate_const = 1.0
+        s.sh_type = getattr(L, "sh_type", 30)
         self.struct = s
 
     def forward(self, x: np.ndarray, threads: int | None = None, trace: bool = False):

@@ -70,33 +70,41 @@ class GgufBuilder:
         return bytes(self.b)
 
 
-def write_layer_file(path, L, arch="gyrotest"):
+def write_layer_file(path, L, arch="gyrotest", block_size=128, listed=None):
     """One MoE layer as a GGUF file: blk.0.ffn_gate_inp.weight (fp32 router, dims (E, n_expert)),
     blk.0.ffn_{gate,up,down}_exps.weight (Gyro experts), the expert counts and scale under
     `arch`, and the released rotation metadata with explicit signs for widths E (gate, up) and
-    F (down)."""
+    F (down), listing `listed` (default: the three expert tensors). With a shared expert (L.SF)
+    also blk.0.ffn_{gate,up,down}_shexp.weight in L.sh_type (dims (E, SF), (E, SF), (SF, E))
+    and the fp32 blk.0.ffn_gate_inp_shexp.weight (dims (E,))."""
     import numpy as np
     ty = int(L.types[0, 0])
     names = [f"blk.0.ffn_{p}_exps.weight" for p in ("gate", "up", "down")]
+    listed = names if listed is None else listed
     kv = [("general.alignment", "u32", 32), ("general.architecture", "str", arch),
           (f"{arch}.expert_count", "u32", L.n_expert), (f"{arch}.expert_used_count", "u32", L.n_used),
           (f"{arch}.block_count", "u32", 1),
           ("agention.trellis.state_bits", "u32", 15), ("prism.hadamard.version", "u32", 1),
-          ("prism.hadamard.block_size", "u32", 128),
+          ("prism.hadamard.block_size", "u32", block_size),
           ("prism.hadamard.transform", "str", "normalized-sylvester-walsh-hadamard"),
           ("prism.hadamard.axis", "str", "input-last-dimension"), ("prism.hadamard.sign_mode", "str", "explicit"),
-          ("prism.hadamard.weight_names", "strs", [names[0], names[1], names[2]]),
+          ("prism.hadamard.weight_names", "strs", list(listed)),
           ("prism.hadamard.sign_widths", "i32s", [L.E, L.F]),
           ("prism.hadamard.sign_values", "i32s", list(L.gate_signs.astype(int)) + list(L.down_signs.astype(int)))]
     if L.expert_weights_scale:
         kv.append((f"{arch}.expert_weights_scale", "f32", L.expert_weights_scale))
-    f = GgufBuilder().header(4, len(kv))
-    for key, kind, v in kv:
-        {"u32": f.kv_u32, "str": f.kv_str, "strs": f.kv_strs, "i32s": f.kv_i32s, "f32": f.kv_f32}[kind](key, v)
     blobs = [("blk.0.ffn_gate_inp.weight", (L.E, L.n_expert), 0, np.ascontiguousarray(L.router, np.float32)),
              (names[0], (L.E, L.F, L.n_expert), ty, np.stack(L.gate)),
              (names[1], (L.E, L.F, L.n_expert), ty, np.stack(L.up)),
              (names[2], (L.F, L.E, L.n_expert), ty, np.stack(L.down))]
+    if L.SF:
+        blobs += [("blk.0.ffn_gate_shexp.weight", (L.E, L.SF), L.sh_type, np.ascontiguousarray(L.sh_gate)),
+                  ("blk.0.ffn_up_shexp.weight", (L.E, L.SF), L.sh_type, np.ascontiguousarray(L.sh_up)),
+                  ("blk.0.ffn_down_shexp.weight", (L.SF, L.E), L.sh_type, np.ascontiguousarray(L.sh_down)),
+                  ("blk.0.ffn_gate_inp_shexp.weight", (L.E,), 0, np.ascontiguousarray(L.sh_gate_inp, np.float32))]
+    f = GgufBuilder().header(len(blobs), len(kv))
+    for key, kind, v in kv:
+        {"u32": f.kv_u32, "str": f.kv_str, "strs": f.kv_strs, "i32s": f.kv_i32s, "f32": f.kv_f32}[kind](key, v)
     off, offs = 0, []
     for name, dims, t, arr in blobs:
         f.tensor(name, dims, t, off)

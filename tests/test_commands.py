@@ -53,3 +53,15 @@ def test_expert_bundle(tmp_path):
 
 def test_usage():
     assert commands.main([]) == 2 and commands.main(["gyro"]) == 2
+
+
+def test_type_names_follow_the_type_table():
+    """validateGyro prints info.name of the type table (src/gyro.zig:33-40): id, name, k, steps,
+    block bytes."""
+    from gyrodx import synth
+    from gyrodx.commands import TYPE_NAMES
+    table = {144: ("TQ2_T", 8, 32, 34), 145: ("TQK6", 6, 32, 26), 146: ("TQK7", 7, 32, 30),
+             147: ("TQP5", 5, 64, 42), 148: ("TQP6", 6, 64, 50), 149: ("TQP7", 7, 64, 58),
+             150: ("TQK5", 5, 32, 22), 151: ("TQK4", 4, 32, 18)}
+    assert TYPE_NAMES == {i: v[0] for i, v in table.items()}
+    assert synth.TYPES == {i: v[1:] for i, v in table.items()}

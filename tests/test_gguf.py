@@ -144,3 +144,62 @@ def test_metadata_values():
     assert m.metadata("prism.hadamard.sign_values")[:4] == [1, -1, 1, -1]
     assert m.metadata("prism.hadamard.axis") == "input-last-dimension"
     assert m.has("prism.hadamard.version") and not m.has("nope")
+
+
+def small_layer(**kw):
+    from gyrodx import synth
+    return synth.make_layer(31, E=512, F=256, n_expert=4, n_used=2, **kw)
+
+
+def test_load_layer_refuses_what_the_model_loader_refuses(tmp_path):
+    """src/model.zig:312 (block size 128), :421-429 (only expert projections are listed) and
+    src/gpu_engine.zig:404 (up-projection signs must be the gate's)."""
+    from gguf_fixture import write_layer_file
+    L = small_layer()
+    names = [f"blk.0.ffn_{p}_exps.weight" for p in ("gate", "up", "down")]
+    cases = {"block256": dict(block_size=256), "up_only": dict(listed=[names[1], names[2]]),
+             "router_listed": dict(listed=names + ["blk.0.ffn_gate_inp.weight"])}
+    for what, kw in cases.items():
+        path = tmp_path / f"{what}.gguf"
+        write_layer_file(path, L, **kw)
+        gguf.open_model(str(path)).validate_gyro()  # the rotation metadata itself is valid
+        with pytest.raises(gguf.UnsupportedConfiguration):
+            gguf.load_layer(str(path), 0)
+    # The released layout loads, with the gate's signs shared by up.
+    path = tmp_path / "ok.gguf"
+    write_layer_file(path, L)
+    G = gguf.load_layer(str(path), 0)
+    np.testing.assert_array_equal(G.gate_signs, L.gate_signs)
+    np.testing.assert_array_equal(G.down_signs, L.down_signs)
+    assert G.SF == 0
+
+
+@pytest.mark.parametrize("sh_type", [8, 30, 0])
+def test_load_layer_reads_the_shared_expert(tmp_path, sh_type):
+    """blk.<l>.ffn_{gate,up,down}_shexp.weight and ffn_gate_inp_shexp.weight (src/model.zig:413-416)
+    round-trip in Q8_0, bf16 and fp32."""
+    from gguf_fixture import write_layer_file
+    L = small_layer(SF=64, sh_type=sh_type)
+    path = tmp_path / "shared.gguf"
+    write_layer_file(path, L)
+    G = gguf.load_layer(str(path), 0)
+    assert (G.SF, G.sh_type) == (64, sh_type)
+    for name in ("sh_gate", "sh_up", "sh_down"):
+        np.testing.assert_array_equal(G.__dict__[name].view(np.uint8).ravel(),
+                                      np.ascontiguousarray(getattr(L, name)).view(np.uint8).ravel())
+    np.testing.assert_array_equal(G.sh_gate_inp, L.sh_gate_inp)
+
+
+def test_validate_gyro_compares_widths_as_u64():
+    """src/gguf.zig:237 compares a listed tensor's first dimension with the sign widths as u64:
+    a dimension of 2^32 + 128 (kept with an unknown tensor type, so no byte range) is not width
+    128. A Gyro tensor in the file makes the rotation metadata apply."""
+    def build(dim0):
+        kv = gyro_meta(None, ["w"], [128], [1, -1] * 64)
+        f = GgufBuilder().header(2, len(kv))
+        for k, (kd, v) in kv.items():
+            {"u32": f.kv_u32, "str": f.kv_str, "strs": f.kv_strs, "i32s": f.kv_i32s, "bool": f.kv_bool}[kd](k, v)
+        f.tensor("g", (128, 4), 144, 0).tensor("w", (dim0, 1), 999, 160).pad()
+        return gguf.parse(f.bytes(), len(f.bytes()) + 4 * 34 + 64)
+    build(128).validate_gyro()
+    assert kind(lambda: build(2 ** 32 + 128).validate_gyro()) == "InvalidMetadata"

@@ -17,7 +17,7 @@ def test_gyro_command(capsys):
     assert [r["type_id"] for r in recs] == list(range(144, 152))
     assert all(r["validation_passed"] and r["max_absolute_error"] == 0.0 and r["values"] == 8192 for r in recs)
     assert commands.main(["gyro", str(KERNEL_DIR / "gyro_decode.co")]) == 0
-    assert '"type_name": "GYRO_K4_S32"' in capsys.readouterr().out
+    assert '"type_name": "TQK4"' in capsys.readouterr().out
 
 
 def test_stream_command(tmp_path, capsys):

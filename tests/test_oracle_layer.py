@@ -174,20 +174,34 @@ def bf16_to_f64(bits):
     return (np.asarray(bits, np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def test_shared_expert_matches_numpy(oracle_mod):
-    """The bf16 shared expert (src/engine.zig:644-653, dotHalf of src/kernels.zig:86-105): the
-    difference the shared expert makes to the oracle's output equals an fp64 numpy model of
-    sigmoid(g . x) * W_d (silu(W_g x) * W_u x) on the unrotated input."""
-    L = synth.make_layer(71, E=256, F=128, n_expert=16, n_used=4, SF=64)
+def shared_f64(L, which):
+    """fp64 weights of a shared matrix in its GGML type: bf16 bits, Q8_0 rows (oracle decode,
+    pinned on the reference's known answer in test_q8.py) or fp32 row bytes."""
+    m = getattr(L, which)
+    cols = L.SF if which == "sh_down" else L.E
+    if L.sh_type == 30:
+        return bf16_to_f64(m)
+    if L.sh_type == 8:
+        import oracle
+        return oracle.q8_0_decode_rows(m, m.shape[0], cols).astype(np.float64)
+    return np.ascontiguousarray(m).view(np.float32).reshape(m.shape[0], cols).astype(np.float64)
+
+
+@pytest.mark.parametrize("sh_type", [30, 8, 0])
+def test_shared_expert_matches_numpy(oracle_mod, sh_type):
+    """The shared expert (src/engine.zig:644-653; dotRow of src/kernels.zig:201-210 for bf16,
+    Q8_0 and fp32 rows): the difference it makes to the oracle's output equals an fp64 numpy model
+    of sigmoid(g . x) * W_d (silu(W_g x) * W_u x) on the unrotated input."""
+    L = synth.make_layer(71, E=256, F=128, n_expert=16, n_used=4, SF=64, sh_type=sh_type)
     x = synth.make_tokens(72, 5, L.E)
     with_sh = oracle_mod.OracleLayer(L).forward(x, threads=2)
     L0 = synth.make_layer(71, E=256, F=128, n_expert=16, n_used=4)
     without = oracle_mod.OracleLayer(L0).forward(x, threads=2)
     x64 = x.astype(np.float64)
-    g = x64 @ bf16_to_f64(L.sh_gate).T
-    u = x64 @ bf16_to_f64(L.sh_up).T
+    g = x64 @ shared_f64(L, "sh_gate").T
+    u = x64 @ shared_f64(L, "sh_up").T
     a = g / (1 + np.exp(-g)) * u
-    sh = a @ bf16_to_f64(L.sh_down).T
+    sh = a @ shared_f64(L, "sh_down").T
     gate = 1 / (1 + np.exp(-(x64 @ L.sh_gate_inp.astype(np.float64))))
     ref = gate[:, None] * sh
     got = with_sh.astype(np.float64) - without.astype(np.float64)

@@ -22,6 +22,18 @@ def test_reference_known_answer():
     x = (np.arange(64) % 7 - 3.0).astype(np.float32)
     expected = sum(0.5 * (j - 16) * x[j] for j in range(32)) + sum(-0.25 * (j - 15) * x[32 + j] for j in range(32))
     assert abs(float(w.astype(np.float64) @ x) - expected) < 1e-4
+    # The C oracle's dotRow of type Q8_0 (dotQ8, src/kernels.zig:107-120) gives the same answer.
+    import ctypes as C
+    row = reference_row()
+    got = oracle.lib().go_dot_row(8, row.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                  x.ctypes.data_as(C.POINTER(C.c_float)), 64)
+    assert abs(got - expected) < 1e-4
+    # A planted mistake (the second block's scale taken as +0.25) misses it.
+    bad = row.copy()
+    bad[34:36] = np.array([0.25], np.float16).view(np.uint8)
+    got_bad = oracle.lib().go_dot_row(8, bad.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                      x.ctypes.data_as(C.POINTER(C.c_float)), 64)
+    assert abs(got_bad - expected) > 1.0
 
 
 def test_every_quant_and_special_scales():

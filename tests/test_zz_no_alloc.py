@@ -2,7 +2,8 @@
 decode path, through the C ABI: outputs equal bit for bit on two calls in a row, the second
 with fewer tokens, on a uniform TQ2_T layer (moe_decode_gu / moe_decode_down) and on a mixed-type
 layer with a shared expert (moe_decode_gu_x / moe_decode_down_x, the shared rows in the scratch
-array). Inputs and outputs are torch device tensors; the first call is queued on the engine's
+array) and at hidden 2560 / F 640 / top-10 with a Q8_0 shared expert (mv_q8 and ew ahead of the
+routed kernels, every intermediate in the scratch array). Inputs and outputs are torch device tensors; the first call is queued on the engine's
 compute stream, the second on a torch stream.
 """
 import numpy as np
@@ -18,10 +19,12 @@ pytestmark = pytest.mark.gpu
 def _layer(kind):
     if kind == "tq2":
         return synth.make_layer(7, E=2048, F=512, n_expert=256, n_used=8)
+    if kind == "coder_q8_shared":  # the shared expert in the mv kernels, its buffers in the scratch array
+        return synth.make_layer(9, E=2560, F=640, n_expert=64, n_used=10, SF=640, sh_type=8)
     return synth.make_layer(8, E=2048, F=512, n_expert=64, n_used=8, mixed_types=True, SF=512)
 
 
-@pytest.mark.parametrize("kind", ["tq2", "mixed_shared"])
+@pytest.mark.parametrize("kind", ["tq2", "mixed_shared", "coder_q8_shared"])
 def test_noalloc_matches_forward(kind):
     layer = _layer(kind)
     eng = Engine(max_tok=8)
