@@ -45,6 +45,7 @@ def lib() -> C.CDLL:
         L.gm_last_routes.argtypes = [vp, u32, C.POINTER(u32), f32p]
         L.gm_last_sort.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(u32)]
         L.gm_dequant.argtypes = [vp, u32, u32, u32, u32, u32, f32p]
+        L.gm_dequant_as.argtypes = [vp, u32, u32, u32, u32, u32, u32, f32p]
         L.gm_set_tokens.argtypes = [vp, f32p, u32]
         L.gm_run.argtypes = [vp, u32, u32, u32, u32, C.POINTER(u32), u32, C.POINTER(C.c_double),
                              C.POINTER(C.c_double)]
@@ -142,9 +143,12 @@ class Engine:
         self._check(lib().gm_last_sort(self._h, n, p(order), p(start)), "gm_last_sort")
         return order, start
 
-    def dequant(self, layer: int, expert: int, proj: int, row0: int, rows: int, cols: int) -> np.ndarray:
+    def dequant(self, layer: int, expert: int, proj: int, row0: int, rows: int, cols: int,
+                decoder: int = 0) -> np.ndarray:
+        """Rows of one expert projection through a path's device decoder: 0 the decode kernels',
+        1 the prefill GEMMs' (fp32 scale x codebook), 2 the prefill B operand (binary16)."""
         out = np.empty((rows, cols), np.float32)
-        self._check(lib().gm_dequant(self._h, layer, expert, proj, row0, rows, _f32p(out)), "gm_dequant")
+        self._check(lib().gm_dequant_as(self._h, layer, expert, proj, row0, rows, decoder, _f32p(out)), "gm_dequant_as")
         return out
 
     def set_tokens(self, x: np.ndarray):

@@ -1144,24 +1144,29 @@ extern "C" int gm_last_tiles(gm_engine *g, uint32_t max_tiles, uint32_t *tiles, 
     });
 }
 
-extern "C" int gm_dequant(gm_engine *g, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
-                          uint32_t rows, float *out) {
+extern "C" int gm_dequant_as(gm_engine *g, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
+                             uint32_t rows, uint32_t decoder, float *out) {
     if (!out) return -1;
     return guarded(g, [&] {
         Engine &e = g->e;
         const gyro::Layer &L = e.layers.at(layer);
-        if (L.type_id != 144) throw gyro::NativeError(-1, "dequant check covers TQ2_T layers");
         const uint32_t cols = proj == 2 ? e.F : e.E, total_rows = proj == 2 ? e.E : e.F;
-        if (expert >= e.NE || proj > 2 || row0 + rows > total_rows) throw gyro::NativeError(-1, "range");
+        if (expert >= e.NE || proj > 2 || decoder > GM_DEQUANT_PREFILL_B16 || !rows || row0 + rows > total_rows)
+            throw gyro::NativeError(-1, "range");
         gyro::Buffer o = e.dev.buffer((uint64_t)rows * cols * 4, gyro::Kind::device);
-        const uint32_t units = rows * (cols / 128);
+        const uint32_t units = rows * (cols / 128) * (decoder ? 2u : 1u);
         e.dev.begin();
-        e.dispatch("moe_dequant", {L.xtab.srv, expert, proj, row0, rows, cols, e.codebook.srv, o.uav, 0},
+        e.dispatch("moe_dequant", {L.xtab.srv, expert, proj, row0, rows, cols, e.codebook.srv, o.uav, 0, decoder},
                    (units + 255) / 256);
         e.dev.wait(e.dev.submit());
         gyro::check(gd_readback(e.dev.ctx, o.handle, 0, rows * cols * 4, out, gyro::kTimeoutMs), "gd_readback");
         e.dev.release(o);
     });
+}
+
+extern "C" int gm_dequant(gm_engine *g, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
+                          uint32_t rows, float *out) {
+    return gm_dequant_as(g, layer, expert, proj, row0, rows, GM_DEQUANT_DECODE, out);
 }
 
 extern "C" int gm_set_tokens(gm_engine *g, const float *x, uint32_t n_total) {

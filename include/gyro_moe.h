@@ -90,10 +90,17 @@ GM_API int gm_last_sort(gm_engine *e, uint32_t n, uint32_t *order, uint32_t *ord
 /* Reads the tile list of the last prefill-path call: count (out) tiles of 4 words each
  * {expert, first sorted row, rows, 0}, at most max_tiles of them. */
 GM_API int gm_last_tiles(gm_engine *e, uint32_t max_tiles, uint32_t *tiles, uint32_t *count);
-/* Decodes rows [row0, row0 + rows) of one expert projection to fp32 with the fast path's
- * device decoder (bit-exact check of the in-kernel dequantisation). */
+/* Decodes rows [row0, row0 + rows) of one expert projection (any Gyro type) to fp32 with the
+ * decode path's block decoders (bit-exact check of the in-kernel dequantisation). */
 GM_API int gm_dequant(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
                       uint32_t rows, float *out);
+/* As gm_dequant with the decoder of one path: GM_DEQUANT_DECODE (the decode kernels'),
+ * GM_DEQUANT_PREFILL (the prefill GEMMs' B-operand decoders, both lane halves; fp32 scale x
+ * codebook value) or GM_DEQUANT_PREFILL_B16 (the B operand as the MFMA reads it: the binary16
+ * product of scale and codebook value, widened to fp32). */
+enum { GM_DEQUANT_DECODE = 0, GM_DEQUANT_PREFILL = 1, GM_DEQUANT_PREFILL_B16 = 2 };
+GM_API int gm_dequant_as(gm_engine *e, uint32_t layer, uint32_t expert, uint32_t proj, uint32_t row0,
+                         uint32_t rows, uint32_t decoder, float *out);
 
 /* Benchmark harness: tokens[n_total][E] are uploaded once; gm_run then processes `calls` calls
  * of `batch` tokens starting at token `first`, call i using layer layers[i % n_layers], with

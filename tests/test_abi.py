@@ -24,7 +24,7 @@ def exported(lib):
 
 @pytest.mark.parametrize("lib,header,prefix,count", [
     ("libgyro_native.so", "gyro_native.h", "gd_", 29),
-    ("libgyro_moe.so", "gyro_moe.h", "gm_", 16),
+    ("libgyro_moe.so", "gyro_moe.h", "gm_", 17),
     ("libgyro_moe.so", "gyro_gguf.h", "gg_", 14),
 ])
 def test_exports(lib, header, prefix, count):
