@@ -57,6 +57,10 @@ PROJ_BYTES = F * (E // 128) * 34  # 278,528 packed bytes per expert projection
 EXPERT_BYTES_PER_TOKEN = TOP_K * 3 * PROJ_BYTES  # 6,684,672
 GU_BYTES_PER_LAUNCH = TOP_K * 2 * PROJ_BYTES  # 4,456,448
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
+GEMM_COUNTERS_FILE = ROOT / "profiles" / "moe_prefill_gemm_counters.md"
+# How the synthetic expert blocks are drawn (gyrodx.synth.random_blocks): trellis stream bytes
+# uniform; block scales binary16 with a random sign, exponent field 7..11 and a uniform mantissa.
+BLOCK_SCALES = "binary16, random sign, exponent field 7..11 (|scale| in [2^-8, 2^-3)), uniform mantissa"
 PREFILL_TOKENS = 1024
 # Routed-expert FLOPs of one prefill call: tokens x top-8 x (gate, up, down) x 2 x E x F.
 PREFILL_GU_FLOPS = PREFILL_TOKENS * TOP_K * 2 * 2 * E * F       # 34,359,738,368
@@ -73,6 +77,16 @@ def read_traffic():
         return None
     m = re.search(r"^bytes_per_launch:\s*(\d+)", TRAFFIC_FILE.read_text(), re.M)
     return int(m.group(1)) if m else None
+
+
+def read_gemm_counters():
+    """MFMA-busy and useful fractions of the prefill GEMMs from the committed counter summary
+    (its `mfma_busy_<kernel>:` and `mfma_useful_<kernel>:` lines), or None when absent."""
+    if not GEMM_COUNTERS_FILE.exists():
+        return None
+    text = GEMM_COUNTERS_FILE.read_text()
+    got = {k: float(v) for k, v in re.findall(r"^(mfma_(?:busy|useful)_moe_prefill_\w+):\s*([0-9.]+)", text, re.M)}
+    return {"source": str(GEMM_COUNTERS_FILE.relative_to(ROOT)), **got} if got else None
 
 
 def copy_calibration(reps: int) -> None:
@@ -177,6 +191,13 @@ def prefill_bench(eng, layer, args):
         "grouped_gemm_tflops": round(PREFILL_FLOPS / gemm_s / 1e12, 1),
         "grouped_gemm_frac_of_peak": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "distinct_experts": distinct, "expert_bytes": distinct * BUNDLE_BYTES,
+        "block_scales": BLOCK_SCALES,
+        # The grouped GEMMs' roofline: routed-expert FLOPs over the two GEMMs' dispatch times
+        # (measured above); the counter pass's MFMA-busy and useful-work fractions beside it.
+        "roofline": {"bound": "mfma", "kernel": "moe_prefill_gu + moe_prefill_down",
+                     "achieved": round(PREFILL_FLOPS / gemm_s / 1e12, 1), "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "counters": read_gemm_counters()},
     }
     return res, x[:PREFILL_TOKENS], out0, zl
 
@@ -514,7 +535,7 @@ def main() -> int:
         "data": "synthetic (seeded TQ2_T bytes, N(0,0.02) router, N(0,1) tokens)",
         "config": {"workload": "single MoE layer, batch-1 decode", "hidden": E, "experts": N_EXPERT,
                    "top_k": TOP_K, "ffn": F, "expert_type": "TQ2_T (GGUF 144)", "tokens": args.steps,
-                   "layer_copies": args.copies, "parallelism": "none (1 GPU)"},
+                   "layer_copies": args.copies, "block_scales": BLOCK_SCALES, "parallelism": "none (1 GPU)"},
         "device_ms_per_step": round(dev_ms / args.steps, 5),
         "expert_hbm_gbs": round(EXPERT_BYTES_PER_TOKEN / (wall_ms / args.steps * 1e-3) / 1e9, 1),
         "kernel_us": {"moe_router": round(router_us, 3), "moe_decode_gu": round(gu_us, 3),
