@@ -12,6 +12,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <map>
@@ -207,9 +208,11 @@ constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
 void *scratch_ptr[kMaxDevices] = {};
 
-void *scratch_address(uint32_t device) {
+// `first` is set for the first lookup on a device (the caller clears what must start at zero).
+void *scratch_address(uint32_t device, bool &first) {
     if (device >= (uint32_t)kMaxDevices) throw NativeError(-1, "device ordinal out of range for the scratch table");
     std::lock_guard<std::mutex> lock(scratch_mutex);
+    first = !scratch_ptr[device];
     if (!scratch_ptr[device]) {
         hipError_t rc = hipSetDevice((int)device);
         if (rc != hipSuccess) throw NativeError(-1, std::string("hipSetDevice: ") + hipGetErrorString(rc));
@@ -227,8 +230,27 @@ void *scratch_address(uint32_t device) {
 // an offset); the per-call buffers follow from kNoallocBase.
 constexpr uint64_t kNoallocShH = 0, kNoallocShHBytes = 64u << 10;
 constexpr uint64_t kNoallocShG = kNoallocShHBytes, kNoallocShGBytes = 256;
-constexpr uint64_t kNoallocBase = 128u << 10;
-static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocBase, "scratch regions overlap");
+
+// Exchange area of moe_decode_fused, in words. One layout for every layer shape, so an area that
+// engines of different shapes share (the scratch array) never holds data where a later call
+// expects a counter; counters are zero between calls and every tagged word is rewritten by each
+// call that polls it.
+namespace xch {
+constexpr uint32_t kCtl = 0;                          // EP, error tag (+ 32), sticky error word (+ 64)
+constexpr uint32_t kMaxGroups = 512, kMaxSlots = 16, kMaxActBlocks = 128;
+constexpr uint32_t kLog = 128;                        // logit and arrival words, one per 128-byte line
+constexpr uint32_t kRoute = kLog + 32 * kMaxGroups;   // 2 x 16 route words (64-bit)
+constexpr uint32_t kCnt = kRoute + 128;               // slot counters, 32 words apart
+constexpr uint32_t kFlag = kCnt + 32 * kMaxSlots;     // slot flags, 32 words apart
+constexpr uint32_t kAct = kFlag + 32 * kMaxSlots;     // [16][1024] SwiGLU outputs
+constexpr uint32_t kWords = kAct + kMaxSlots * 1024;
+constexpr uint32_t kSpinLimit = 1u << 16;             // polls (about 64 ms) before a wait gives up
+}  // namespace xch
+
+constexpr uint64_t kNoallocXch = 128u << 10, kNoallocXchBytes = 160u << 10;
+constexpr uint64_t kNoallocBase = kNoallocXch + kNoallocXchBytes;
+static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocXch, "scratch regions overlap");
+static_assert(xch::kWords * 4ull <= kNoallocXchBytes, "exchange area exceeds its scratch region");
 
 }  // namespace
 
@@ -244,6 +266,12 @@ struct DecodeBufs {
     uint32_t logits, logits_off, ids, ids_off, weights, weights_off, xh, xh_off, gu, gu_off;
     uint32_t sh_h, sh_g;  // the fused shared expert's rows and gate dots (offset 0)
     SharedBufs shared;    // the shared expert outside the fused kernels
+    uint32_t xch;         // moe_decode_fused's exchange area (offset 0)
+};
+
+// Work split of moe_decode_fused: G groups, FB rows per gate/up unit, RB rows per down unit.
+struct FusedSplit {
+    uint32_t G = 0, FB = 0, RB = 0;
 };
 
 // Residual stream of a stack step: the layer input is normalised by the layer's RMSNorm inside
@@ -261,6 +289,16 @@ class Engine {
     bool direct = false;
     void *direct_stream = nullptr;
     Buffer na_base, na_shh, na_shg, na_x, na_out;  // table entries into `scratch` and for the caller's x, out
+    Buffer na_xch;                                 // the scratch array's moe_decode_fused exchange area
+    // Single-launch decode (moe_decode_fused): its exchange area, the group count (compute units),
+    // the mode (environment GYRO_DECODE_FUSED: 1 takes batch-1 calls on it where it fits, 2 makes
+    // a batch-1 decode call that it cannot take an error; otherwise 0, the three-kernel path, which
+    // is faster on MI355X) and the polls a wait makes before it gives up (GYRO_DECODE_SPIN_LIMIT,
+    // default 65536).
+    Buffer xch_area;
+    uint32_t cus = 0;
+    uint32_t fused_mode = 0;
+    uint32_t spin_limit = xch::kSpinLimit;
     std::string error;
     uint32_t max_tok = 0;
     uint32_t E = 0, F = 0, NE = 0, U = 0;
@@ -386,18 +424,30 @@ class Engine {
         fill_zero(range_flag);
         // Table entries of the no-allocation entry point: into this GPU's scratch array, and two
         // whose addresses each call sets (the caller's input and output).
-        uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter));
+        bool first_use = false;
+        uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter, first_use));
         na_base = dev.wrap(sp, GM_NOALLOC_SCRATCH_BYTES);
         na_shh = dev.wrap(sp + kNoallocShH, kNoallocShHBytes);
         na_shg = dev.wrap(sp + kNoallocShG, kNoallocShGBytes);
+        na_xch = dev.wrap(sp + kNoallocXch, kNoallocXchBytes);
         na_x = dev.wrap(nullptr, 0);
         na_out = dev.wrap(nullptr, 0);
+        if (first_use) fill_zero(na_xch);
+        // The single-launch decode kernel: one group per compute unit, its exchange area zeroed.
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, (int)adapter) != hipSuccess) cu = 0;
+        cus = (uint32_t)std::max(cu, 0);
+        const char *fe = std::getenv("GYRO_DECODE_FUSED");
+        fused_mode = fe && fe[0] == '1' ? 1u : fe && fe[0] == '2' ? 2u : 0u;
+        if (const char *sl = std::getenv("GYRO_DECODE_SPIN_LIMIT")) spin_limit = (uint32_t)std::strtoul(sl, nullptr, 10);
+        xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
+        fill_zero(xch_area);
     }
 
     // The decode path's own intermediate buffers.
     DecodeBufs engine_bufs() const {
         return {router_out.uav, 0, ids.uav, 0, weights.uav, 0, xh.uav, 0, gu_part.uav, 0, sh_h.uav, sh_g.uav,
-                engine_shared()};
+                engine_shared(), xch_area.uav};
     }
 
     void allocate_activations() {
@@ -744,7 +794,57 @@ class Engine {
     // Layers other than uniform TQ2_T (or with the fused shared expert) take the type-generic kernels.
     bool decode_generic_types(const Layer &L) const { return L.type_id != 144 || decode_fused_shared(L); }
 
-    // MI355X decode path: router + rotation, routed gate/up, down + combine.
+    // moe_decode_fused takes batch-1 calls of uniform TQ2_T layers without a shared expert when
+    // every group's gate/up units (FB rows of one slot) and down units (RB rows of every slot)
+    // fit its per-thread items: at most 4 units of each kind per group, 2 FB E / 128 items per
+    // gate/up unit and 2 U RB F / 128 per down unit, 2048 items, 512 output rows and 2048
+    // (row, slot) sums per group, and U F / 128 rotated down-input blocks in LDS.
+    FusedSplit fused_split(const Layer &L, uint32_t n) const {
+        FusedSplit fs;
+        if (!fused_mode || n != 1 || L.type_id != 144 || L.SF || E % 256 || E > 4096 || F % 128 || F > 1024 || U < 1 ||
+            U > xch::kMaxSlots || NE > xch::kMaxGroups || U * (F / 128) > xch::kMaxActBlocks)
+            return fs;
+        const uint32_t G = std::min(cus, xch::kMaxGroups), nb = E / 128, nbF = F / 128;
+        if (G == 0) return fs;
+        auto per_group = [G](uint32_t units) { return (units + G - 1) / G; };
+        // Down units: the smallest row count that divides E with at most one unit per group.
+        uint32_t RB = (E + G - 1) / G;
+        while (E % RB) ++RB;
+        const uint32_t nd = per_group(E / RB);
+        if (nd > 4 || nd * U * RB * 2 * nbF > 2048 || nd * RB > 512 || nd * RB * U > 2048) return fs;
+        for (uint32_t FB : {16u, 8u}) {
+            const uint32_t ng = per_group(U * (F / FB));
+            if (ng > 4 || ng * 2 * FB * nb > 2048) continue;
+            fs.G = G;
+            fs.FB = FB;
+            fs.RB = RB;
+            return fs;
+        }
+        return fs;
+    }
+
+    // Keeps batch-1 decode on the three-kernel path for its lifetime (a recomputation).
+    struct UnfusedScope {
+        Engine *e;
+        uint32_t was;
+        explicit UnfusedScope(Engine *eng) : e(eng), was(eng->fused_mode) { e->fused_mode = 0; }
+        ~UnfusedScope() { e->fused_mode = was; }
+    };
+
+    // Reads and clears the sticky error word of the exchange area: set when a moe_decode_fused
+    // group gave up a wait (its groups were not all running within the spin limit).
+    bool take_fused_error(const Buffer &area) {
+        uint32_t w = 0;
+        check(gd_readback(dev.ctx, area.handle, (xch::kCtl + 64) * 4, 4, &w, kTimeoutMs), "gd_readback");
+        if (!w) return false;
+        const uint32_t zero = 0;
+        upload(area, (xch::kCtl + 64) * 4, &zero, 4);
+        return true;
+    }
+
+    // MI355X decode path: router + rotation, routed gate/up, down + combine; at batch 1, when the
+    // engine was created with GYRO_DECODE_FUSED=1 or 2 and fused_split allows, one launch of
+    // moe_decode_fused instead.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {},
                     const DecodeBufs *bufs = nullptr) {
@@ -754,6 +854,22 @@ class Engine {
             throw NativeError(-1, "decode path needs <= 256 experts, n <= 8, E a multiple of 256 up to 4096, F a "
                                   "multiple of 128 up to 1024 and top-1..16 (or, for other than uniform TQ2_T "
                                   "experts, E a multiple of 1024 with F 512 and top-8)");
+        const FusedSplit fs = fused_split(L, n);
+        if (!fs.G && n == 1 && fused_mode == 2)
+            throw NativeError(-1, "GYRO_DECODE_FUSED=2: this batch-1 decode call cannot take moe_decode_fused");
+        if (fs.G) {
+            const uint32_t norm = st.on ? (L.has_norm ? 2u : 1u) : 0u;
+            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_fused",
+                                 {x_uav, x_off, L.router.srv, L.has_bias ? L.bias.srv : kNone, L.signs.srv,
+                                  (L.has_gate_signs ? 1u : 0u) | (L.has_down_signs ? 2u : 0u), B.xch, xch::kLog,
+                                  xch::kRoute, xch::kAct, xch::kCnt, xch::kFlag, out_uav, out_off,
+                                  (uint32_t)L.base, (uint32_t)(L.base >> 32), slot_stride, L.gate_bytes, codebook.srv, E,
+                                  F, NE, U, bits(L.scale), xch::kCtl, B.ids, B.ids_off, B.weights, B.weights_off,
+                                  st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, flag_uav(), spin_limit,
+                                  norm, fs.FB, fs.RB, L.has_norm ? L.norm.srv : 0u, bits(L.norm_eps)},
+                                 fs.G);
+            return;
+        }
         const bool fused_sh = decode_fused_shared(L);
         if (L.SF && !fused_sh) {
             // The shared expert first; its gated output (plus a stack's stream) is the residual
@@ -962,6 +1078,13 @@ class Engine {
         dev.begin();
         stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
         dev.wait(dev.submit());
+        if (path == GM_PATH_DECODE && take_fused_error(xch_area)) {
+            UnfusedScope unfused{this};
+            upload(x_in, 0, x, (uint64_t)n * E * 4);
+            dev.begin();
+            stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
+            dev.wait(dev.submit());
+        }
         if (fast_path(path) && take_range_flag()) {
             upload(x_in, 0, x, (uint64_t)n * E * 4);
             dev.begin();
@@ -1010,6 +1133,7 @@ class Engine {
         B.sh_h = na_shh.uav;
         B.sh_g = na_shg.uav;
         B.shared = {};
+        B.xch = na_xch.uav;
         if (L.SF && !decode_fused_shared(L)) {
             SharedBufs &S = B.shared;
             S.h = S.a = S.o = S.g = S.s = na_base.uav;
@@ -1043,6 +1167,12 @@ class Engine {
         dev.begin();
         ffn(path, il, n, x_in.uav, 0, out.uav, 0);
         dev.wait(dev.submit());
+        if (path == GM_PATH_DECODE && take_fused_error(xch_area)) {
+            UnfusedScope unfused{this};
+            dev.begin();
+            ffn(path, il, n, x_in.uav, 0, out.uav, 0);
+            dev.wait(dev.submit());
+        }
         if (fast_path(path) && take_range_flag()) {
             dev.begin();
             ffn(GM_PATH_GENERIC, il, n, x_in.uav, 0, out.uav, 0);
@@ -1217,6 +1347,9 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
         if (bracket_us) *bracket_us = br_n ? br / (double)br_n : 0.0;
+        if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
+            throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
+                                        "this run are invalid (gm_forward recomputes such calls on the three-kernel path)");
         if (Engine::fast_path(path) && e.take_range_flag())
             throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
                                         "are invalid (gm_forward recomputes such calls on GM_PATH_GENERIC)");
@@ -1256,6 +1389,9 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         }
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
+        if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
+            throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
+                                        "this run are invalid (gm_forward_stack recomputes such calls on the three-kernel path)");
         if (Engine::fast_path(path) && e.take_range_flag())
             throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
                                         "are invalid (gm_forward_stack recomputes such calls on GM_PATH_GENERIC)");
