@@ -137,6 +137,13 @@ __device__ __forceinline__ float tq2_block_dot_h(const uint32_t q[8], const uint
     return acc0 + acc1;
 }
 
+// The 9 words from the 4-byte-aligned start of the 34-byte block at byte `off` (even) of `base`.
+__device__ __forceinline__ void tq2_load_block(const uint8_t *base, uint64_t off, uint32_t d[9]) {
+    gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(base + (off & ~uint64_t(3))));
+#pragma unroll
+    for (int j = 0; j < 9; ++j) d[j] = w[j];
+}
+
 // Extracts the scale and the 8 aligned stream words of a 34-byte block that starts at byte
 // offset `off` (even) inside the 32-bit words d[] (d[0] holds bytes off & ~3 ..).
 // Blocks at offsets 0 mod 4 have their stream at 2 mod 4, and vice versa.

@@ -1,88 +1,119 @@
 // Decode path, step 3, for the shapes moe_decode_down does not take (F other than 512, top-U
-// other than 8, more than two K-parts): SwiGLU and the down-input rotation, the fused TQ2_T
-// dequant-GEMV of the down rows and the route-weighted combine (src/engine.zig:603-641).
+// other than 8, hidden not a multiple of 1024): the down-input rotation, the fused TQ2_T
+// dequant-GEMV of the down rows and the route-weighted combine (src/engine.zig:607-641).
 //
-// A group owns 8 output rows of one token for all U selected experts, so the combine stays
-// local and runs in k order.
-// (1) Down inputs: unit (k, bb) of 16 lanes forms block bb of expert k's input
-//     a = H_128(s_down * silu(g) * u), 8 consecutive values per lane (the gate/up partials of the
-//     K-parts added in part order), with the 16-lane butterfly of moe_decode_down, into LDS.
-// (2) Down rows: the 8 rows of each expert are one contiguous run of 8 F / 128 blocks
-//     (272 F / 128 bytes, 4-byte aligned), copied to LDS in 16-byte chunks by all threads.
-// (3) Wave w computes output row w: unit (k, bb, hf) decodes half hf (16 trellis steps) of
-//     block bb against block bb of a_k; the unit sums go through LDS, lane k < U adds expert
-//     k's 2 F / 128 units in (bb, hf) order, and the experts are combined in k order (times the
-//     route weights) before the residual is added.
-// Grid: x = E / 8, y = n_tok; 512 threads.
-// Constants (as moe_decode_down): 0 gu_uav 1 gu_off 2 ids_uav 3 ids_off 4 weights_uav
-// 5 weights_off 6 base_lo 7 base_hi 8 slot_stride 9 down_off 10 codebook_srv 11 signs_srv
-// (0xffffffff: none) 12 signs_off 13 out_uav 14 out_off 15 E 16 F 17 n_used 18 n_tok 19 parts
-// 20 n_expert 21 residual 22 res_uav 23 res_off.
-// Requires TQ2_T experts, F a multiple of 128 up to 1024, 1 <= n_used <= 16, parts <= 8.
+// A group owns R consecutive output rows of one token for all U selected experts, so the
+// combine stays local and runs in slot order; the host picks R so that a token spans about one
+// group per CU.
+//  - Item (slot k, block bb, half hf, row pair): each thread loads the expert id of its item,
+//    its inputs' values (below), then block bb of both rows straight from HBM (9 words each),
+//    so the weight loads are in flight while the inputs are rotated.
+//  - Input unit (k, bb) of 16 lanes: block bb of a_k = H_128(s_down * act_k) / sqrt(128) (the
+//    16-lane butterfly of moe_decode_down), 8 consecutive values per lane, into LDS.
+//  - Item dots: the thread reads its 64 fp32 activations (half hf of block bb of a_k) from LDS
+//    once and decodes that half of both rows' blocks against them (tq2_half_dot); per (row, k)
+//    the half sums in (block, half) order times w_k, then per row the slots in slot order, then
+//    the residual (every LDS sum reads its operands at once).
+// Grid: x = E / R, y = n_tok; 512 threads.
+// Constants: 0 act_uav 1 act_off (act[(t U + k) F + f], from moe_decode_gu_g) 2 ids_uav 3 ids_off
+// 4 weights_uav 5 weights_off 6 base_lo 7 base_hi 8 slot_stride 9 down_off 10 codebook_srv
+// 11 signs_srv (0xffffffff: none) 12 signs_off 13 out_uav 14 out_off 15 E 16 F 17 n_used
+// 18 n_tok 19 R 20 n_expert 21 residual 22 res_uav 23 res_off.
+// Requires TQ2_T experts, F a multiple of 128 up to 1024, 1 <= n_used <= 16, n_used F / 128 <=
+// DG_MAX_ABLK, n_used F / 64 ceil(R / 2) <= 512 DG_ITEMS and R n_used <= 512 (the host checks).
 #include "gyro_fast.h"
 #include "fwht.h"
 
-#define DG_ROWS 8
+#ifndef DG_MAX_ABLK
+#define DG_MAX_ABLK 64  // rotated input blocks (slots x F / 128) in LDS
+#define DG_PIPELINE moe_decode_down_g
+#endif
+#define DG_ITEMS 2  // (slot, block, half, row pair) items per thread
 #define DG_MAX_U 16
-#define DG_MAX_NB 8                          // F <= 1024
-#define DG_BLOCK_STRIDE 132                  // floats per 128-block in LDS (bank spread)
-#define DG_MAX_UNITS (DG_MAX_U * DG_MAX_NB * 2)
+#define DG_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
+#define DG_BLOCK_STRIDE 132  // floats per 128-block of an input in LDS (bank spread)
 
-GD_PIPELINE_NAMED(moe_decode_down_g, 512) {
-    __shared__ uint4 book4[512];
-    __shared__ float act[DG_MAX_U * DG_MAX_NB * DG_BLOCK_STRIDE];
-    __shared__ gd_u32x4 rows[DG_MAX_U * DG_ROWS * DG_MAX_NB * 34 / 16 + 1];  // + 1: the last block's 9th word
+DG_DEFINE(DG_PIPELINE, 512) {
+    __shared__ gd_u32x4 book4[512];
+    __shared__ float actr[DG_MAX_ABLK * DG_BLOCK_STRIDE];
+    __shared__ float dred[2 * DG_ITEMS * 512];  // half dots by (slot, row, block, half)
+    __shared__ float kr[512];  // (row, slot) terms
+    __shared__ float sw[DG_MAX_U];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t E = a.c[15], F = a.c[16], U = a.c[17], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
-    const uint32_t NB = F / 128u, t = blockIdx.y, row0 = blockIdx.x * DG_ROWS;
-    const uint32_t n_slots = n_tok * U;
-    const bool has_signs = a.c[11] != 0xffffffffu;
-    const uint32_t *GU = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1];
-    cuint *ids = as_const(gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * U);
-    cfloat *wtp = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * U);
-    reinterpret_cast<gd_u32x4 *>(book4)[tid] = gd_global4(gd_buf<const uint32_t>(a, a.c[10]))[tid];
+    const uint32_t E = a.c[15], F = a.c[16], U = a.c[17], R = a.c[19], NE = a.c[20];
+    const uint32_t NB = F / 128u, t = blockIdx.y, r0 = blockIdx.x * R;
+    const uint32_t NP = (R + 1u) / 2u, PK = NB * 2u * NP;  // row pairs; items per slot
+    const uint32_t n_items = U * PK;
+    const uint32_t *IDS = gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * U;
 
-    // (2) Down rows: expert k's run starts at row0 * 34 NB bytes of its down matrix.
-    const uint32_t run_chunks = DG_ROWS * NB * 34u / 16u;  // 17 NB
-    const uint64_t layer_base = (uint64_t)a.c[6] | ((uint64_t)a.c[7] << 32);
-    for (uint32_t c = tid; c < U * run_chunks; c += 512u) {
-        const uint32_t k = c / run_chunks, j = c - k * run_chunks;
-        const uint32_t e = min(ids[k], NE - 1u);
-        const uint8_t *src = reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)e * a.c[8] + a.c[9] +
-                             (size_t)row0 * NB * 34u;
-        rows[c] = *gd_global4(reinterpret_cast<const uint32_t *>(src + j * 16u));
+    // Expert ids of this thread's items (item j = ((k NB + bb) 2 + hf) NP + pair), then their blocks.
+    uint32_t e[DG_ITEMS];
+#pragma unroll
+    for (int s = 0; s < DG_ITEMS; ++s) {
+        const uint32_t j = tid + 512u * (uint32_t)s;
+        e[s] = j < n_items ? gd_global(IDS)[j / PK] : 0u;
     }
-
-    // (1) Down inputs, unit (k, bb) per 16 lanes.
+    // The codebook and weights are stored to LDS only after the block loads are issued (an LDS
+    // store of a loaded value waits for every load issued before it; so does the rotation).
+    const uint32_t swv = tid < U ? gd_global(gd_buf<const uint32_t>(a, a.c[4]) + a.c[5] + t * U)[tid] : 0u;
+    const gd_u32x4 bkv = gd_global4(gd_buf<const uint32_t>(a, a.c[10]))[tid];
+    const uint64_t layer_base = (uint64_t)a.c[6] | ((uint64_t)a.c[7] << 32);
+    const uint8_t *LB = reinterpret_cast<const uint8_t *>(layer_base);
+    const uint32_t stride = a.c[8], down_off = a.c[9], drow_bytes = NB * 34u;
+    // Inputs: unit (k, bb) per 16 lanes, up to DG_MAX_ABLK / 32 passes, every pass's loads
+    // issued before the first is rotated.
+    const bool has_signs = a.c[11] != 0xffffffffu;
+    const float *ACT = gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * U * F;
     const uint32_t l16 = lane & 15u;
-    for (uint32_t u = tid >> 4; u < U * NB; u += 32u) {  // uniform per 16-lane row
-        const uint32_t k = u / NB, bb = u - k * NB, i0 = bb * 128u + l16 * 8u;
-        const uint32_t slot = t * U + k;
-        float g[8] = {}, up[8] = {};
-        for (uint32_t p = 0; p < parts; ++p) {
-            gd_gu32x4 *gp = gd_global4(GU + ((size_t)(p * n_slots + slot) * 2u) * F + i0);
+    constexpr int PASSES = DG_MAX_ABLK / 32;
+    gd_u32x4 av[PASSES][2], svv[PASSES][2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const gd_u32x4 gv = gp[j], uv = gp[F / 4u + j];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    g[4 * j + c] += gd_bits_f32(gv[c]);
-                    up[4 * j + c] += gd_bits_f32(uv[c]);
-                }
+    for (int ps = 0; ps < PASSES; ++ps) {
+        const uint32_t u = (tid >> 4) + 32u * (uint32_t)ps;
+        if (u < U * NB) {  // uniform per 16-lane row
+            const uint32_t k = u / NB, bb = u - k * NB, i0 = bb * 128u + l16 * 8u;
+            gd_gu32x4 *ap = gd_global4(reinterpret_cast<const uint32_t *>(ACT + (size_t)k * F + i0));
+            av[ps][0] = ap[0];
+            av[ps][1] = ap[1];
+            if (has_signs) {
+                gd_gu32x4 *S = gd_global4(gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] + i0);
+                svv[ps][0] = S[0];
+                svv[ps][1] = S[1];
             }
         }
+    }
+    // The blocks after the inputs' loads, so the inputs can be rotated while they are in flight.
+    uint32_t dw[DG_ITEMS][2][9];
+    bool odd[DG_ITEMS][2];
+#pragma unroll
+    for (int s = 0; s < DG_ITEMS; ++s) {
+        const uint32_t j = tid + 512u * (uint32_t)s;
+        odd[s][0] = odd[s][1] = false;
+        if (j < n_items) {
+            const uint32_t rem = j % PK, bb = rem / (2u * NP), pair = rem % NP;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t row = min(2u * pair + (uint32_t)i, R - 1u);  // an odd R repeats its last row
+                const uint64_t off = (uint64_t)min(e[s], NE - 1u) * stride + down_off +
+                                     (uint64_t)(r0 + row) * drow_bytes + bb * 34u;
+                tq2_load_block(LB, off, dw[s][i]);
+                odd[s][i] = (off & 2u) != 0u;
+            }
+        }
+    }
+
+    book4[tid] = bkv;
+    if (tid < U) sw[tid] = gd_bits_f32(swv);
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+        const uint32_t u = (tid >> 4) + 32u * (uint32_t)ps;
+        if (u >= U * NB) break;  // uniform per 16-lane row
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gd_silu_rcp(g[j]) * up[j];
+        for (int j = 0; j < 4; ++j) { v[j] = gd_bits_f32(av[ps][0][j]); v[4 + j] = gd_bits_f32(av[ps][1][j]); }
         if (has_signs) {
-            gd_gu32x4 *S = gd_global4(gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] + i0);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const gd_u32x4 sv = S[j];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) v[4 * j + c] *= gd_bits_f32(sv[c]);
-            }
+            for (int j = 0; j < 4; ++j) { v[j] *= gd_bits_f32(svv[ps][0][j]); v[4 + j] *= gd_bits_f32(svv[ps][1][j]); }
 #pragma unroll
             for (int w = 1; w < 8; w <<= 1)
 #pragma unroll
@@ -94,76 +125,85 @@ GD_PIPELINE_NAMED(moe_decode_down_g, 512) {
                     }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p1 = gd_dpp_f<0xB1>(v[j]);
+                const float p1 = gd_dpp_f<0xB1>(v[j]);  // quad_perm [1,0,3,2]
                 v[j] = (l16 & 1u) ? p1 - v[j] : v[j] + p1;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p2 = gd_dpp_f<0x4E>(v[j]);
+                const float p2 = gd_dpp_f<0x4E>(v[j]);  // quad_perm [2,3,0,1]
                 v[j] = (l16 & 2u) ? p2 - v[j] : v[j] + p2;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float up4 = gd_dpp_f<0x104>(v[j]);
-                const float dn4 = gd_dpp_f<0x114>(v[j]);
+                const float up4 = gd_dpp_f<0x104>(v[j]), dn4 = gd_dpp_f<0x114>(v[j]);  // row_shl:4, row_shr:4
                 v[j] = (l16 & 4u) ? dn4 - v[j] : v[j] + up4;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float up8 = gd_dpp_f<0x108>(v[j]);
-                const float dn8 = gd_dpp_f<0x118>(v[j]);
+                const float up8 = gd_dpp_f<0x108>(v[j]), dn8 = gd_dpp_f<0x118>(v[j]);  // row_shl:8, row_shr:8
                 v[j] = (l16 & 8u) ? dn8 - v[j] : v[j] + up8;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] *= GD_INV_SQRT128;
         }
-        float4 *dst = reinterpret_cast<float4 *>(act + u * DG_BLOCK_STRIDE + l16 * 8u);
+        float4 *dst = reinterpret_cast<float4 *>(actr + u * DG_BLOCK_STRIDE + l16 * 8u);
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     __syncthreads();
 
-    // (3) Output row `wave`: unit 2 (k NB + bb) + hf on lanes l, l + 64, ...
-    const uint32_t n_units = U * NB * 2u;
-    const uint32_t *rw = reinterpret_cast<const uint32_t *>(rows);
-    float part[DG_MAX_UNITS / 64];
-    uint32_t pk[DG_MAX_UNITS / 64];
+    // Item dots: the half's 64 activations from LDS once, then that half of both rows' blocks;
+    // dred[((k R + row) NB + bb) 2 + hf].
+    const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
 #pragma unroll
-    for (int i = 0; i < DG_MAX_UNITS / 64; ++i) {
-        const uint32_t u = lane + 64u * (uint32_t)i;
-        part[i] = 0.f;
-        pk[i] = DG_MAX_U;
-        if (u < n_units) {
-            const uint32_t kb = u >> 1, hf = u & 1u, k = kb / NB, bb = kb - k * NB;
-            const uint32_t off = (k * DG_ROWS + wave) * NB * 34u + bb * 34u;  // byte in rows
-            uint32_t d[9];
+    for (int s = 0; s < DG_ITEMS; ++s) {
+        const uint32_t j = tid + 512u * (uint32_t)s;
+        if (j < n_items) {
+            const uint32_t k = j / PK, rem = j - k * PK, bh = rem / NP, pair = rem - bh * NP;
+            const uint32_t bb = bh >> 1, hf = bh & 1u;
+            const float4 *ar = reinterpret_cast<const float4 *>(actr + (k * NB + bb) * DG_BLOCK_STRIDE + 64u * hf);
+            float x[64];
 #pragma unroll
-            for (int j = 0; j < 9; ++j) d[j] = rw[(off >> 2) + j];
-            float sc;
-            uint32_t q[8];
-            tq2_unpack(d, (off & 2u) != 0u, sc, q);
-            part[i] = sc * tq2_half_dot(q, hf, reinterpret_cast<const uint32_t *>(book4),
-                                        act + kb * DG_BLOCK_STRIDE + 64u * hf);
-            pk[i] = k;
+            for (int c = 0; c < 16; ++c) {
+                const float4 v = ar[c];
+                x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t row = 2u * pair + (uint32_t)i;
+                float sc;
+                uint32_t q[8];
+                tq2_unpack(dw[s][i], odd[s][i], sc, q);
+                const float h = sc * tq2_half_dot(q, hf, book, x);
+                if (row < R) dred[((k * R + row) * NB + bb) * 2u + hf] = h;
+            }
         }
     }
-    // Per-expert sums of the units in unit order: lanes write their partials to LDS, then
-    // lane k < U adds expert k's 2 NB units in order.
-    __shared__ float upart[DG_ROWS][DG_MAX_UNITS];
-#pragma unroll
-    for (int i = 0; i < DG_MAX_UNITS / 64; ++i)
-        if (pk[i] < DG_MAX_U) upart[wave][lane + 64u * (uint32_t)i] = part[i];
     __syncthreads();
-    float s = 0.f;
-    if (lane < U)
-        for (uint32_t j = 0; j < 2u * NB; ++j) s += upart[wave][lane * 2u * NB + j];
-    // Lane 0 combines the experts in k order.
-    float acc = 0.f;
-    for (uint32_t k = 0; k < U; ++k)
-        acc += wtp[k] * gd_bits_f32((uint32_t)__builtin_amdgcn_readlane((int)gd_f32_bits(s), (int)k));
-    if (lane == 0u) {
-        const uint32_t orow = row0 + wave;
-        if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + t * E + orow] + acc;
-        gd_buf<float>(a, a.c[13])[a.c[14] + t * E + orow] = acc;
+    // (row, slot): w_k times the row's half sums in (block, half) order (2 NB <= 16 loads at once).
+    const uint32_t nbh = 2u * NB;
+    for (uint32_t p = tid; p < R * U; p += 512u) {
+        const uint32_t row = p / U, k = p - row * U;
+        const float *d = dred + (k * R + row) * nbh;
+        float dk = 0.f;
+#pragma unroll
+        for (uint32_t bh = 0; bh < 16u; ++bh) {
+            const float v = d[bh < nbh ? bh : nbh - 1u];
+            dk += bh < nbh ? v : 0.f;
+        }
+        kr[p] = sw[k] * dk;
+    }
+    __syncthreads();
+    if (tid < R) {  // the output row: slots in slot order, then the residual
+        const float *pk = kr + tid * U;
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t k = 0; k < DG_MAX_U; ++k) {
+            const float v = pk[k < U ? k : U - 1u];
+            acc += k < U ? v : 0.f;
+        }
+        const uint32_t r = t * E + r0 + tid;
+        if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + r] + acc;
+        gd_buf<float>(a, a.c[13])[a.c[14] + r] = acc;
     }
 }

@@ -1,124 +1,183 @@
 // Decode path, step 2, for the shapes moe_decode_gu does not take (hidden not a multiple of
-// 1024, top-U other than 8): routing and the fused TQ2_T dequant-GEMV of the gate and up rows,
-// as moe_decode_gu, with a partial last K-part and a runtime expert count.
+// 1024, F other than 512, top-U other than 8): routing and the fused TQ2_T dequant-GEMV of the
+// gate and up rows with the SwiGLU (src/engine.zig:567-606 without the down rotation).
 //
-// Every wave computes the token's top-U from the router logits (route_fast.h), so no separate
-// routing launch exists. A group of eight waves owns 64 rows of one projection (gate or up) of
-// one selected expert over one K-part of up to 8 Gyro blocks (1024 columns); lane l of wave w decodes
-// block l % 8 of row 8 w + l / 8 (32 trellis steps, two v_dot2_f32_f16 per step, codebook pairs
-// from LDS) and the 8-lane groups add their blocks with DPP ((b0 + b1) + (b2 + b3)) +
-// ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook and the
-// part's 1024 binary16 activations (both into LDS, one barrier, then each lane keeps its block's
-// 128 activations in registers). Once routing names the expert, every lane loads the 9 words of
-// its own block straight from HBM, so no further barrier is needed.
+// The n_tok x n_used x F output rows (token, slot, row) are cut into runs of RPG consecutive
+// rows, one run per group, so one launch round covers a token on the whole GPU whatever the
+// shape (RPG <= F: a run touches at most two slots and two tokens).
+//  - Independent loads first: each token's logits, the codebook and each token's rotated input
+//    (binary16, staged in LDS with block b's 16-byte chunk c at b * 16 + (c + b) % 16).
+//  - Routing (route_fast.h, unrolled rounds): wave 0 selects the first token's experts up to the
+//    last rank the run needs, wave 1 the second token's; a group whose run holds a token's first
+//    row runs all rounds for that token and stores its ids and weights.
+//  - Item (row, block), up to GG_ITEMS per thread: the row's gate and up blocks, each loaded
+//    straight from HBM (9 words each) and decoded against the block's 128 activations, read once
+//    from LDS for both (tq2_block_dot_h); each row's gate and up sums in block order through LDS.
+//  - act[(t n_used + k) F + f] = silu(g) * u.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
-// Grid: x = F / 64, y = 2 * parts (projection-major, parts = ceil(E / 1024); the last part
-// holds the E / 128 - 8 (parts - 1) remaining blocks), z = n_tok * n_used; 512 threads.
-// Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
-// Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
+// Grid: ceil(n_tok n_used F / RPG) groups; 512 threads.
+// Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used 4 scale (fp32 bits) 5 ids_uav
 // 6 ids_off 7 weights_uav 8 weights_off 9 xh16_uav 10 xh16_off (words) 11 base_lo 12 base_hi
-// 13 slot_stride 14 proj_bytes 15 codebook_srv 16 gu_uav 17 gu_off 18 E 19 F 20 n_tok.
-// Requires TQ2_T experts, E a multiple of 256, n_expert <= 256, 1 <= n_used <= 16 and F a
-// multiple of 64.
+// 13 slot_stride 14 proj_bytes 15 codebook_srv 16 act_uav 17 act_off 18 E 19 F 20 n_tok 21 RPG.
+// Requires TQ2_T experts, E a multiple of 256 up to 4096, n_expert <= 256, 1 <= n_used <= 16,
+// F a multiple of 128, RPG <= F and RPG E / 128 <= 512 GG_ITEMS (the host checks).
 #include "gyro_fast.h"
 #include "fwht.h"
 #include "route_fast.h"
 
-#define GU_ROWS 64
-#define GU_MAX_U 16
+#define GG_ITEMS 2       // (row, block) items per thread
+#define GG_MAX_U 16
+#define GG_MAX_RPG 512   // RPG E / 128 <= 1024 items
 
-GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
-    __shared__ uint4 book4[512];
-    __shared__ uint4 xpart[128];  // the part's 1024 activations as binary16 pairs
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t NE = a.c[2], U = a.c[3], E = a.c[18], F = a.c[19], n_tok = a.c[20];
-    const uint32_t slot = blockIdx.z, t = slot / U, k = slot - t * U;
-    const uint32_t parts = (E + 1023u) / 1024u, proj = blockIdx.y / parts, part = blockIdx.y - proj * parts;
-    const uint32_t nbp = min(8u, E / 128u - part * 8u);  // blocks of this part
-    const uint32_t row0 = blockIdx.x * GU_ROWS;
-    const uint32_t b = lane & 7u, r = wave * 8u + (lane >> 3);  // this lane's block and row
-
-    // Independent loads first, all in flight together (global loads, which no LDS store orders).
-    float lv[4];
-    rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
-    const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
-    const uint32_t xw = tid < nbp * 64u ? gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + part * 512u)[tid] : 0u;
-    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    // Chunk c (16 bytes) of block bx at position bx * 16 + (c + bx) % 16: the 8 blocks that a
-    // wave reads at one chunk index sit in 8 different bank groups.
-    const uint32_t bx = tid >> 6, cx = (tid >> 2) & 15u;
-    reinterpret_cast<uint32_t *>(xpart)[(bx * 16u + ((cx + bx) & 15u)) * 4u + (tid & 3u)] = xw;
-    __syncthreads();
-    uint32_t xs[64];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint4 v = xpart[b * 16u + ((j + b) & 15u)];
-        xs[4 * j] = v.x; xs[4 * j + 1] = v.y; xs[4 * j + 2] = v.z; xs[4 * j + 3] = v.w;
-    }
-
-    // Routing: this group needs the expert of rank k only, so it stops after round k; the one
-    // group that records the token's ids and weights runs all rounds and forms the weights once
-    // its own weight loads are in flight.
-    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
+// Selection rounds 0 .. need of one token (uniform per wave): the ids of ranks ka and kb; when
+// `writer`, every round and the token's ids and renormalised weights (rf_weights) stored by
+// lanes 0 .. U - 1.
+__device__ __forceinline__ void gg_route(const float lv[4], uint32_t NE, uint32_t U, uint32_t need, uint32_t ka,
+                                         uint32_t kb, bool writer, float scale, uint32_t *ids_out, float *w_out,
+                                         uint32_t &ida, uint32_t &idb) {
+    const uint32_t lane = threadIdx.x & 63u;
     uint64_t key[4];
     rf_init<4>(lv, NE, key);
-    uint32_t ids[GU_MAX_U], e = 0;
-    float top[GU_MAX_U];
+    uint32_t ids[GG_MAX_U];
+    float top[GG_MAX_U];
+    ida = idb = 0u;
 #pragma unroll
-    for (int j = 0; j < GU_MAX_U; ++j) {
-        if ((uint32_t)j < U && ((uint32_t)j <= k || writer)) {  // uniform
-            ids[j] = rf_next<4>(key, top[j]);
-            if ((uint32_t)j == k) e = ids[j];
+    for (int k = 0; k < GG_MAX_U; ++k) {
+        ids[k] = 0u;
+        top[k] = 0.f;
+        if ((uint32_t)k < U && ((uint32_t)k <= need || writer)) {  // uniform
+            ids[k] = rf_next<4>(key, top[k]);
+            if ((uint32_t)k == ka) ida = ids[k];
+            if ((uint32_t)k == kb) idb = ids[k];
         }
     }
-    e = e < NE ? e : NE - 1u;  // ids are always < NE for finite logits; never address past the layer
+    if (!writer) return;
+    float wts[GG_MAX_U], total = 0.f;
+#pragma unroll
+    for (int k = 0; k < GG_MAX_U; ++k) {
+        wts[k] = 0.f;
+        if ((uint32_t)k < U) {
+            wts[k] = expf(top[k] - top[0]);
+            total += wts[k];
+        }
+    }
+    const float inv = 1.0f / total;
+    uint32_t id = ids[0];
+    float w = wts[0];
+#pragma unroll
+    for (int k = 1; k < GG_MAX_U; ++k) {
+        id = lane == (uint32_t)k ? ids[k] : id;
+        w = lane == (uint32_t)k ? wts[k] : w;
+    }
+    w *= inv;
+    if (scale != 0.f && scale != 1.f) w *= scale;
+    if (lane < U) {
+        ids_out[lane] = id;
+        w_out[lane] = w;
+    }
+}
 
-    // Block b of row r of the part: 34 bytes at byte 34 b of the part (word aligned for even b),
-    // read as the 9 words from its 4-byte-aligned start.
+GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
+    __shared__ gd_u32x4 book4[512];
+    __shared__ uint4 xh4[2][4096 / 8];  // the run's (up to) two tokens' rotated inputs
+    __shared__ float gred[2 * GG_ITEMS * 512];  // (row, projection) block dots
+    __shared__ float gsum[2 * GG_MAX_RPG];
+    __shared__ uint32_t sid[2];  // experts of the run's first and second slot
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t NE = a.c[2], U = a.c[3], E = a.c[18], F = a.c[19], n_tok = a.c[20], RPG = a.c[21];
+    const uint32_t nb = E / 128u, UF = U * F;
+    const uint32_t row0 = blockIdx.x * RPG, rows = min(RPG, n_tok * UF - row0);
+    const uint32_t s0 = row0 / F, s1 = (row0 + rows - 1u) / F;  // s1 <= s0 + 1
+    const uint32_t t0 = s0 / U, t1 = s1 / U, k0 = s0 - t0 * U, k1 = s1 - t1 * U;
+
+    // Independent loads: logits (wave 0: t0, wave 1: t1), codebook, rotated inputs.
+    const uint32_t tw = wave == 0u ? t0 : t1;
+    float lv[4];
+    if (wave < 2u) rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + tw * NE, NE, lv);
+    book4[tid] = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
+    const uint32_t *XH = gd_buf<const uint32_t>(a, a.c[9]) + a.c[10];
+    for (uint32_t q = tid; q < (t1 != t0 ? 2u : 1u) * (E / 8u); q += 512u) {  // uint4 chunks
+        const uint32_t ti = q / (E / 8u), c16 = q - ti * (E / 8u), b = c16 >> 4, c = c16 & 15u;
+        const gd_u32x4 v = gd_global4(XH + (size_t)(ti ? t1 : t0) * (E / 2u))[c16];
+        xh4[ti][b * 16u + ((c + b) & 15u)] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+
+    // Routing.
+    const float scale = gd_bits_f32(a.c[4]);
+    uint32_t *ids_out = gd_buf<uint32_t>(a, a.c[5]) + a.c[6];
+    float *w_out = gd_buf<float>(a, a.c[7]) + a.c[8];
+    if (wave == 0u) {
+        const bool writer = row0 % UF == 0u;  // the run holds t0's first row
+        const uint32_t need = t1 == t0 ? k1 : k0;
+        uint32_t ida, idb;
+        gg_route(lv, NE, U, need, k0, k1, writer, scale, ids_out + t0 * U, w_out + t0 * U, ida, idb);
+        if (lane == 0) {
+            sid[0] = min(ida, NE - 1u);
+            if (t1 == t0) sid[1] = min(idb, NE - 1u);
+        }
+    } else if (wave == 1u && t1 != t0) {  // the run holds t1's first row (k1 == 0)
+        uint32_t ida, idb;
+        gg_route(lv, NE, U, 0u, k1, k1, true, scale, ids_out + t1 * U, w_out + t1 * U, ida, idb);
+        if (lane == 0) sid[1] = min(ida, NE - 1u);
+    }
+    __syncthreads();
+
+    // Items: row rr of the run and block b (b fastest), the gate and the up block of that row
+    // against the same 128 activations: 2 x 9 words from HBM each.
     const uint64_t layer_base = (uint64_t)a.c[11] | ((uint64_t)a.c[12] << 32);
-    const uint32_t row_bytes = E / 128u * 34u;
-    // Lanes past the last part's blocks contribute zero; their address stays on block 0.
-    const bool live = b < nbp;
-    gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(
-        reinterpret_cast<const uint8_t *>(layer_base) + (uint64_t)e * a.c[13] + (proj ? a.c[14] : 0u) +
-        (uint64_t)(row0 + r) * row_bytes + part * 272u + (((live ? b : 0u) * 34u) & ~3u)));
-    uint32_t d[9];
+    const uint8_t *LB = reinterpret_cast<const uint8_t *>(layer_base);
+    const uint32_t stride = a.c[13], proj_bytes = a.c[14], row_bytes = nb * 34u, n_items = rows * nb;
+    uint32_t dw[GG_ITEMS][2][9];
+    bool odd[GG_ITEMS];
 #pragma unroll
-    for (int j = 0; j < 9; ++j) d[j] = w[j];
-    if (writer && wave == 0u) {
-        // Softmax over the selected logits in rank order, times the scale unless it is 0 or 1.
-        float wts[GU_MAX_U], total = 0.f;
+    for (int s = 0; s < GG_ITEMS; ++s) {
+        const uint32_t j = tid + 512u * (uint32_t)s;
+        odd[s] = false;
+        if (j < n_items) {
+            const uint32_t rr = j / nb, b = j - rr * nb;
+            const uint32_t R = row0 + rr, f = R % F, e = sid[R / F != s0 ? 1 : 0];
+            const uint64_t off = (uint64_t)e * stride + (uint64_t)f * row_bytes + b * 34u;
 #pragma unroll
-        for (int j = 0; j < GU_MAX_U; ++j)
-            if ((uint32_t)j < U) {
-                wts[j] = expf(top[j] - top[0]);
-                total += wts[j];
-            }
-        const float inv = 1.0f / total, scale = gd_bits_f32(a.c[4]);
-        if (lane < U) {
-            uint32_t id = ids[0];
-            float wv = wts[0];
-#pragma unroll
-            for (int j = 1; j < GU_MAX_U; ++j) {
-                if ((uint32_t)j >= U) break;
-                id = lane == (uint32_t)j ? ids[j] : id;
-                wv = lane == (uint32_t)j ? wts[j] : wv;
-            }
-            wv *= inv;
-            if (scale != 0.f && scale != 1.f) wv *= scale;
-            gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * U + lane] = id;
-            gd_buf<float>(a, a.c[7])[a.c[8] + t * U + lane] = wv;
+            for (int p = 0; p < 2; ++p) tq2_load_block(LB, off + (p ? proj_bytes : 0u), dw[s][p]);
+            odd[s] = (off & 2u) != 0u;  // proj_bytes is a multiple of 4
         }
     }
-    float sc;
-    uint32_t q[8];
-    tq2_unpack(d, (b & 1u) != 0u, sc, q);
-    float v = live ? sc * tq2_block_dot_h(q, reinterpret_cast<const uint32_t *>(book4), xs) : 0.f;
-    v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
-    v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2
-    v = v + gd_dpp_f<0x104>(v);  // row_shl:4: + lane + 4 (read by lanes b < 4)
-    if (b == 0u) {
-        const uint32_t n_slots = n_tok * U;
-        gd_buf<float>(a, a.c[16])[a.c[17] + ((size_t)(part * n_slots + slot) * 2u + proj) * F + row0 + r] = v;
+    const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
+#pragma unroll
+    for (int s = 0; s < GG_ITEMS; ++s) {
+        const uint32_t j = tid + 512u * (uint32_t)s;
+        if (j < n_items) {
+            const uint32_t rr = j / nb, b = j - rr * nb;
+            const uint32_t ti = (row0 + rr) / UF != t0 ? 1u : 0u;
+            uint32_t xs[64];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const uint4 v = xh4[ti][b * 16u + (((uint32_t)c + b) & 15u)];
+                xs[4 * c] = v.x; xs[4 * c + 1] = v.y; xs[4 * c + 2] = v.z; xs[4 * c + 3] = v.w;
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                float sc;
+                uint32_t q[8];
+                tq2_unpack(dw[s][p], odd[s], sc, q);
+                gred[(2u * rr + (uint32_t)p) * nb + b] = sc * tq2_block_dot_h(q, book, xs);
+            }
+        }
     }
+    __syncthreads();
+    // Row sums in block order (nb <= 32 loads at once), then the SwiGLU.
+    for (uint32_t p = tid; p < rows * 2u; p += 512u) {
+        const float *src = gred + p * nb;
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t b = 0; b < 32u; ++b) {
+            const float v = src[b < nb ? b : nb - 1u];
+            acc += b < nb ? v : 0.f;
+        }
+        gsum[p] = acc;
+    }
+    __syncthreads();
+    float *act = gd_buf<float>(a, a.c[16]) + a.c[17];
+    for (uint32_t rr = tid; rr < rows; rr += 512u) act[row0 + rr] = gd_silu_rcp(gsum[2u * rr]) * gsum[2u * rr + 1u];
 }

@@ -770,10 +770,10 @@ class Engine {
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
-    // Routed experts: uniform TQ2_T layers take moe_decode_gu (E a multiple of 1024, top-8) or
-    // moe_decode_gu_g (E a multiple of 256 up to 4096, F a multiple of 128 up to 1024, top-1..16),
-    // and moe_decode_down (F 512, top-8, at most two K-parts) or moe_decode_down_g; other layers
-    // the type-generic kernels (_x for E a multiple of 1024, F 512, top-8; _xg otherwise).
+    // Routed experts: uniform TQ2_T layers take moe_decode_gu and moe_decode_down (E 1024 or 2048,
+    // F 512, top-8) or moe_decode_gu_g and moe_decode_down_g / _gl (E a multiple of 256 up to 4096,
+    // F a multiple of 128 up to 1024, top-1..16); other layers the type-generic kernels (_x for E
+    // a multiple of 1024, F 512, top-8; _xg otherwise).
     // Shared expert: a bf16 one of width <= 1024 (a multiple of 256) on E <= 2048 at the _x shapes
     // runs fused into moe_router and moe_decode_down_x; any other (bf16, Q8_0 or fp32, any width
     // a multiple of 64) runs in the mv kernels first and enters the down kernel as its residual
@@ -786,7 +786,10 @@ class Engine {
         return decode_generic_tuned() || general;
     }
     bool decode_generic_tuned() const { return E % 1024 == 0 && F == 512 && U == 8; }
-    bool decode_fast_down() const { return F == 512 && U == 8 && parts <= 2; }
+    // Uniform TQ2_T layers take moe_decode_gu / moe_decode_down at their compile-time shape
+    // (hidden 1024 or 2048, F 512, top-8), moe_decode_gu_g / moe_decode_down_g(l) otherwise.
+    bool decode_tuned_tq2() const { return E % 1024 == 0 && F == 512 && U == 8 && parts <= 2; }
+    uint32_t cus_or(uint32_t fallback) const { return cus ? cus : fallback; }
     bool decode_fused_shared(const Layer &L) const {
         return L.SF && L.sh_kind == GM_SHARED_BF16 && decode_generic_tuned() && L.SF <= 1024 && L.SF % 256 == 0 &&
                E <= 2048;
@@ -892,16 +895,37 @@ class Engine {
                               rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u, flag_uav()},
                              std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
         if (!decode_generic_types(L)) {
-            dispatch_maybe_timed(bracket == 2, marks, E % 1024 == 0 && U == 8 ? "moe_decode_gu" : "moe_decode_gu_g",
-                                 {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
-                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n},
-                                 F / 64, 2 * parts, n * U);
-            dispatch_maybe_timed(bracket == 3, marks, decode_fast_down() ? "moe_decode_down" : "moe_decode_down_g",
+            if (decode_tuned_tq2()) {
+                dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
+                                     {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh,
+                                      B.xh_off, base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n},
+                                     F / 64, 2 * parts, n * U);
+                dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
+                                     {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
+                                      2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
+                                      out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
+                                      st.res_off},
+                                     E / 8, n);
+                return;
+            }
+            // Other shapes: runs of RPG (token, slot, row) rows per gate/up group (at most 1024
+            // (row, block) items) and R output rows per down group (R divides E; at most 1024
+            // (slot, block, half, row pair) items and 512 (row, slot) sums), about one group per
+            // CU for a token.
+            const uint32_t nb = E / 128, total = n * U * F, target = cus_or(256);
+            const uint32_t rpg = std::max(1u, std::min({(total + target - 1) / target, F, 1024u / nb}));
+            uint32_t R = std::max(1u, E / target);
+            while (R > 1 && (E % R || U * (F / 128) * 2 * ((R + 1) / 2) > 1024 || R * U > 512)) --R;
+            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_g",
+                                 {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh,
+                                  B.xh_off, base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n,
+                                  rpg},
+                                 (total + rpg - 1) / rpg);
+            dispatch_maybe_timed(bracket == 3, marks, U * (F / 128) <= 64 ? "moe_decode_down_g" : "moe_decode_down_gl",
                                  {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
                                   2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                                  out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
-                                  st.res_off},
-                                 E / 8, n);
+                                  out_off, E, F, U, n, R, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
+                                 E / R, n);
             return;
         }
         dispatch_maybe_timed(bracket == 2, marks, decode_generic_tuned() ? "moe_decode_gu_x" : "moe_decode_gu_xg",
