@@ -147,5 +147,14 @@ __device__ __forceinline__ void gd_range_flag(const uint64_t *table, uint32_t fl
     if (flag && bad) reinterpret_cast<uint32_t *>(table[flag])[0] = 1u;
 }
 
+// XCD-aware order of the x groups of a grid: the dispatcher hands workgroup i (linear id) to
+// XCD i % 8, so logical index (i % 8) (G / 8) + i / 8 gives each XCD a contiguous run of G / 8
+// groups and neighbouring groups, which share the cache lines at their edges, one L2. A grid
+// whose x size G is a multiple of 8 keeps the property for every row y (linear id x + y G).
+// Identity when G % 8 != 0.
+__device__ __forceinline__ uint32_t gd_xcd_group(uint32_t x, uint32_t G) {
+    return (G & 7u) ? x : (x & 7u) * (G >> 3) + (x >> 3);
+}
+
 // 1 / sqrt(128) rounded to binary32, the normalisation of a 128-point Walsh-Hadamard block.
 #define GD_INV_SQRT128 0.0883883461356163f

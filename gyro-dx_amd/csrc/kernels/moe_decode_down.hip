@@ -39,7 +39,7 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const uint32_t E = a.c[15], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
-    const uint32_t t = blockIdx.y, row0 = blockIdx.x * DN_ROWS;
+    const uint32_t t = blockIdx.y, row0 = gd_xcd_group(blockIdx.x, gridDim.x) * DN_ROWS;
     const uint32_t n_slots = n_tok * DN_U;
     const bool has_signs = a.c[11] != 0xffffffffu;
 

@@ -41,7 +41,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
     __shared__ float sw[DG_MAX_U];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t E = a.c[15], F = a.c[16], U = a.c[17], R = a.c[19], NE = a.c[20];
-    const uint32_t NB = F / 128u, t = blockIdx.y, r0 = blockIdx.x * R;
+    const uint32_t NB = F / 128u, t = blockIdx.y, r0 = gd_xcd_group(blockIdx.x, gridDim.x) * R;
     const uint32_t NP = (R + 1u) / 2u, PK = NB * 2u * NP;  // row pairs; items per slot
     const uint32_t n_items = U * PK;
     const uint32_t *IDS = gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * U;

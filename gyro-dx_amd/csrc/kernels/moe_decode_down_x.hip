@@ -57,7 +57,7 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     __shared__ float shs[DN_ROWS];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t E = a.c[15], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
-    const uint32_t t = blockIdx.y, row0 = blockIdx.x * DN_ROWS;
+    const uint32_t t = blockIdx.y, row0 = gd_xcd_group(blockIdx.x, gridDim.x) * DN_ROWS;
     const uint32_t n_slots = n_tok * DN_U;
 
     // Down input of expert `wave`, block b = lane / 16, values l16 * 8 .. l16 * 8 + 7 of the

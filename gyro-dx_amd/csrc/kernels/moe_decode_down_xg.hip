@@ -46,7 +46,7 @@ GD_PIPELINE_NAMED(moe_decode_down_xg, 512) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t E = a.c[15], F = a.c[16], U = a.c[17], n_tok = a.c[18], parts = a.c[19], NE = a.c[20];
-    const uint32_t NB = F / 128u, t = blockIdx.y, row0 = blockIdx.x * DG_ROWS;
+    const uint32_t NB = F / 128u, t = blockIdx.y, row0 = gd_xcd_group(blockIdx.x, gridDim.x) * DG_ROWS;
     const uint32_t n_slots = n_tok * U;
     const bool has_signs = a.c[11] != 0xffffffffu;
     const uint32_t *GU = gd_buf<const uint32_t>(a, a.c[0]) + a.c[1];
