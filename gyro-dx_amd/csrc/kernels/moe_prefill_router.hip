@@ -10,10 +10,13 @@
 // adds the S planes in plane order. The MFMA operands take one row per lane, so each of these
 // waves stages its own 32-wide K chunks of the 32 token rows and the 32 router rows into LDS
 // first: direct global-to-LDS loads (8 lanes per 128-byte row, whole rows per load), the
-// 16-byte chunk q of row r stored at position q ^ (r % 8), two chunks ahead in three buffers per
-// wave, four chunks ahead in five buffers per wave; only the wave's own load count is waited
-// for, so the K loop has no barrier, and the operands of chunk c + 1 are read from LDS while the
-// MFMAs of chunk c run. Lane half h takes
+// 16-byte chunk q of row r stored at position q ^ (r % 8), four chunks ahead in five buffers per
+// wave; only the wave's own load count is waited for, so the K loop has no barrier. A wave's
+// MFMA holds back that wave's following instructions until it has nearly finished (other waves
+// issue meanwhile), and this wave is the only MFMA wave on its SIMD, so each chunk's sixteen
+// MFMAs carry the chunk's other work one piece at a time: a staging load after each of the
+// first eight, the reads of chunk c + 1 (into the other of two operand sets, no copies) after
+// the next four. Lane half h takes
 // k + 4h .. k + 4h + 3 of every 8 for both operands, so every product x[t][k] W[r][k] enters the
 // sum once. Waves 4..7 meanwhile rotate: all n * E/128 blocks are spread over the rotation
 // waves of the grid, eight blocks per wave at a time, so the rotation's memory traffic and VALU
@@ -64,6 +67,85 @@ __device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf,
     for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
 }
 
+// Operands of one staged chunk for this lane (row m, lane half h): four float4 of the token row
+// and four of the router row, k = 8 j + 4 h .. + 3 of the chunk for j = 0..3.
+struct RtOps {
+    float4 x[4], w[4];
+};
+__device__ __forceinline__ void rt_read(const RtLds &sm, uint32_t wave, uint32_t buf, uint32_t m, uint32_t h, RtOps &o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
+        o.x[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
+        o.w[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
+    }
+}
+__device__ __forceinline__ void rt_mfma4(f32x16 &acc, const float4 &x, const float4 &w) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.x, w.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.y, w.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.z, w.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.w, w.w, acc, 0, 0, 0);
+}
+// Chunk c's sixteen MFMAs (operands `cur`) with the chunk's other work between them, so that the
+// matrix pipe always has the next MFMA waiting: the eight loads staging chunk c + 4 (into the
+// buffer of chunk c - 1, read into registers two chunks ago) one after each of the first eight
+// MFMAs, then the wait for chunk c + 1 and its reads into `next`, two after each of the next
+// four. The following chunk's MFMAs use `next` once the four MFMAs after the reads have issued.
+// STEADY: chunks c + 1 .. c + 4 are all in flight (c + 4 < nc), so the wait is one immediate
+// count; otherwise `ahead` (the chunks issued after chunk c + 1) picks it.
+template <bool STEADY>
+__device__ __forceinline__ void rt_chunk(RtLds &sm, uint32_t wave, uint32_t c, uint32_t nc, uint32_t m, uint32_t h,
+                                         const void *xbase, const void *wbase, const uint32_t xoff[4],
+                                         const uint32_t woff[4], const RtOps &cur, RtOps &next, f32x16 &acc) {
+    const bool stage = STEADY || c + 4u < nc;
+    const uint32_t buf = (c + 4u) % RT_NBUF, kbytes = (c + 4u) * RT_KC * 4u;
+    const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float *xj = reinterpret_cast<const float *>(&cur.x[j]), *wj = reinterpret_cast<const float *>(&cur.w[j]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xj[q], wj[q], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (stage) {
+                if (j == 0) gg_dma16(lx + (uint32_t)q * 1024u, xbase, xoff[q] + kbytes);
+                else gg_dma16(lw + (uint32_t)q * 1024u, wbase, woff[q] + kbytes);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const bool more = STEADY || c + 1u < nc;
+    if (STEADY) {
+        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");  // chunks c + 2 .. c + 4 in flight
+    } else if (more) {
+        rt_wait(min(nc - 2u - c, RT_NBUF - 2u));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t rb = (c + 1u) % RT_NBUF;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float *>(&cur.x[2])[q],
+                                                   reinterpret_cast<const float *>(&cur.w[2])[q], acc, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
+            const uint32_t p = (2u * (uint32_t)q + h) ^ (m & 7u);
+            next.x[q] = __builtin_bit_cast(float4, sm.x[wave][rb][m * 8u + p]);
+            next.w[q] = __builtin_bit_cast(float4, sm.w[wave][rb][m * 8u + p]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    rt_mfma4(acc, cur.x[3], cur.w[3]);
+    // The operands stay allocated to the end of the chunk: a VGPR written while an MFMA that
+    // reads it is in flight holds the write (and the wave) until the MFMA has read it, about 27
+    // of its 64 cycles; left free, the compiler reuses them for address arithmetic right after
+    // the MFMA that reads them.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        asm volatile("" ::"v"(cur.x[j].x), "v"(cur.x[j].y), "v"(cur.x[j].z), "v"(cur.x[j].w));
+        asm volatile("" ::"v"(cur.w[j].x), "v"(cur.w[j].y), "v"(cur.w[j].z), "v"(cur.w[j].w));
+    }
+}
+
 // Sixteen values as binary16 pairs (32 bytes) at dst; `bad` records a value outside the range.
 __device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16], bool &bad) {
     gd_u32x4 o[2];
@@ -104,41 +186,19 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
             woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
         }
         for (uint32_t c = 0; c < nc && c < RT_NBUF - 1u; ++c) rt_stage(sm, wave, c, X, W, xoff, woff, c * RT_KC * 4u);
-        // Rows beyond n or n_expert were staged as copies of the last row; their operands are
-        // zeroed here.
-        const bool tv = t0 + m < n, rv = r0 + m < NE;
-        float4 xv[4], wv[4];
-        auto read_chunk = [&](uint32_t buf) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
-                xv[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
-                wv[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
-            }
-        };
+        // Rows beyond n or n_expert were staged as copies of the last row (finite values); they
+        // reach only tile rows and columns that are never stored.
+        RtOps ops[2];
         rt_wait(min(nc - 1u, RT_NBUF - 2u));  // chunks 1 .. 3 may be in flight
-        read_chunk(0);
-        for (uint32_t c = 0; c < nc; ++c) {
-            float4 xa[4], wa[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xa[j] = tv ? xv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-                wa[j] = rv ? wv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            // Chunk c + 4 into the buffer of chunk c - 1, whose operands were read (and waited
-            // for) before the MFMAs of chunk c - 1.
-            if (c + 4u < nc) rt_stage(sm, wave, (c + 4u) % RT_NBUF, X, W, xoff, woff, (c + 4u) * RT_KC * 4u);
-            if (c + 1u < nc) {
-                rt_wait(min(nc - 2u - c, RT_NBUF - 2u));  // chunks c + 2 .. c + 4 may be in flight
-                read_chunk((c + 1u) % RT_NBUF);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].x, wa[j].x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].y, wa[j].y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].z, wa[j].z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[j].w, wa[j].w, acc, 0, 0, 0);
-            }
+        rt_read(sm, wave, 0, m, h, ops[0]);
+        uint32_t c = 0;
+        for (; c + 5u < nc; c += 2u) {  // chunks c + 4 and c + 5 exist: steady state
+            rt_chunk<true>(sm, wave, c, nc, m, h, X, W, xoff, woff, ops[0], ops[1], acc);
+            rt_chunk<true>(sm, wave, c + 1u, nc, m, h, X, W, xoff, woff, ops[1], ops[0], acc);
+        }
+        for (; c < nc; c += 2u) {
+            rt_chunk<false>(sm, wave, c, nc, m, h, X, W, xoff, woff, ops[0], ops[1], acc);
+            if (c + 1u < nc) rt_chunk<false>(sm, wave, c + 1u, nc, m, h, X, W, xoff, woff, ops[1], ops[0], acc);
         }
         // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m. The wave's
         // buffers are free: its last LDS reads were waited for before its last MFMAs.
