@@ -220,9 +220,13 @@ def prefill_bench(eng, layer, args):
     eng.set_tokens(x)
     eng.run(PATH_PREFILL, PREFILL_TOKENS, min(batches, 4), layers, first=0)  # warm-up
     dev_ms, wall_ms, _ = eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, first=0)
+    # The engine runs both GEMMs as one persistent launch (bracket 2) unless created with
+    # GYRO_PREFILL_FUSED=0 (then moe_prefill_gu, bracket 2, and moe_prefill_down, bracket 3).
+    fused = os.environ.get("GYRO_PREFILL_FUSED", "1") != "0"
+    gemms = (("moe_prefill_gemm", 2),) if fused else (("moe_prefill_gu", 2), ("moe_prefill_down", 3))
     us = {}
-    for name, br in (("moe_prefill_router", 1), ("moe_prefill_topk", 4), ("moe_prefill_sort", 5),
-                     ("moe_prefill_gu", 2), ("moe_prefill_down", 3), ("moe_prefill_combine", 6)):
+    for name, br in (("moe_prefill_router", 1), ("moe_prefill_topk", 4), ("moe_prefill_sort", 5), *gemms,
+                     ("moe_prefill_combine", 6)):
         us[name] = round(eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, bracket=br, first=0)[2], 3)
     out0 = eng.read_outputs(PREFILL_TOKENS)
     # Distinct experts of the first batch (product path routes, read back after a forward).
@@ -231,7 +235,7 @@ def prefill_bench(eng, layer, args):
     distinct = int(np.unique(ids).size)
     t_call = wall_ms / batches * 1e-3
     t_dev = dev_ms / batches * 1e-3
-    gemm_s = (us["moe_prefill_gu"] + us["moe_prefill_down"]) * 1e-6
+    gemm_s = sum(us[name] for name, _ in gemms) * 1e-6
     res = {
         "workload": "single MoE layer, 1024-token prefill, Zipf(1.1) router bias, bf16 N(0,1) tokens",
         "tokens_per_call": PREFILL_TOKENS, "calls": batches, "layer_copies": args.copies,
@@ -246,14 +250,41 @@ def prefill_bench(eng, layer, args):
         "grouped_gemm_frac_of_peak": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "distinct_experts": distinct, "expert_bytes": distinct * BUNDLE_BYTES,
         "block_scales": BLOCK_SCALES,
-        # The grouped GEMMs' roofline: routed-expert FLOPs over the two GEMMs' dispatch times
-        # (measured above); the counter pass's MFMA-busy and useful-work fractions beside it.
-        "roofline": {"bound": "mfma", "kernel": "moe_prefill_gu + moe_prefill_down",
+        # The grouped GEMMs' roofline: routed-expert FLOPs over the GEMM launch's dispatch time
+        # (measured above); the counter pass's MFMA-busy and useful-work fractions of the
+        # gate/up and down units beside it.
+        "roofline": {"bound": "mfma", "kernel": " + ".join(name for name, _ in gemms),
                      "achieved": round(PREFILL_FLOPS / gemm_s / 1e12, 1), "peak": MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
                      "traffic": None, "counters": read_gemm_counters()},
     }
+    if fused:
+        res["two_launch_gemms"] = prefill_two_launch(zl, x, args)
     return res, x[:PREFILL_TOKENS], out0, zl
+
+
+def prefill_two_launch(zl, x, args):
+    """The same timed calls on an engine that runs the GEMMs as two launches (moe_prefill_gu,
+    moe_prefill_down): device time per call and the two kernels' dispatch times."""
+    from gyrodx.engine import PATH_PREFILL, Engine
+    saved = os.environ.get("GYRO_PREFILL_FUSED")
+    os.environ["GYRO_PREFILL_FUSED"] = "0"
+    try:
+        eng = Engine(max_tok=PREFILL_TOKENS)
+    finally:
+        if saved is None:
+            os.environ.pop("GYRO_PREFILL_FUSED", None)
+        else:
+            os.environ["GYRO_PREFILL_FUSED"] = saved
+    layers = [eng.add_layer(zl) for _ in range(args.copies)]
+    eng.set_tokens(x)
+    batches = args.prefill_calls
+    eng.run(PATH_PREFILL, PREFILL_TOKENS, min(batches, 4), layers, first=0)
+    dev_ms, _, _ = eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, first=0)
+    us = {name: round(eng.run(PATH_PREFILL, PREFILL_TOKENS, batches, layers, bracket=br, first=0)[2], 3)
+          for name, br in (("moe_prefill_gu", 2), ("moe_prefill_down", 3))}
+    eng.close()
+    return {"device_us_per_call": round(dev_ms / batches * 1e3, 2), "kernel_us": us}
 
 
 def prefill_cpu(layer, x, gpu_out, budget_s: float = 8.0):
@@ -505,7 +536,9 @@ def coder_bench(args):
         flops = PREFILL_TOKENS * cU * 3 * 2 * cE * cF
         dev_s = pdev / calls * 1e-3
         pus = {}
-        for name, br in (("router", 1), ("topk", 4), ("sort", 5), ("gate/up", 2), ("down", 3), ("combine", 6)):
+        one = type_id == 144 and os.environ.get("GYRO_PREFILL_FUSED", "1") != "0"  # TQ2_T: one GEMM launch
+        gemms = (("gate/up + down (one launch)", 2),) if one else (("gate/up", 2), ("down", 3))
+        for name, br in (("router", 1), ("topk", 4), ("sort", 5), *gemms, ("combine", 6)):
             pus[name] = round(eng.run(PATH_PREFILL, PREFILL_TOKENS, calls, ids, bracket=br, first=0)[2], 3)
         rec["prefill"] = {"tokens": PREFILL_TOKENS, "calls": calls, "tok_s": round(PREFILL_TOKENS * calls / pwall * 1e3, 1),
                           "device_us_per_call": round(dev_s * 1e6, 2), "kernel_us": pus, "flops_per_call": flops,

@@ -576,6 +576,7 @@ __device__ __forceinline__ void gh_kloop(GhLds &sm, const GhState &t, f32x16 (&a
     for (int r = 0; r < NRB; ++r) acc[r] = (f32x16){};
     const uint32_t nj = 2u * t.nk;
     uint32_t abuf = 0;  // buffer of sub-block j: j % 3
+#pragma unroll 1
     for (uint32_t kb = 0; kb < t.nk; ++kb) {
         const uint32_t j = 2u * kb;
         // Even sub-block: stage A(j + 2); read and unpack the weight block, first gathers.
@@ -625,7 +626,7 @@ __device__ __forceinline__ void gh_prologue(GhLds &sm, const GhState &t) {
 // the 128-point Walsh-Hadamard transform of every row as an MFMA product with H_128, and rows
 // of 128 binary16 values to out[row0 + i][fb * 128 ..].
 // sgn: the down sign of this gate lane's column (1 without signs), loaded before the K loop.
-template <int NRB>
+template <int NRB, bool COHERENT = false>
 __device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
                                                uint32_t h, bool signs, float sgn, uint32_t *out, uint32_t row0,
                                                uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
@@ -697,7 +698,17 @@ __device__ __forceinline__ void gh_gu_epilogue(GhLds &sm, const f32x16 (&acc)[NR
         (__attribute__((address_space(1))) gd_u32x4 *)(uintptr_t)(out + (size_t)row0 * (F / 2u) + fb * 64u);
     for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
         const uint32_t i = idx >> 4, c = idx & 15u;
-        og[(size_t)i * (F / 8u) + c] = rows_src[i * 16u + (c ^ (i & 15u))];
+        const gd_u32x4 v = rows_src[i * 16u + (c ^ (i & 15u))];
+        if constexpr (COHERENT) {
+            // Device-scope stores (written through to the point of coherence), for readers on
+            // other XCDs within the same launch.
+            __attribute__((address_space(1))) uint64_t *d =
+                reinterpret_cast<__attribute__((address_space(1))) uint64_t *>(og + (size_t)i * (F / 8u) + c);
+            __hip_atomic_store(d, (uint64_t)v[0] | ((uint64_t)v[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(d + 1, (uint64_t)v[2] | ((uint64_t)v[3] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            og[(size_t)i * (F / 8u) + c] = v;
+        }
     }
 }
 

@@ -299,6 +299,14 @@ class Engine {
     uint32_t cus = 0;
     uint32_t fused_mode = 0;
     uint32_t spin_limit = xch::kSpinLimit;
+    // Prefill GEMMs of uniform TQ2_T layers: one persistent launch over both (moe_prefill_gemm)
+    // unless the environment sets GYRO_PREFILL_FUSED=0 (then moe_prefill_gu and moe_prefill_down);
+    // the polls a down unit makes for its tile's gate/up rows before it gives up
+    // (GYRO_PREFILL_SPIN_LIMIT, default 2^20); its queue word, give-up word and tile counters.
+    bool prefill_fused = true;
+    uint32_t prefill_spin_limit = 1u << 20;
+    Buffer gemm_sched;
+    static constexpr uint32_t kSchedWords = 64;  // words before the tile counters
     std::string error;
     uint32_t max_tok = 0;
     uint32_t E = 0, F = 0, NE = 0, U = 0;
@@ -440,6 +448,10 @@ class Engine {
         const char *fe = std::getenv("GYRO_DECODE_FUSED");
         fused_mode = fe && fe[0] == '1' ? 1u : fe && fe[0] == '2' ? 2u : 0u;
         if (const char *sl = std::getenv("GYRO_DECODE_SPIN_LIMIT")) spin_limit = (uint32_t)std::strtoul(sl, nullptr, 10);
+        const char *pf = std::getenv("GYRO_PREFILL_FUSED");
+        prefill_fused = !(pf && pf[0] == '0');
+        if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
+            prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
         fill_zero(xch_area);
     }
@@ -468,6 +480,8 @@ class Engine {
         order = dev.buffer(T * U * 4, Kind::device);
         meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
         fill_zero(meta);
+        gemm_sched = dev.buffer((kSchedWords + max_tiles(max_tok)) * 4ull, Kind::device);
+        fill_zero(gemm_sched);
         // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
         Buffer z = dev.buffer(T * E * f, Kind::device);
         fill_zero(z);
@@ -834,6 +848,24 @@ class Engine {
         ~UnfusedScope() { e->fused_mode = was; }
     };
 
+    struct UnfusedPrefillScope {
+        Engine *e;
+        bool was;
+        explicit UnfusedPrefillScope(Engine *eng) : e(eng), was(eng->prefill_fused) { e->prefill_fused = false; }
+        ~UnfusedPrefillScope() { e->prefill_fused = was; }
+    };
+    // Reads and clears the give-up word of moe_prefill_gemm: set when a down unit stopped waiting
+    // for its tile's gate/up rows (the call's outputs are then invalid).
+    bool take_gemm_error() {
+        if (!gemm_sched.handle) return false;
+        uint32_t w = 0;
+        check(gd_readback(dev.ctx, gemm_sched.handle, 4, 4, &w, kTimeoutMs), "gd_readback");
+        if (!w) return false;
+        const uint32_t zero = 0;
+        upload(gemm_sched, 4, &zero, 4);
+        return true;
+    }
+
     // Reads and clears the sticky error word of the exchange area: set when a moe_decode_fused
     // group gave up a wait (its groups were not all running within the spin limit).
     bool take_fused_error(const Buffer &area) {
@@ -959,8 +991,9 @@ class Engine {
     }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
-    // down GEMMs, shared expert, combine. bracket: 1 router, 2 gate/up, 3 down, 4 top-k, 5 sort,
-    // 6 combine, 7 shared gate/up, 8 shared down.
+    // down GEMMs (one persistent launch for uniform TQ2_T layers), shared expert, combine.
+    // bracket: 1 router, 2 gate/up (the persistent launch: both GEMMs), 3 down (none with the
+    // persistent launch), 4 top-k, 5 sort, 6 combine, 7 shared gate/up, 8 shared down.
     void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                      int bracket = 0, std::vector<uint32_t> *marks = nullptr, uint32_t res_uav = kNone,
                      uint32_t res_off = 0) {
@@ -986,9 +1019,17 @@ class Engine {
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U},
                              (n + 3) / 4);
+        const bool fused = prefill_fused && L.type_id == 144;
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
-                             {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows}, 1);
-        if (L.type_id == 144) {
+                             {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows, fused ? gemm_sched.uav : 0u}, 1);
+        if (fused) {
+            // Both GEMMs in one persistent launch of two groups per compute unit (bracket 2).
+            dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gemm",
+                                 {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
+                                  codebook.srv, signs, E, act.uav, 0, E, F, U, 1u, down.uav, 0, gemm_sched.uav,
+                                  prefill_spin_limit},
+                                 2 * cus_or(256));
+        } else if (L.type_id == 144) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
                                  {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
                                   codebook.srv, signs, E, act.uav, 0, E, F, U, 1u},
@@ -1109,6 +1150,13 @@ class Engine {
             stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
             dev.wait(dev.submit());
         }
+        if (path == GM_PATH_PREFILL && take_gemm_error()) {
+            UnfusedPrefillScope unfused{this};
+            upload(x_in, 0, x, (uint64_t)n * E * 4);
+            dev.begin();
+            stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
+            dev.wait(dev.submit());
+        }
         if (fast_path(path) && take_range_flag()) {
             upload(x_in, 0, x, (uint64_t)n * E * 4);
             dev.begin();
@@ -1193,6 +1241,12 @@ class Engine {
         dev.wait(dev.submit());
         if (path == GM_PATH_DECODE && take_fused_error(xch_area)) {
             UnfusedScope unfused{this};
+            dev.begin();
+            ffn(path, il, n, x_in.uav, 0, out.uav, 0);
+            dev.wait(dev.submit());
+        }
+        if (path == GM_PATH_PREFILL && take_gemm_error()) {
+            UnfusedPrefillScope unfused{this};
             dev.begin();
             ffn(path, il, n, x_in.uav, 0, out.uav, 0);
             dev.wait(dev.submit());
@@ -1374,6 +1428,9 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
         if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
             throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
                                         "this run are invalid (gm_forward recomputes such calls on the three-kernel path)");
+        if (path == GM_PATH_PREFILL && e.take_gemm_error())
+            throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
+                                        "this run are invalid (gm_forward recomputes such calls with two GEMM launches)");
         if (Engine::fast_path(path) && e.take_range_flag())
             throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
                                         "are invalid (gm_forward recomputes such calls on GM_PATH_GENERIC)");
@@ -1416,6 +1473,9 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
             throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
                                         "this run are invalid (gm_forward_stack recomputes such calls on the three-kernel path)");
+        if (path == GM_PATH_PREFILL && e.take_gemm_error())
+            throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
+                                        "this run are invalid (gm_forward_stack recomputes such calls with two GEMM launches)");
         if (Engine::fast_path(path) && e.take_range_flag())
             throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
                                         "are invalid (gm_forward_stack recomputes such calls on GM_PATH_GENERIC)");

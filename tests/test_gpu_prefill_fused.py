@@ -1,0 +1,104 @@
+"""The persistent prefill GEMM launch (moe_prefill_gemm: the gate/up and down units of
+src/engine.zig:567-633 from one work queue) against the two-launch path (moe_prefill_gu,
+moe_prefill_down) and the CPU oracle.
+
+Both paths run the same units on the same tiles, so their outputs must be equal bit for bit; the
+persistent one must also meet the oracle bar of the prefill tests (relative RMS 2e-3, cosine
+0.9999 against the fp32 results of src/engine.zig:520-653). Shapes: the 1024-token Zipf layer of
+the benchmark, the real model's expert shape (hidden 2560, F 640 with its odd block count per
+down row, top-10), the widest hidden (4096, sixteen down units per tile) with top-16, F 384 with
+top-6, and batches of 1 and 33 tokens (one and a few tiles). The forced give-up (a spin limit of
+zero polls) must leave gm_forward's result unchanged: the call is recomputed with two launches.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from gyrodx import synth
+from gyrodx.engine import PATH_PREFILL, Engine
+
+pytestmark = pytest.mark.gpu
+REL_RMS, COSINE = 2e-3, 0.9999
+
+
+def make_engine(max_tok, fused, spin_limit=None):
+    saved = {k: os.environ.get(k) for k in ("GYRO_PREFILL_FUSED", "GYRO_PREFILL_SPIN_LIMIT")}
+    os.environ["GYRO_PREFILL_FUSED"] = "1" if fused else "0"
+    if spin_limit is not None:
+        os.environ["GYRO_PREFILL_SPIN_LIMIT"] = str(spin_limit)
+    try:
+        return Engine(max_tok=max_tok)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+SHAPES = [
+    # E, F, experts, top-k, tokens, extra make_layer arguments
+    (2048, 512, 256, 8, 1024, {"zipf": 1.1}),
+    (2560, 640, 64, 10, 300, {}),
+    (4096, 256, 16, 16, 64, {}),
+    (2048, 384, 64, 6, 200, {"signs": False}),
+    (1024, 256, 32, 4, 1, {}),
+    (1024, 256, 32, 4, 33, {"zipf": 1.1}),
+]
+
+
+@pytest.mark.parametrize("E,F,NE,U,n,kw", SHAPES,
+                         ids=[f"E{s[0]}-F{s[1]}-x{s[2]}-top{s[3]}-n{s[4]}" + "".join(f"-{k}" for k in s[5]) for s in SHAPES])
+def test_persistent_gemm_matches_two_launches(oracle_mod, E, F, NE, U, n, kw):
+    L = synth.make_layer(1500 + E // 128 + F // 64 + U, E=E, F=F, n_expert=NE, n_used=U, **kw)
+    x = synth.make_tokens(1501 + n, n, E, bf16=True)
+    outs = {}
+    for fused in (True, False):
+        eng = make_engine(max(n, 64), fused)
+        try:
+            eng.add_layer(L)
+            print(f"prefill E={E} F={F} experts={NE} top-{U} n={n} {'persistent' if fused else 'two launches'}",
+                  flush=True)
+            outs[fused] = eng.forward(0, x, PATH_PREFILL)
+            if fused:
+                tiles = eng.last_tiles()
+                print(f"  {len(tiles)} tiles", flush=True)
+        finally:
+            eng.close()
+    np.testing.assert_array_equal(outs[True].view(np.uint32), outs[False].view(np.uint32))
+    ref = oracle_mod.OracleLayer(L).forward(x)
+    r, c = oracle_mod.rel_rms(ref, outs[True]), oracle_mod.cosine(ref, outs[True])
+    print(f"  bit-equal to the two-launch path; rel_rms {r:.3e} cosine {c:.8f}", flush=True)
+    assert r <= REL_RMS and c >= COSINE
+
+
+def test_persistent_gemm_give_up_recomputes():
+    """With a spin limit of zero polls a down unit whose tile is not finished gives up at once;
+    gm_forward then recomputes the call with two launches, so its result is unchanged. gm_run
+    reports such a call as invalid instead."""
+    L = synth.make_layer(1560, zipf=1.1)
+    n = 1024
+    x = synth.make_tokens(1561, 2 * n, bf16=True)
+    ref_eng = make_engine(n, False)
+    try:
+        ref_eng.add_layer(L)
+        ref = ref_eng.forward(0, x[:n], PATH_PREFILL)
+    finally:
+        ref_eng.close()
+    eng = make_engine(n, True, spin_limit=0)
+    try:
+        eng.add_layer(L)
+        print("persistent prefill GEMM, spin limit 0", flush=True)
+        out = eng.forward(0, x[:n], PATH_PREFILL)
+        np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+        eng.set_tokens(x)
+        try:
+            eng.run(PATH_PREFILL, n, 2, [0])
+            print("  gm_run: no unit gave up", flush=True)
+        except RuntimeError as err:
+            assert "gave up waiting" in str(err), err
+            print("  gm_run reported the give-up", flush=True)
+        # The give-up word is cleared: a call with a normal limit on a fresh engine is clean.
+    finally:
+        eng.close()

@@ -95,6 +95,7 @@ PREFILL = ("moe_prefill_router", "moe_prefill_topk", "moe_prefill_sort", "moe_pr
            "moe_prefill_combine")
 PREFILL_X = ("moe_prefill_gu_x", "moe_prefill_down_x")
 PREFILL_SH = ("moe_prefill_router", "moe_prefill_shared", "moe_prefill_shared", "moe_prefill_combine")
+PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm")
 
 
 def sequence(kind: str, ns):
@@ -111,6 +112,8 @@ def sequence(kind: str, ns):
     if kind == "decode_xg":
         return [block(*DECODE_TQ2)[0], *block(*DECODE_XG)]
     p = block(*PREFILL)
+    if kind == "prefill_gemm":  # the sort with the queue buffer and both GEMMs in one launch
+        return [*p[:2], *block(*PREFILL_ONE), p[5]]
     mid = block(*PREFILL_X) if ns.mixed else p[3:5]
     if ns.SF:
         sh = block(*PREFILL_SH)
@@ -133,6 +136,8 @@ CASES = [
     ("prefill", 1024, 384, 32, 6, 50, {"mixed_types": True}),
     ("prefill", 1024, 512, 32, 8, 40, {"SF": 256}),
     ("prefill", 1024, 256, 16, 4, 30, {"mixed_types": True, "SF": 128, "signs": False}),
+    ("prefill_gemm", 1024, 512, 64, 8, 100, {}),
+    ("prefill_gemm", 2560, 640, 64, 10, 70, {"zipf": 1.1}),
 ]
 IDS = [f"{c[0]}-E{c[1]}-F{c[2]}-x{c[3]}-top{c[4]}-n{c[5]}" + "".join(f"-{k}" for k in c[6]) for c in CASES]
 
@@ -203,6 +208,7 @@ def names(L, n: int, cus: int, buffer):
         S *= 2
     ns.S = S
     ns.tiles = -(-n * U // 128) + min(NE, n * U)
+    ns.cus = cus
     # Call buffers, each sized for nt >= n tokens (whole 64-token tiles and one more) so that no
     # kernel's tile rounding can reach past a buffer.
     nt = -(-n // 64) * 64 + 64
@@ -210,7 +216,7 @@ def names(L, n: int, cus: int, buffer):
                  ids=nt * U * 4, weights=nt * U * 4, gu=ns.parts * nt * U * 2 * F * 4, act=nt * U * F * 4,
                  order=nt * U * 4, meta=(1024 + 4 * (ns.tiles + 64)) * 4, act16=nt * U * F * 2,
                  down32=nt * U * E * 4, sh_h=nt * 2 * max(SF, 1) * 4, sh_g=nt * 4, x16=nt * E * 2,
-                 sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4)
+                 sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4, sched=(64 + ns.tiles + 64) * 4)
     for k, v in sizes.items():
         setattr(ns, k, buffer(v, None))
     return ns
@@ -343,7 +349,7 @@ def device_cus() -> int:
 def test_snippets_replay(oracle_mod, case):
     kind, L, x = make_case(case)
     n, E, U = x.shape[0], L.E, L.n_used
-    path = PATH_PREFILL if kind == "prefill" else PATH_DECODE
+    path = PATH_PREFILL if kind.startswith("prefill") else PATH_DECODE
     ol = oracle_mod.OracleLayer(L)
     ref, tr = ol.forward(x, trace=True)
     logits = ol.router_f64(x)
