@@ -22,8 +22,8 @@
 // [1024 + 4 i ..] tile i = {expert, first sorted row, rows, 0}.
 // Grid: 1; 1024 threads. Requires n_expert <= 512, n_slots <= 32768, tile_rows <= 256.
 // Constants: 0 ids_uav 1 ids_off 2 n_slots 3 n_expert 4 order_uav 5 order_off 6 meta_uav
-// 7 tile_rows 8 sched_uav (0: none; else words 0 .. 63 + tile count are zeroed for
-// moe_prefill_gemm: its queue word, give-up word and one counter per tile).
+// 7 tile_rows 8 sched_uav (0: none; else words 0 .. 63 + 2 x tile count are zeroed for
+// moe_prefill_gemm: its queue words, give-up word, one counter and one ready slot per tile).
 #include "gd_kernel.h"
 
 #define SORT_MAX_E 512
@@ -114,7 +114,7 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
     if (tid == 0) meta[1023] = tstart[NE];
     if (a.c[8]) {  // the persistent GEMM's queue word, give-up word and per-tile counters
         uint32_t *sched = gd_buf<uint32_t>(a, a.c[8]);
-        for (uint32_t i = tid; i < 64u + tstart[NE]; i += 1024u) sched[i] = 0u;
+        for (uint32_t i = tid; i < 64u + 2u * tstart[NE]; i += 1024u) sched[i] = 0u;
     }
     // Cursors: segment start plus the counts of earlier runs.
     if (tid < NE) {

@@ -301,12 +301,12 @@ class Engine {
     uint32_t spin_limit = xch::kSpinLimit;
     // Prefill GEMMs of uniform TQ2_T layers: one persistent launch over both (moe_prefill_gemm)
     // unless the environment sets GYRO_PREFILL_FUSED=0 (then moe_prefill_gu and moe_prefill_down);
-    // the polls a down unit makes for its tile's gate/up rows before it gives up
-    // (GYRO_PREFILL_SPIN_LIMIT, default 2^20); its queue word, give-up word and tile counters.
+    // the polls a down unit makes for a ready tile before it gives up (GYRO_PREFILL_SPIN_LIMIT,
+    // default 2^20); its queue words, give-up word, tile counters and ready list.
     bool prefill_fused = true;
     uint32_t prefill_spin_limit = 1u << 20;
     Buffer gemm_sched;
-    static constexpr uint32_t kSchedWords = 64;  // words before the tile counters
+    static constexpr uint32_t kSchedWords = 64;  // words before the tile counters and the ready list
     std::string error;
     uint32_t max_tok = 0;
     uint32_t E = 0, F = 0, NE = 0, U = 0;
@@ -480,7 +480,7 @@ class Engine {
         order = dev.buffer(T * U * 4, Kind::device);
         meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
         fill_zero(meta);
-        gemm_sched = dev.buffer((kSchedWords + max_tiles(max_tok)) * 4ull, Kind::device);
+        gemm_sched = dev.buffer((kSchedWords + 2ull * max_tiles(max_tok)) * 4ull, Kind::device);
         fill_zero(gemm_sched);
         // The shared-expert inputs of moe_combine: zero output and gate (sigmoid(0) * 0 = 0).
         Buffer z = dev.buffer(T * E * f, Kind::device);

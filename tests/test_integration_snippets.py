@@ -216,7 +216,7 @@ def names(L, n: int, cus: int, buffer):
                  ids=nt * U * 4, weights=nt * U * 4, gu=ns.parts * nt * U * 2 * F * 4, act=nt * U * F * 4,
                  order=nt * U * 4, meta=(1024 + 4 * (ns.tiles + 64)) * 4, act16=nt * U * F * 2,
                  down32=nt * U * E * 4, sh_h=nt * 2 * max(SF, 1) * 4, sh_g=nt * 4, x16=nt * E * 2,
-                 sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4, sched=(64 + ns.tiles + 64) * 4)
+                 sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4, sched=(64 + 2 * ns.tiles + 64) * 4)
     for k, v in sizes.items():
         setattr(ns, k, buffer(v, None))
     return ns
