@@ -543,13 +543,15 @@ __device__ __forceinline__ void gh_half(const GhLds &sm, uint32_t arow, const ui
         for (int i = 0; i < NRB; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], bv, acc[i], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
+            // The A operand first: LDS reads retire in order, so the wait for it before the next
+            // MFMA then leaves the (younger) gathers of step s + 2 in flight.
+            if (sl < 3) av[i] = gh_a(sm, (arow ^ (32u * (uint32_t)(sl + 1))) + (uint32_t)i * 32u * GH_AROW);
             if (s < 6) {
 #pragma unroll
                 for (int piece = 0; piece < 2; ++piece)
                     if (i < kPieceSlots && piece * kPieceSlots / 2 == i)
                         gg_gather_piece(q, s + 2, piece, sel, sm.book, pr[s & 1], raw[s & 1]);
             }
-            if (sl < 3) av[i] = gh_a(sm, (arow ^ (32u * (uint32_t)(sl + 1))) + (uint32_t)i * 32u * GH_AROW);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
