@@ -261,6 +261,47 @@ __device__ __forceinline__ float gyro_block_dot(const uint32_t (&w)[gyro_nw<ID>(
     }
 }
 
+// Half hf of a block against its 64 fp32 activations x[0 .. 63]: trellis steps hf S / 2 ..
+// hf S / 2 + S / 2 - 1 (hf per lane). For hf = 1 the circular stream is first rotated left by
+// the S K / 2 bits of a half, which puts the states of those steps where steps 0 .. S / 2 - 1
+// read theirs; the sums then run as in gyro_block_dot.
+template <int ID, typename XP>
+__device__ __forceinline__ float gyro_half_dot(const uint32_t (&w)[gyro_nw<ID>()], uint32_t hf, const uint32_t *book,
+                                               XP x) {
+    if constexpr (ID == 144) {
+        return tq2_half_dot(w, hf, book, x);
+    } else {
+        constexpr int NW = gyro_nw<ID>(), S = GyroT<ID>::S, HB = S / 2 * GyroT<ID>::K, q = HB / 32, r = HB % 32;
+        uint32_t v[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const uint32_t hi = w[(i - q + NW) % NW], lo = w[(i - q - 1 + 2 * NW) % NW];
+            const uint32_t rot = r ? __builtin_amdgcn_alignbit(hi, lo, 32 - r) : hi;
+            v[i] = hf ? rot : w[i];
+        }
+        float acc0 = 0.f, acc1 = 0.f;
+        if constexpr (S == 32) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                uint32_t a0, a1;
+                cb_addr(gyro_kstate<ID>(v, t), a0, a1);
+                const uint32_t p0 = lds_word(book, a0), p1 = lds_word(book, a1);
+                acc0 = fma_hi(p0, x[4 * t + 1], fma_lo(p0, x[4 * t], acc0));
+                acc1 = fma_hi(p1, x[4 * t + 3], fma_lo(p1, x[4 * t + 2], acc1));
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 32; t += 2) {
+                const uint32_t p0 = lds_word(book, cb_addr0(gyro_kstate<ID>(v, t)));
+                const uint32_t p1 = lds_word(book, cb_addr0(gyro_kstate<ID>(v, t + 1)));
+                acc0 = fma_hi(p0, x[2 * t + 1], fma_lo(p0, x[2 * t], acc0));
+                acc1 = fma_hi(p1, x[2 * t + 3], fma_lo(p1, x[2 * t + 2], acc1));
+            }
+        }
+        return acc0 + acc1;
+    }
+}
+
 // Expands X(ID) for the (uniform) Gyro type id; unknown ids do nothing.
 #define GYRO_TYPE_SWITCH(id, X)       \
     switch (id) {                     \

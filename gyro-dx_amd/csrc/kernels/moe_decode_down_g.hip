@@ -28,8 +28,15 @@
 #define DG_MAX_ABLK 64  // rotated input blocks (slots x F / 128) in LDS
 #define DG_PIPELINE moe_decode_down_g
 #endif
+#ifndef DG_GENERIC
+#define DG_GENERIC 0  // 1: any Gyro type per expert, rows from the expert table
+#endif
+// Words loaded per block: TQ2_T's 34 bytes, or the widest type's 58 (whole words from the
+// block's first byte rounded down to a word; the arena's slack covers reads past the last row).
+#define DG_WORDS (DG_GENERIC ? 15 : 9)
 #define DG_ITEMS 2  // (slot, block, half, row pair) items per thread
 #define DG_MAX_U 16
+#define DG_MAX_EXPERTS 256
 #define DG_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
 #define DG_BLOCK_STRIDE 132  // floats per 128-block of an input in LDS (bank spread)
 
@@ -39,65 +46,106 @@ DG_DEFINE(DG_PIPELINE, 512) {
     __shared__ float dred[2 * DG_ITEMS * 512];  // half dots by (slot, row, block, half)
     __shared__ float kr[512];  // (row, slot) terms
     __shared__ float sw[DG_MAX_U];
+#if DG_GENERIC
+    __shared__ gd_u32x4 xdesc[DG_MAX_EXPERTS];  // per expert {down lo, down hi, types, pad}
+#endif
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t E = a.c[15], F = a.c[16], U = a.c[17], R = a.c[19], NE = a.c[20];
     const uint32_t NB = F / 128u, t = blockIdx.y, r0 = gd_xcd_group(blockIdx.x, gridDim.x) * R;
     const uint32_t NP = (R + 1u) / 2u, PK = NB * 2u * NP;  // row pairs; items per slot
     const uint32_t n_items = U * PK;
     const uint32_t *IDS = gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * U;
+#if DG_GENERIC
+    // The expert table's down pointers and types first: they go to LDS while the ids load.
+    const gd_u32x4 xdv = gd_global4(gd_buf<const uint32_t>(a, a.c[24]))[2u * min(tid, NE - 1u) + 1u];
+#endif
 
-    // Expert ids of this thread's items (item j = ((k NB + bb) 2 + hf) NP + pair), then their blocks.
+    // Expert ids of this thread's items (item j = ((k NB + bb) 2 + hf) NP + pair), then their
+    // blocks. A thread past the last item loads that item's block again, so that the first item's
+    // block loads are issued by every thread: with loads skipped on some path, the compiler could
+    // only wait for all loads (the blocks included) before the inputs are rotated.
     uint32_t e[DG_ITEMS];
 #pragma unroll
     for (int s = 0; s < DG_ITEMS; ++s) {
-        const uint32_t j = tid + 512u * (uint32_t)s;
-        e[s] = j < n_items ? gd_global(IDS)[j / PK] : 0u;
+        const uint32_t j = min(tid + 512u * (uint32_t)s, n_items - 1u);
+        e[s] = gd_global(IDS)[j / PK];
     }
+    // The output row's address and its residual now, not after the sums: there they would add
+    // two table reads and a load to the end of the group. Without a residual the output row is
+    // read instead, and not used.
+    float *OUT = gd_buf<float>(a, a.c[13]) + a.c[14];
+    const bool residual = a.c[21] != 0u;
+    const float *RES = residual ? gd_buf<const float>(a, a.c[22]) + a.c[23] : OUT;
+    const uint32_t orow = t * E + r0 + min(tid, R - 1u);
+    const uint32_t resv = gd_global(reinterpret_cast<const uint32_t *>(RES))[orow];
     // The codebook and weights are stored to LDS only after the block loads are issued (an LDS
     // store of a loaded value waits for every load issued before it; so does the rotation).
     const uint32_t swv = tid < U ? gd_global(gd_buf<const uint32_t>(a, a.c[4]) + a.c[5] + t * U)[tid] : 0u;
     const gd_u32x4 bkv = gd_global4(gd_buf<const uint32_t>(a, a.c[10]))[tid];
+#if !DG_GENERIC
     const uint64_t layer_base = (uint64_t)a.c[6] | ((uint64_t)a.c[7] << 32);
     const uint8_t *LB = reinterpret_cast<const uint8_t *>(layer_base);
     const uint32_t stride = a.c[8], down_off = a.c[9], drow_bytes = NB * 34u;
+#endif
     // Inputs: unit (k, bb) per 16 lanes, up to DG_MAX_ABLK / 32 passes, every pass's loads
-    // issued before the first is rotated.
+    // issued before the first is rotated. Every lane loads (a row past the last unit repeats
+    // it; without signs the inputs stand in for them), so that the waits for the ids and the
+    // inputs leave the loads issued after them in flight.
     const bool has_signs = a.c[11] != 0xffffffffu;
     const float *ACT = gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * U * F;
+    const uint32_t *SG = has_signs ? gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] : reinterpret_cast<const uint32_t *>(ACT);
     const uint32_t l16 = lane & 15u;
     constexpr int PASSES = DG_MAX_ABLK / 32;
     gd_u32x4 av[PASSES][2], svv[PASSES][2];
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
-        const uint32_t u = (tid >> 4) + 32u * (uint32_t)ps;
-        if (u < U * NB) {  // uniform per 16-lane row
-            const uint32_t k = u / NB, bb = u - k * NB, i0 = bb * 128u + l16 * 8u;
-            gd_gu32x4 *ap = gd_global4(reinterpret_cast<const uint32_t *>(ACT + (size_t)k * F + i0));
-            av[ps][0] = ap[0];
-            av[ps][1] = ap[1];
-            if (has_signs) {
-                gd_gu32x4 *S = gd_global4(gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] + i0);
-                svv[ps][0] = S[0];
-                svv[ps][1] = S[1];
-            }
-        }
+        if (ps >= 2 && 32u * (uint32_t)ps >= U * NB) break;  // uniform: passes past 64 blocks only when used
+        const uint32_t u = min((tid >> 4) + 32u * (uint32_t)ps, U * NB - 1u);
+        const uint32_t k = u / NB, bb = u - k * NB, i0 = bb * 128u + l16 * 8u;
+        gd_gu32x4 *ap = gd_global4(reinterpret_cast<const uint32_t *>(ACT + (size_t)k * F + i0));
+        av[ps][0] = ap[0];
+        av[ps][1] = ap[1];
+        gd_gu32x4 *S = gd_global4(SG + i0);
+        svv[ps][0] = S[0];
+        svv[ps][1] = S[1];
     }
+#if DG_GENERIC
+    if (tid < NE) xdesc[tid] = xdv;
+    __syncthreads();
+#endif
     // The blocks after the inputs' loads, so the inputs can be rotated while they are in flight.
-    uint32_t dw[DG_ITEMS][2][9];
+    uint32_t dw[DG_ITEMS][2][DG_WORDS];
     bool odd[DG_ITEMS][2];
+    uint32_t ty[DG_ITEMS];
 #pragma unroll
     for (int s = 0; s < DG_ITEMS; ++s) {
-        const uint32_t j = tid + 512u * (uint32_t)s;
+        const uint32_t j = min(tid + 512u * (uint32_t)s, n_items - 1u);
         odd[s][0] = odd[s][1] = false;
-        if (j < n_items) {
+        ty[s] = 144u;
+        if (s == 0 || n_items > 512u * (uint32_t)s) {  // uniform
             const uint32_t rem = j % PK, bb = rem / (2u * NP), pair = rem % NP;
+#if DG_GENERIC
+            const gd_u32x4 xd = xdesc[min(e[s], NE - 1u)];
+            ty[s] = (xd[2] >> 16) & 0xffu;
+            GyroType gt;
+            gd_type(ty[s], gt);  // the host admits only the eight types
+            const uint8_t *LB = reinterpret_cast<const uint8_t *>(((uint64_t)xd[1] << 32) | xd[0]);
+#endif
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const uint32_t row = min(2u * pair + (uint32_t)i, R - 1u);  // an odd R repeats its last row
+#if DG_GENERIC
+                const uint64_t off = ((uint64_t)(r0 + row) * NB + bb) * gt.block_bytes;
+                gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(LB + (off & ~uint64_t(3))));
+#pragma unroll
+                for (int q = 0; q < DG_WORDS; ++q) dw[s][i][q] = w[q];
+                odd[s][i] = ((reinterpret_cast<uintptr_t>(LB) + off) & 2u) != 0u;
+#else
                 const uint64_t off = (uint64_t)min(e[s], NE - 1u) * stride + down_off +
                                      (uint64_t)(r0 + row) * drow_bytes + bb * 34u;
                 tq2_load_block(LB, off, dw[s][i]);
                 odd[s][i] = (off & 2u) != 0u;
+#endif
             }
         }
     }
@@ -168,14 +216,30 @@ DG_DEFINE(DG_PIPELINE, 512) {
                 const float4 v = ar[c];
                 x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
             }
+            float h[2] = {0.f, 0.f};
+#if DG_GENERIC
+#define DG_CASE(ID)                                                       \
+    _Pragma("unroll") for (int i = 0; i < 2; ++i) {                       \
+        float sc;                                                         \
+        uint32_t q[gyro_nw<ID>()];                                        \
+        gyro_unpack<ID>(dw[s][i], odd[s][i], sc, q);                      \
+        h[i] = sc * gyro_half_dot<ID>(q, hf, book, x);                    \
+    }
+            GYRO_TYPE_SWITCH(ty[s], DG_CASE)
+#undef DG_CASE
+#else
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const uint32_t row = 2u * pair + (uint32_t)i;
                 float sc;
                 uint32_t q[8];
                 tq2_unpack(dw[s][i], odd[s][i], sc, q);
-                const float h = sc * tq2_half_dot(q, hf, book, x);
-                if (row < R) dred[((k * R + row) * NB + bb) * 2u + hf] = h;
+                h[i] = sc * tq2_half_dot(q, hf, book, x);
+            }
+#endif
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t row = 2u * pair + (uint32_t)i;
+                if (row < R) dred[((k * R + row) * NB + bb) * 2u + hf] = h[i];
             }
         }
     }
@@ -202,8 +266,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
             const float v = pk[k < U ? k : U - 1u];
             acc += k < U ? v : 0.f;
         }
-        const uint32_t r = t * E + r0 + tid;
-        if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + r] + acc;
-        gd_buf<float>(a, a.c[13])[a.c[14] + r] = acc;
+        if (residual) acc = gd_bits_f32(resv) + acc;
+        OUT[orow] = acc;
     }
 }

@@ -28,6 +28,14 @@
 #define GG_ITEMS 2       // (row, block) items per thread
 #define GG_MAX_U 16
 #define GG_MAX_RPG 512   // RPG E / 128 <= 1024 items
+#ifndef GG_PIPELINE
+#define GG_PIPELINE moe_decode_gu_g
+#define GG_GENERIC 0     // 1: any Gyro type per expert and projection, rows from the expert table
+#endif
+// Words loaded per block: TQ2_T's 34 bytes, or the widest type's 58 (whole words from the
+// block's first byte rounded down to a word; the arena's slack covers reads past the last row).
+#define GG_WORDS (GG_GENERIC ? 15 : 9)
+#define GG_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
 
 // Selection rounds 0 .. need of one token (uniform per wave): the ids of ranks ka and kb; when
 // `writer`, every round and the token's ids and renormalised weights (rf_weights) stored by
@@ -77,8 +85,11 @@ __device__ __forceinline__ void gg_route(const float lv[4], uint32_t NE, uint32_
     }
 }
 
-GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
+GG_DEFINE(GG_PIPELINE, 512) {
     __shared__ gd_u32x4 book4[512];
+#if GG_GENERIC
+    __shared__ gd_u32x4 xdesc[2 * 256];  // the expert table: {gate, up}, {down, types, pad} per expert
+#endif
     __shared__ uint4 xh4[2][4096 / 8];  // the run's (up to) two tokens' rotated inputs
     __shared__ float gred[2 * GG_ITEMS * 512];  // (row, projection) block dots
     __shared__ float gsum[2 * GG_MAX_RPG];
@@ -95,7 +106,13 @@ GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
     const uint32_t tw = wave == 0u ? t0 : t1;
     float lv[4];
     if (wave < 2u) rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + tw * NE, NE, lv);
+#if GG_GENERIC
+    const gd_u32x4 xdv = gd_global4(gd_buf<const uint32_t>(a, a.c[22]))[min(tid, 2u * NE - 1u)];
+#endif
     book4[tid] = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
+#if GG_GENERIC
+    if (tid < 2u * NE) xdesc[tid] = xdv;
+#endif
     const uint32_t *XH = gd_buf<const uint32_t>(a, a.c[9]) + a.c[10];
     for (uint32_t q = tid; q < (t1 != t0 ? 2u : 1u) * (E / 8u); q += 512u) {  // uint4 chunks
         const uint32_t ti = q / (E / 8u), c16 = q - ti * (E / 8u), b = c16 >> 4, c = c16 & 15u;
@@ -125,22 +142,43 @@ GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
 
     // Items: row rr of the run and block b (b fastest), the gate and the up block of that row
     // against the same 128 activations: 2 x 9 words from HBM each.
+    const uint32_t n_items = rows * nb;
+#if !GG_GENERIC
     const uint64_t layer_base = (uint64_t)a.c[11] | ((uint64_t)a.c[12] << 32);
     const uint8_t *LB = reinterpret_cast<const uint8_t *>(layer_base);
-    const uint32_t stride = a.c[13], proj_bytes = a.c[14], row_bytes = nb * 34u, n_items = rows * nb;
-    uint32_t dw[GG_ITEMS][2][9];
-    bool odd[GG_ITEMS];
+    const uint32_t stride = a.c[13], proj_bytes = a.c[14], row_bytes = nb * 34u;
+#endif
+    uint32_t dw[GG_ITEMS][2][GG_WORDS];
+    bool odd[GG_ITEMS][2];
+    uint32_t ty[GG_ITEMS][2];
 #pragma unroll
     for (int s = 0; s < GG_ITEMS; ++s) {
         const uint32_t j = tid + 512u * (uint32_t)s;
-        odd[s] = false;
+        odd[s][0] = odd[s][1] = false;
+        ty[s][0] = ty[s][1] = 144u;
         if (j < n_items) {
             const uint32_t rr = j / nb, b = j - rr * nb;
             const uint32_t R = row0 + rr, f = R % F, e = sid[R / F != s0 ? 1 : 0];
+#if GG_GENERIC
+            const gd_u32x4 ptr = xdesc[2u * e], tys = xdesc[2u * e + 1u];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                ty[s][p] = (tys[2] >> (8 * p)) & 0xffu;
+                GyroType gt;
+                gd_type(ty[s][p], gt);  // the host admits only the eight types
+                const uint64_t addr = (((uint64_t)ptr[2 * p + 1] << 32) | ptr[2 * p]) +
+                                      ((uint64_t)f * nb + b) * gt.block_bytes;
+                gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(addr & ~uint64_t(3)));
+#pragma unroll
+                for (int q = 0; q < GG_WORDS; ++q) dw[s][p][q] = w[q];
+                odd[s][p] = (addr & 2u) != 0u;
+            }
+#else
             const uint64_t off = (uint64_t)e * stride + (uint64_t)f * row_bytes + b * 34u;
 #pragma unroll
             for (int p = 0; p < 2; ++p) tq2_load_block(LB, off + (p ? proj_bytes : 0u), dw[s][p]);
-            odd[s] = (off & 2u) != 0u;  // proj_bytes is a multiple of 4
+            odd[s][0] = odd[s][1] = (off & 2u) != 0u;  // proj_bytes is a multiple of 4
+#endif
         }
     }
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
@@ -158,10 +196,24 @@ GD_PIPELINE_NAMED(moe_decode_gu_g, 512) {
             }
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
+                float v = 0.f;
+#if GG_GENERIC
+#define GG_CASE(ID)                                                       \
+    {                                                                     \
+        float sc;                                                         \
+        uint32_t q[gyro_nw<ID>()];                                        \
+        gyro_unpack<ID>(dw[s][p], odd[s][p], sc, q);                      \
+        v = sc * gyro_block_dot_h<ID>(q, book, xs);                       \
+    }
+                GYRO_TYPE_SWITCH(ty[s][p], GG_CASE)
+#undef GG_CASE
+#else
                 float sc;
                 uint32_t q[8];
-                tq2_unpack(dw[s][p], odd[s], sc, q);
-                gred[(2u * rr + (uint32_t)p) * nb + b] = sc * tq2_block_dot_h(q, book, xs);
+                tq2_unpack(dw[s][p], odd[s][p], sc, q);
+                v = sc * tq2_block_dot_h(q, book, xs);
+#endif
+                gred[(2u * rr + (uint32_t)p) * nb + b] = v;
             }
         }
     }

@@ -926,8 +926,9 @@ class Engine {
                               bits(L.norm_eps), 2 * rsf, rsf ? L.sh_gu.srv : 0u, rsf ? B.sh_h : 0u,
                               rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u, flag_uav()},
                              std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
-        if (!decode_generic_types(L)) {
-            if (decode_tuned_tq2()) {
+        const bool generic = decode_generic_types(L);
+        if (!generic || !decode_generic_tuned()) {
+            if (!generic && decode_tuned_tq2()) {
                 dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
                                      {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh,
                                       B.xh_off, base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n},
@@ -943,35 +944,32 @@ class Engine {
             // Other shapes: runs of RPG (token, slot, row) rows per gate/up group (at most 1024
             // (row, block) items) and R output rows per down group (R divides E; at most 1024
             // (slot, block, half, row pair) items and 512 (row, slot) sums), about one group per
-            // CU for a token.
+            // CU for a token. Layers of other types take the same kernels in their type-generic
+            // form (_xg: rows through the expert table, each expert's types).
             const uint32_t nb = E / 128, total = n * U * F, target = cus_or(256);
             const uint32_t rpg = std::max(1u, std::min({(total + target - 1) / target, F, 1024u / nb}));
             uint32_t R = std::max(1u, E / target);
             while (R > 1 && (E % R || U * (F / 128) * 2 * ((R + 1) / 2) > 1024 || R * U > 512)) --R;
-            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_g",
+            const uint32_t xt = generic ? L.xtab.srv : 0u;
+            dispatch_maybe_timed(bracket == 2, marks, generic ? "moe_decode_gu_xg" : "moe_decode_gu_g",
                                  {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh,
-                                  B.xh_off, base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n,
-                                  rpg},
+                                  B.xh_off, generic ? 0u : base_lo, generic ? 0u : base_hi, generic ? 0u : slot_stride,
+                                  generic ? 0u : L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n, rpg, xt},
                                  (total + rpg - 1) / rpg);
-            dispatch_maybe_timed(bracket == 3, marks, U * (F / 128) <= 64 ? "moe_decode_down_g" : "moe_decode_down_gl",
-                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
-                                  2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                                  out_off, E, F, U, n, R, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
+            const char *down = generic ? "moe_decode_down_xg"
+                                       : (U * (F / 128) <= 64 ? "moe_decode_down_g" : "moe_decode_down_gl");
+            dispatch_maybe_timed(bracket == 3, marks, down,
+                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, generic ? 0u : base_lo,
+                                  generic ? 0u : base_hi, generic ? 0u : slot_stride, generic ? 0u : 2 * L.gate_bytes,
+                                  codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, R, NE,
+                                  st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, xt},
                                  E / R, n);
             return;
         }
-        dispatch_maybe_timed(bracket == 2, marks, decode_generic_tuned() ? "moe_decode_gu_x" : "moe_decode_gu_xg",
+        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_x",
                              {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
                               L.xtab.srv, codebook.srv, B.gu, B.gu_off, E, F, n},
                              F / 64, 2 * parts, n * U);
-        if (!decode_generic_tuned()) {
-            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_xg",
-                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
-                                  L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
-                                  st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off},
-                                 E / 8, n);
-            return;
-        }
         dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
                              {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
