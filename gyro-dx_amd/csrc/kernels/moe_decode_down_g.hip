@@ -14,13 +14,17 @@
 //    once and decodes that half of both rows' blocks against them (tq2_half_dot); per (row, k)
 //    the half sums in (block, half) order times w_k, then per row the slots in slot order, then
 //    the residual (every LDS sum reads its operands at once).
+// Load order: the ids, the residual, the slot weights, the codebook and the inputs, then the
+// blocks, every one issued by every lane (a lane past the last item or unit repeats it), so
+// that each wait leaves the loads issued after it in flight.
 // Grid: x = E / R, y = n_tok; 512 threads.
 // Constants: 0 act_uav 1 act_off (act[(t U + k) F + f], from moe_decode_gu_g) 2 ids_uav 3 ids_off
 // 4 weights_uav 5 weights_off 6 base_lo 7 base_hi 8 slot_stride 9 down_off 10 codebook_srv
 // 11 signs_srv (0xffffffff: none) 12 signs_off 13 out_uav 14 out_off 15 E 16 F 17 n_used
-// 18 n_tok 19 R 20 n_expert 21 residual 22 res_uav 23 res_off.
-// Requires TQ2_T experts, F a multiple of 128 up to 1024, 1 <= n_used <= 16, n_used F / 128 <=
-// DG_MAX_ABLK, n_used F / 64 ceil(R / 2) <= 512 DG_ITEMS and R n_used <= 512 (the host checks).
+// 18 n_tok 19 R 20 n_expert 21 residual 22 res_uav 23 res_off (24 xtab_srv: the generic form).
+// Requires TQ2_T experts (any types in the generic form), F a multiple of 128 up to 1024,
+// 1 <= n_used <= 16, n_used F / 128 <= DG_MAX_ABLK, n_used F / 64 ceil(R / 2) <= 512 DG_ITEMS
+// and R n_used <= 512 (the host checks).
 #include "gyro_fast.h"
 #include "fwht.h"
 
@@ -38,13 +42,16 @@
 #define DG_MAX_U 16
 #define DG_MAX_EXPERTS 256
 #define DG_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
-#define DG_BLOCK_STRIDE 132  // floats per 128-block of an input in LDS (bank spread)
+// A rotated 128-block in LDS: half 0 at 0, half 1 at DG_HALF_OFF, blocks DG_BLOCK_STRIDE floats
+// apart. Modulo the 64 banks, blocks are 8 banks apart and halves 4: the dozen (block, half)
+// rows that a wave's items read at one 16-byte step fall in different banks.
+#define DG_BLOCK_STRIDE 136
+#define DG_HALF_OFF 68
 
 DG_DEFINE(DG_PIPELINE, 512) {
     __shared__ gd_u32x4 book4[512];
     __shared__ float actr[DG_MAX_ABLK * DG_BLOCK_STRIDE];
     __shared__ float dred[2 * DG_ITEMS * 512];  // half dots by (slot, row, block, half)
-    __shared__ float kr[512];  // (row, slot) terms
     __shared__ float sw[DG_MAX_U];
 #if DG_GENERIC
     __shared__ gd_u32x4 xdesc[DG_MAX_EXPERTS];  // per expert {down lo, down hi, types, pad}
@@ -76,8 +83,8 @@ DG_DEFINE(DG_PIPELINE, 512) {
     float *OUT = gd_buf<float>(a, a.c[13]) + a.c[14];
     const bool residual = a.c[21] != 0u;
     const float *RES = residual ? gd_buf<const float>(a, a.c[22]) + a.c[23] : OUT;
-    const uint32_t orow = t * E + r0 + min(tid, R - 1u);
-    const uint32_t resv = gd_global(reinterpret_cast<const uint32_t *>(RES))[orow];
+    // Lane k of 16-lane row q stores output row q (see the row sums below).
+    const uint32_t resv = gd_global(reinterpret_cast<const uint32_t *>(RES))[t * E + r0 + min(tid >> 4, R - 1u)];
     // The codebook and weights are stored to LDS only after the block loads are issued (an LDS
     // store of a loaded value waits for every load issued before it; so does the rotation).
     const uint32_t swv = tid < U ? gd_global(gd_buf<const uint32_t>(a, a.c[4]) + a.c[5] + t * U)[tid] : 0u;
@@ -194,7 +201,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] *= GD_INV_SQRT128;
         }
-        float4 *dst = reinterpret_cast<float4 *>(actr + u * DG_BLOCK_STRIDE + l16 * 8u);
+        float4 *dst = reinterpret_cast<float4 *>(actr + u * DG_BLOCK_STRIDE + l16 * 8u + (l16 >= 8u ? DG_HALF_OFF - 64u : 0u));
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
@@ -209,7 +216,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
         if (j < n_items) {
             const uint32_t k = j / PK, rem = j - k * PK, bh = rem / NP, pair = rem - bh * NP;
             const uint32_t bb = bh >> 1, hf = bh & 1u;
-            const float4 *ar = reinterpret_cast<const float4 *>(actr + (k * NB + bb) * DG_BLOCK_STRIDE + 64u * hf);
+            const float4 *ar = reinterpret_cast<const float4 *>(actr + (k * NB + bb) * DG_BLOCK_STRIDE + DG_HALF_OFF * hf);
             float x[64];
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
@@ -244,29 +251,33 @@ DG_DEFINE(DG_PIPELINE, 512) {
         }
     }
     __syncthreads();
-    // (row, slot): w_k times the row's half sums in (block, half) order (2 NB <= 16 loads at once).
-    const uint32_t nbh = 2u * NB;
-    for (uint32_t p = tid; p < R * U; p += 512u) {
-        const uint32_t row = p / U, k = p - row * U;
-        const float *d = dred + (k * R + row) * nbh;
-        float dk = 0.f;
+    // Output rows, 32 at a time: lane k of 16-lane row q holds slot k of output row q, w_k times
+    // the row's half sums in (block, half) order (2 NB <= 16 loads at once); the 16 lanes then
+    // add the slot terms in slot order (one DPP step per slot), and lane U - 1 adds the residual
+    // and stores. No second pass through LDS.
+    const uint32_t nbh = 2u * NB, k16 = tid & 15u;
+    for (uint32_t row = tid >> 4; row < R; row += 32u) {  // uniform per 16-lane row
+        float term = 0.f;
+        if (k16 < U) {
+            const float *d = dred + (k16 * R + row) * nbh;
+            float dk = 0.f;
 #pragma unroll
-        for (uint32_t bh = 0; bh < 16u; ++bh) {
-            const float v = d[bh < nbh ? bh : nbh - 1u];
-            dk += bh < nbh ? v : 0.f;
+            for (uint32_t bh = 0; bh < 16u; ++bh) {
+                const float v = d[bh < nbh ? bh : nbh - 1u];
+                dk += bh < nbh ? v : 0.f;
+            }
+            term = sw[k16] * dk;
         }
-        kr[p] = sw[k] * dk;
-    }
-    __syncthreads();
-    if (tid < R) {  // the output row: slots in slot order, then the residual
-        const float *pk = kr + tid * U;
-        float acc = 0.f;
+        float acc = 0.f + term;
 #pragma unroll
-        for (uint32_t k = 0; k < DG_MAX_U; ++k) {
-            const float v = pk[k < U ? k : U - 1u];
-            acc += k < U ? v : 0.f;
+        for (uint32_t k = 1; k < DG_MAX_U; ++k) {
+            const float prev = gd_dpp_f<0x111>(acc);  // row_shr:1, lane k - 1
+            acc = k16 == k ? prev + term : acc;
         }
-        if (residual) acc = gd_bits_f32(resv) + acc;
-        OUT[orow] = acc;
+        if (k16 == U - 1u) {
+            const uint32_t o = t * E + r0 + row;
+            if (residual) acc = (row < 32u ? gd_bits_f32(resv) : RES[o]) + acc;
+            OUT[o] = acc;
+        }
     }
 }

@@ -18,8 +18,10 @@
 // Grid: ceil(n_tok n_used F / RPG) groups; 512 threads.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used 4 scale (fp32 bits) 5 ids_uav
 // 6 ids_off 7 weights_uav 8 weights_off 9 xh16_uav 10 xh16_off (words) 11 base_lo 12 base_hi
-// 13 slot_stride 14 proj_bytes 15 codebook_srv 16 act_uav 17 act_off 18 E 19 F 20 n_tok 21 RPG.
-// Requires TQ2_T experts, E a multiple of 256 up to 4096, n_expert <= 256, 1 <= n_used <= 16,
+// 13 slot_stride 14 proj_bytes 15 codebook_srv 16 act_uav 17 act_off 18 E 19 F 20 n_tok 21 RPG
+// (22 xtab_srv: the generic form).
+// Requires TQ2_T experts (any types in the generic form), E a multiple of 256 up to 4096,
+// n_expert <= 256, 1 <= n_used <= 16,
 // F a multiple of 128, RPG <= F and RPG E / 128 <= 512 GG_ITEMS (the host checks).
 #include "gyro_fast.h"
 #include "fwht.h"

@@ -112,9 +112,10 @@ def test_prefill_path_generic_types_odd_down_blocks(oracle_mod, type_id, E, F, N
 @pytest.mark.parametrize("type_id,E,F,NE,U", [(148, 2560, 640, 64, 10), (0, 1024, 384, 64, 6),
                                                (151, 1280, 1024, 48, 16)])
 def test_decode_path_generic_types_other_shapes(oracle_mod, type_id, E, F, NE, U):
-    """The general type-generic decode (moe_decode_gu_xg, moe_decode_down_xg): a partial last
-    K-part (hidden 2560 and 1280), odd block counts per down row (F 640, 384), F 1024 and top-k
-    widths 6, 10 and 16, at 1, 3 and 8 tokens."""
+    """The general type-generic decode (moe_decode_gu_xg, moe_decode_down_xg): hidden 2560 and
+    1280, odd block counts per down row (F 640, 384), F 1024, top-k widths 6, 10 and 16, one
+    type or all eight mixed per expert and projection (both half-block stream rotations: word
+    and half-word), at 1, 3 and 8 tokens."""
     from gyrodx.engine import PATH_DECODE
     kw = dict(mixed_types=True) if type_id == 0 else dict(type_id=type_id)
     layer = synth.make_layer(170 + U, E=E, F=F, n_expert=NE, n_used=U, **kw)
