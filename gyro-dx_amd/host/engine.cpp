@@ -299,6 +299,15 @@ class Engine {
     uint32_t cus = 0;
     uint32_t fused_mode = 0;
     uint32_t spin_limit = xch::kSpinLimit;
+    // Router and gate/up in one launch (moe_decode_rgu) for the tuned TQ2_T shapes when the
+    // environment sets GYRO_DECODE_RGU=1 (measured no faster than the three-kernel path on MI355X):
+    // its logit words (8 tokens x 256 experts, 64-bit, 128 bytes apart) and the call epoch, never
+    // 0, that tags them. A wait that gives up stores the sticky error word of xch_area, as
+    // moe_decode_fused does.
+    bool rgu_on = false;
+    uint32_t rgu_epoch = 0;
+    Buffer rgu_area;
+    static constexpr uint32_t kRguTokens = 8, kRguExperts = 256;
     // Prefill GEMMs of uniform TQ2_T layers: one persistent launch over both (moe_prefill_gemm)
     // unless the environment sets GYRO_PREFILL_FUSED=0 (then moe_prefill_gu and moe_prefill_down);
     // the polls a down unit makes for a ready tile before it gives up (GYRO_PREFILL_SPIN_LIMIT,
@@ -454,6 +463,10 @@ class Engine {
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
         fill_zero(xch_area);
+        const char *rg = std::getenv("GYRO_DECODE_RGU");
+        rgu_on = rg && rg[0] == '1';
+        rgu_area = dev.buffer((uint64_t)kRguTokens * kRguExperts * 128u, Kind::device);
+        fill_zero(rgu_area);
     }
 
     // The decode path's own intermediate buffers.
@@ -840,13 +853,32 @@ class Engine {
         return fs;
     }
 
-    // Keeps batch-1 decode on the three-kernel path for its lifetime (a recomputation).
+    // Keeps decode on the three-kernel path (no moe_decode_fused, no moe_decode_rgu) for its
+    // lifetime (a recomputation).
     struct UnfusedScope {
         Engine *e;
         uint32_t was;
-        explicit UnfusedScope(Engine *eng) : e(eng), was(eng->fused_mode) { e->fused_mode = 0; }
-        ~UnfusedScope() { e->fused_mode = was; }
+        bool was_rgu;
+        explicit UnfusedScope(Engine *eng) : e(eng), was(eng->fused_mode), was_rgu(eng->rgu_on) {
+            e->fused_mode = 0;
+            e->rgu_on = false;
+        }
+        ~UnfusedScope() {
+            e->fused_mode = was;
+            e->rgu_on = was_rgu;
+        }
     };
+
+    // moe_decode_rgu takes the tuned TQ2_T shapes (hidden 1024 or 2048, F 512, top-8) without the
+    // fused shared expert, at most 8 tokens of at most 256 experts, when each of its first
+    // P = min(G, n_expert) groups computes at most two router rows; not the no-allocation entry
+    // point (its buffers are the caller's scratch).
+    bool rgu_fits(uint32_t n, const DecodeBufs *bufs) const {
+        if (!rgu_on || bufs || n == 0 || n > kRguTokens || NE > kRguExperts || NE == 0 || (E != 1024 && E != 2048))
+            return false;
+        const uint32_t G = (F / 64) * 2 * parts * n * U, P = std::min(G, NE);
+        return (NE + P - 1) / P <= 2;
+    }
 
     struct UnfusedPrefillScope {
         Engine *e;
@@ -919,6 +951,25 @@ class Engine {
         }
         const uint32_t rsf = fused_sh ? L.SF : 0u;  // shared rows computed inside moe_router
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
+        const bool generic = decode_generic_types(L);
+        if (!generic && decode_tuned_tq2() && rgu_fits(n, bufs)) {
+            // Router, rotation, routing and gate/up in one launch, then the down kernel.
+            rgu_epoch = rgu_epoch + 1u == 0u ? 1u : rgu_epoch + 1u;
+            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_rgu",
+                                 {x_uav, x_off, E, n, L.router.srv, L.has_bias ? L.bias.srv : kNone, NE, E, F,
+                                  L.has_gate_signs ? L.signs.srv : kNone, st.on ? (L.has_norm ? 2u : 1u) : 0u,
+                                  L.has_norm ? L.norm.srv : 0u, bits(L.norm_eps), rgu_area.uav, rgu_epoch, spin_limit,
+                                  B.xch, xch::kCtl + 64, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off,
+                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, flag_uav()},
+                                 F / 64, 2 * parts, n * U);
+            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
+                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
+                                  2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
+                                  out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
+                                  st.res_off},
+                                 E / 8, n);
+            return;
+        }
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
                               B.logits, B.logits_off, L.has_gate_signs ? L.signs.srv : kNone, 0, B.xh, B.xh_off,
@@ -926,7 +977,6 @@ class Engine {
                               bits(L.norm_eps), 2 * rsf, rsf ? L.sh_gu.srv : 0u, rsf ? B.sh_h : 0u,
                               rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u, flag_uav()},
                              std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
-        const bool generic = decode_generic_types(L);
         if (!generic || !decode_generic_tuned()) {
             if (!generic && decode_tuned_tq2()) {
                 dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
@@ -1424,8 +1474,8 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
         *device_ms = dev;
         if (bracket_us) *bracket_us = br_n ? br / (double)br_n : 0.0;
         if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
-            throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
-                                        "this run are invalid (gm_forward recomputes such calls on the three-kernel path)");
+            throw gyro::NativeError(-1, "a decode call in one launch (moe_decode_fused or moe_decode_rgu) gave up waiting for its workgroups: the "
+                                        "outputs of this run are invalid (gm_forward recomputes such calls on the three-kernel path)");
         if (path == GM_PATH_PREFILL && e.take_gemm_error())
             throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
                                         "this run are invalid (gm_forward recomputes such calls with two GEMM launches)");
@@ -1469,8 +1519,8 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
         if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
-            throw gyro::NativeError(-1, "a single-launch decode call gave up waiting for its workgroups: the outputs of "
-                                        "this run are invalid (gm_forward_stack recomputes such calls on the three-kernel path)");
+            throw gyro::NativeError(-1, "a decode call in one launch (moe_decode_fused or moe_decode_rgu) gave up waiting for its workgroups: the "
+                                        "outputs of this run are invalid (gm_forward_stack recomputes such calls on the three-kernel path)");
         if (path == GM_PATH_PREFILL && e.take_gemm_error())
             throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
                                         "this run are invalid (gm_forward_stack recomputes such calls with two GEMM launches)");
