@@ -29,8 +29,10 @@
 // 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used 17 range flag (as moe_prefill_gu)
 // 18 down32_uav 19 down32_off (words) 20 sched_uav (u32: [0] gate/up queue, [1] give-up, [2] down
 // queue, [3] ready count, [64 + t] tile t's finished gate/up units, [64 + tiles + s] ready slot s:
-// tile + 1, 0 while empty) 21 spin limit (polls of a ready slot).
-#include "gemm_units.h"
+// tile + 1, 0 while empty) 21 spin limit (polls of a ready slot) 22 small-tile rows SR (16 or 8:
+// tiles of at most SR rows take the small units of gemm_small.h; 0: none; the host passes
+// gs_rows_for(E) when E and F are multiples of 512).
+#include "gemm_small.h"
 
 __device__ __forceinline__ GuUnitArgs gemm_gu_args(const GdArgs &a) {
     const uint32_t *meta = gd_buf<const uint32_t>(a, a.c[0]);
@@ -69,7 +71,7 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gemm, 512, 4) {
     const uint32_t *meta = gd_buf<const uint32_t>(a, a.c[0]);
     const uint32_t tiles = __builtin_amdgcn_readfirstlane(meta[1023]);
     const uint32_t E = a.c[14], F = a.c[15], nfb = F / 128u, neb = E / 256u;
-    const uint32_t n_gu = tiles * nfb, n_units = n_gu + tiles * neb, limit = a.c[21];
+    const uint32_t n_gu = tiles * nfb, n_units = n_gu + tiles * neb, limit = a.c[21], small = a.c[22];
     // Global (not flat) accesses: a flat atomic still in flight would make the compiler wait for
     // all LDS traffic at every counted LDS wait of the next unit's K loop.
     __attribute__((address_space(1))) uint32_t *sched =
@@ -95,7 +97,11 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gemm, 512, 4) {
         const uint32_t u = take(0);
         if (u >= n_gu) break;  // uniform
         const uint32_t tile = u / nfb, fb = u - tile * nfb;
-        gu_unit<true>(sm, gemm_gu_args(a), tile_list[tile], fb);
+        const uint4 td = tile_list[tile];
+        const uint32_t trows = __builtin_amdgcn_readfirstlane(td.z);
+        if (small == 16u && trows <= 16u) gs_gu_unit<16, true>(sm, gemm_gu_args(a), td, fb);
+        else if (small == 8u && trows <= 8u) gs_gu_unit<8, true>(sm, gemm_gu_args(a), td, fb);
+        else gu_unit<true>(sm, gemm_gu_args(a), td, fb);
         __builtin_amdgcn_s_waitcnt(0);  // this thread's act16 stores acknowledged
         __syncthreads();
         if (tid == 0) {
@@ -131,6 +137,10 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_gemm, 512, 4) {
         const uint32_t r = __builtin_amdgcn_readfirstlane(*unit_word);
         __syncthreads();  // every wave has read the word
         if (r == 0u || r > tiles) continue;  // gave up (the call is marked invalid): skip the unit
-        dn_unit(sm, gemm_dn_args(a), tile_list[r - 1u], eb);
+        const uint4 td = tile_list[r - 1u];
+        const uint32_t trows = __builtin_amdgcn_readfirstlane(td.z);
+        if (small == 16u && trows <= 16u) gs_dn_unit<16>(sm, gemm_dn_args(a), td, eb);
+        else if (small == 8u && trows <= 8u) gs_dn_unit<8>(sm, gemm_dn_args(a), td, eb);
+        else dn_unit(sm, gemm_dn_args(a), td, eb);
     }
 }

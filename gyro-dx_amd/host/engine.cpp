@@ -314,6 +314,13 @@ class Engine {
     // default 2^20); its queue words, give-up word, tile counters and ready list.
     bool prefill_fused = true;
     uint32_t prefill_spin_limit = 1u << 20;
+    // Small-tile units in moe_prefill_gemm (tiles of at most 16 rows, 8 past hidden 2048; hidden
+    // and F multiples of 512) unless the environment sets GYRO_PREFILL_SMALL=0.
+    bool prefill_small = true;
+    uint32_t small_rows() const {
+        if (!prefill_small || E % 512 || F % 512) return 0;
+        return E <= 2048 ? 16u : (E <= 4096 ? 8u : 0u);
+    }
     Buffer gemm_sched;
     static constexpr uint32_t kSchedWords = 64;  // words before the tile counters and the ready list
     std::string error;
@@ -459,6 +466,8 @@ class Engine {
         if (const char *sl = std::getenv("GYRO_DECODE_SPIN_LIMIT")) spin_limit = (uint32_t)std::strtoul(sl, nullptr, 10);
         const char *pf = std::getenv("GYRO_PREFILL_FUSED");
         prefill_fused = !(pf && pf[0] == '0');
+        const char *psm = std::getenv("GYRO_PREFILL_SMALL");
+        prefill_small = !(psm && psm[0] == '0');
         if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
@@ -1075,7 +1084,7 @@ class Engine {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gemm",
                                  {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
                                   codebook.srv, signs, E, act.uav, 0, E, F, U, 1u, down.uav, 0, gemm_sched.uav,
-                                  prefill_spin_limit},
+                                  prefill_spin_limit, small_rows()},
                                  2 * cus_or(256));
         } else if (L.type_id == 144) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",
