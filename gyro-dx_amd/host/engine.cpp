@@ -314,12 +314,19 @@ class Engine {
     // default 2^20); its queue words, give-up word, tile counters and ready list.
     bool prefill_fused = true;
     uint32_t prefill_spin_limit = 1u << 20;
-    // Small-tile units in moe_prefill_gemm (tiles of at most 16 rows, 8 past hidden 2048; hidden
-    // and F multiples of 512) unless the environment sets GYRO_PREFILL_SMALL=0.
-    bool prefill_small = true;
+    // The persistent GEMM with the small-tile units (moe_prefill_gemm_s: tiles of at most 16 rows,
+    // 8 past hidden 2048; hidden and F multiples of 512) for calls whose expert segments average at
+    // most 8 slots (n n_used <= 8 n_expert), where most tiles are small; the small units' code costs
+    // the other units 3-5% (register allocation), so larger calls take moe_prefill_gemm. The
+    // environment's GYRO_PREFILL_SMALL: 0 never, 2 always (where the shape allows), else that rule.
+    uint32_t prefill_small = 1;
     uint32_t small_rows() const {
-        if (!prefill_small || E % 512 || F % 512) return 0;
+        if (E % 512 || F % 512) return 0;
         return E <= 2048 ? 16u : (E <= 4096 ? 8u : 0u);
+    }
+    bool use_small(uint32_t n) const {
+        if (!prefill_small || !small_rows()) return false;
+        return prefill_small == 2 || n * U <= 8 * NE;
     }
     Buffer gemm_sched;
     static constexpr uint32_t kSchedWords = 64;  // words before the tile counters and the ready list
@@ -467,7 +474,7 @@ class Engine {
         const char *pf = std::getenv("GYRO_PREFILL_FUSED");
         prefill_fused = !(pf && pf[0] == '0');
         const char *psm = std::getenv("GYRO_PREFILL_SMALL");
-        prefill_small = !(psm && psm[0] == '0');
+        prefill_small = psm && psm[0] == '0' ? 0u : (psm && psm[0] == '2' ? 2u : 1u);
         if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
@@ -1081,10 +1088,11 @@ class Engine {
                              {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows, fused ? gemm_sched.uav : 0u}, 1);
         if (fused) {
             // Both GEMMs in one persistent launch of two groups per compute unit (bracket 2).
-            dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gemm",
+            const bool small = use_small(n);
+            dispatch_maybe_timed(bracket == 2, marks, small ? "moe_prefill_gemm_s" : "moe_prefill_gemm",
                                  {meta.uav, order.uav, 0, xh.uav, 0, base_lo, base_hi, slot_stride, L.gate_bytes,
                                   codebook.srv, signs, E, act.uav, 0, E, F, U, 1u, down.uav, 0, gemm_sched.uav,
-                                  prefill_spin_limit, small_rows()},
+                                  prefill_spin_limit, small ? small_rows() : 0u},
                                  2 * cus_or(256));
         } else if (L.type_id == 144) {
             dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gu",

@@ -9,6 +9,12 @@ the benchmark, the real model's expert shape (hidden 2560, F 640 with its odd bl
 down row, top-10), the widest hidden (4096, sixteen down units per tile) with top-16, F 384 with
 top-6, and batches of 1 and 33 tokens (one and a few tiles). The forced give-up (a spin limit of
 zero polls) must leave gm_forward's result unchanged: the call is recomputed with two launches.
+
+moe_prefill_gemm_s is the same launch with small-tile units for sort tiles of at most 16 rows (8
+past hidden 2048); the engine takes it when the average expert segment is short (tokens x top-k
+at most 8 x experts) and the shape has them (hidden and F multiples of 512, hidden at most 4096).
+Forced on for every call, it must give the bits of moe_prefill_gemm and of the two launches, on
+shapes where tiles of 1 to 16 rows are common and where the large tiles of a Zipf router mix in.
 """
 import os
 
@@ -22,9 +28,13 @@ pytestmark = pytest.mark.gpu
 REL_RMS, COSINE = 2e-3, 0.9999
 
 
-def make_engine(max_tok, fused, spin_limit=None):
-    saved = {k: os.environ.get(k) for k in ("GYRO_PREFILL_FUSED", "GYRO_PREFILL_SPIN_LIMIT")}
+def make_engine(max_tok, fused, spin_limit=None, small=None):
+    """small: GYRO_PREFILL_SMALL ('0' never moe_prefill_gemm_s, '2' always where the shape has
+    small units, None the engine's own choice)."""
+    saved = {k: os.environ.get(k) for k in ("GYRO_PREFILL_FUSED", "GYRO_PREFILL_SPIN_LIMIT", "GYRO_PREFILL_SMALL")}
     os.environ["GYRO_PREFILL_FUSED"] = "1" if fused else "0"
+    if small is not None:
+        os.environ["GYRO_PREFILL_SMALL"] = small
     if spin_limit is not None:
         os.environ["GYRO_PREFILL_SPIN_LIMIT"] = str(spin_limit)
     try:
@@ -102,3 +112,40 @@ def test_persistent_gemm_give_up_recomputes():
         # The give-up word is cleared: a call with a normal limit on a fresh engine is clean.
     finally:
         eng.close()
+
+
+SMALL_SHAPES = [
+    # E, F, experts, top-k, tokens, extra make_layer arguments
+    (2048, 512, 256, 8, 128, {}),
+    (2048, 512, 256, 8, 256, {"zipf": 1.1}),
+    (1024, 512, 64, 4, 37, {}),
+    (4096, 512, 64, 8, 100, {}),
+    (3072, 1024, 32, 6, 1, {"signs": False}),
+]
+
+
+@pytest.mark.parametrize("E,F,NE,U,n,kw", SMALL_SHAPES,
+                         ids=[f"E{s[0]}-F{s[1]}-x{s[2]}-top{s[3]}-n{s[4]}" + "".join(f"-{k}" for k in s[5]) for s in SMALL_SHAPES])
+def test_small_units_match(oracle_mod, E, F, NE, U, n, kw):
+    L = synth.make_layer(1600 + E // 128 + F // 64 + U, E=E, F=F, n_expert=NE, n_used=U, **kw)
+    x = synth.make_tokens(1601 + n, n, E, bf16=True)
+    outs = {}
+    for name, fused, small in (("moe_prefill_gemm_s", True, "2"), ("moe_prefill_gemm", True, "0"),
+                               ("two launches", False, "0")):
+        eng = make_engine(max(n, 64), fused, small=small)
+        try:
+            eng.add_layer(L)
+            print(f"prefill E={E} F={F} experts={NE} top-{U} n={n} {name}", flush=True)
+            outs[name] = eng.forward(0, x, PATH_PREFILL)
+            if name == "moe_prefill_gemm_s":
+                rows = [t[2] for t in eng.last_tiles()]
+                print(f"  {len(rows)} tiles, {sum(r <= (16 if E <= 2048 else 8) for r in rows)} small", flush=True)
+        finally:
+            eng.close()
+    for name in ("moe_prefill_gemm", "two launches"):
+        np.testing.assert_array_equal(outs["moe_prefill_gemm_s"].view(np.uint32), outs[name].view(np.uint32),
+                                      err_msg=name)
+    ref = oracle_mod.OracleLayer(L).forward(x)
+    r, c = oracle_mod.rel_rms(ref, outs["moe_prefill_gemm_s"]), oracle_mod.cosine(ref, outs["moe_prefill_gemm_s"])
+    print(f"  bit-equal; rel_rms {r:.3e} cosine {c:.8f}", flush=True)
+    assert r <= REL_RMS and c >= COSINE

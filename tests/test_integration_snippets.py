@@ -96,7 +96,7 @@ PREFILL = ("moe_prefill_router", "moe_prefill_topk", "moe_prefill_sort", "moe_pr
            "moe_prefill_combine")
 PREFILL_X = ("moe_prefill_gu_x", "moe_prefill_down_x")
 PREFILL_SH = ("moe_prefill_router", "moe_prefill_shared", "moe_prefill_shared", "moe_prefill_combine")
-PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm")
+PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm", "moe_prefill_gemm_s")
 
 
 def sequence(kind: str, ns):
@@ -115,8 +115,9 @@ def sequence(kind: str, ns):
     if kind == "decode_xg":
         return [block(*DECODE_TQ2)[0], *block(*DECODE_XG)]
     p = block(*PREFILL)
-    if kind == "prefill_gemm":  # the sort with the queue buffer and both GEMMs in one launch
-        return [*p[:2], *block(*PREFILL_ONE), p[5]]
+    if kind in ("prefill_gemm", "prefill_gemm_s"):  # the sort with the queue buffer, both GEMMs in one launch
+        sort, gemm, gemm_s = block(*PREFILL_ONE)
+        return [*p[:2], sort, gemm_s if kind == "prefill_gemm_s" else gemm, p[5]]
     mid = block(*PREFILL_X) if ns.mixed else p[3:5]
     if ns.SF:
         sh = block(*PREFILL_SH)
@@ -144,6 +145,8 @@ CASES = [
     ("prefill", 1024, 256, 16, 4, 30, {"mixed_types": True, "SF": 128, "signs": False}),
     ("prefill_gemm", 1024, 512, 64, 8, 100, {}),
     ("prefill_gemm", 2560, 640, 64, 10, 70, {"zipf": 1.1}),
+    ("prefill_gemm_s", 2048, 512, 256, 8, 40, {}),
+    ("prefill_gemm_s", 4096, 1024, 64, 6, 9, {"signs": False}),
 ]
 IDS = [f"{c[0]}-E{c[1]}-F{c[2]}-x{c[3]}-top{c[4]}-n{c[5]}" + "".join(f"-{k}" for k in c[6]) for c in CASES]
 
@@ -215,6 +218,7 @@ def names(L, n: int, cus: int, buffer):
     ns.S = S
     ns.tiles = -(-n * U // 128) + min(NE, n * U)
     ns.cus = cus
+    ns.small_rows = 0 if E % 512 or F % 512 else (16 if E <= 2048 else (8 if E <= 4096 else 0))
     # Call buffers, each sized for nt >= n tokens (whole 64-token tiles and one more) so that no
     # kernel's tile rounding can reach past a buffer.
     nt = -(-n // 64) * 64 + 64
