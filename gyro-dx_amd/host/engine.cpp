@@ -281,6 +281,12 @@ struct StackStep {
     uint32_t res_uav = kNone, res_off = 0;
 };
 
+// The next layer's RMSNorm, computed by the prefill combine of a stack (moe_prefill_combine_norm):
+// its weight (kNone: none) and eps; the normalised rows go to the engine's `hn`.
+struct NormNext {
+    uint32_t w_srv = kNone, eps_bits = 0;
+};
+
 class Engine {
   public:
     Device dev;
@@ -320,6 +326,9 @@ class Engine {
     // the other units 3-5% (register allocation), so larger calls take moe_prefill_gemm. The
     // environment's GYRO_PREFILL_SMALL: 0 never, 2 always (where the shape allows), else that rule.
     uint32_t prefill_small = 1;
+    // Stack prefill: the combine also computes the next layer's RMSNorm (environment's
+    // GYRO_STACK_NORM_FUSED=0: moe_stack_norm before every layer instead).
+    bool stack_norm_fused = true;
     uint32_t small_rows() const {
         if (E % 512 || F % 512) return 0;
         return E <= 2048 ? 16u : (E <= 4096 ? 8u : 0u);
@@ -475,6 +484,8 @@ class Engine {
         prefill_fused = !(pf && pf[0] == '0');
         const char *psm = std::getenv("GYRO_PREFILL_SMALL");
         prefill_small = psm && psm[0] == '0' ? 0u : (psm && psm[0] == '2' ? 2u : 1u);
+        const char *snf = std::getenv("GYRO_STACK_NORM_FUSED");
+        stack_norm_fused = !(snf && snf[0] == '0');
         if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
@@ -1060,7 +1071,7 @@ class Engine {
     // persistent launch), 4 top-k, 5 sort, 6 combine, 7 shared gate/up, 8 shared down.
     void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                      int bracket = 0, std::vector<uint32_t> *marks = nullptr, uint32_t res_uav = kNone,
-                     uint32_t res_off = 0) {
+                     uint32_t res_off = 0, const NormNext *norm_next = nullptr) {
         const Layer &L = layers.at(il);
         if (!prefill_supported(L))
             throw NativeError(-1, "prefill path needs E a multiple of 256, F a multiple of 128 and at least 256, top-1 to top-16 of <= 256 experts, a shared expert (if "
@@ -1125,6 +1136,15 @@ class Engine {
                                   bits(L.sh_unscale[2]), 0, E},
                                  E / 128, tt);
         }
+        if (norm_next) {
+            if (E > 4096) throw NativeError(-1, "the fused stack norm covers E <= 4096");
+            dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine_norm",
+                                 {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u,
+                                  res_uav, res_off, L.SF ? 1u : 0u, L.SF ? sh_o.uav : 0u, 0, x_uav, x_off,
+                                  L.SF ? L.sh_gate.srv : 0u, norm_next->w_srv, hn.uav, 0, norm_next->eps_bits},
+                                 n);
+            return;
+        }
         dispatch_maybe_timed(bracket == 6, marks, "moe_prefill_combine",
                              {down.uav, 0, weights.uav, 0, out_uav, out_off, E, U, res_uav != kNone ? 1u : 0u, res_uav,
                               res_off, L.SF ? 1u : 0u, L.SF ? sh_o.uav : 0u, 0, x_uav, x_off,
@@ -1151,12 +1171,15 @@ class Engine {
     // (y_uav, y_off); y may be x. Per layer l, with s the stream (x before the first layer, y
     // after): y = s + MoE_l(RMSNorm_l(s)).
     //   decode:    the router normalises s itself and the down kernel adds s (three launches);
-    //   prefill:   moe_stack_norm writes RMSNorm_l(s) to hn, the combine adds s;
+    //   prefill:   moe_stack_norm writes RMSNorm_l(s) to hn, the combine adds s and (unless
+    //              stack_norm_fused is off) writes RMSNorm_{l+1} of the new stream to hn, so
+    //              only the first layer runs moe_stack_norm;
     //   others:    moe_stack_norm also adds the previous layer's output (in `out`) to the stream
     //              and writes it to y; the path writes `out`; ew adds the last one.
     void stack(const uint32_t *list, uint32_t n_layers, uint32_t path, uint32_t n, uint32_t x_uav, uint32_t x_off,
                uint32_t y_uav, uint32_t y_off) {
         if (E > 4096) throw NativeError(-1, "stack RMSNorm covers E <= 4096");
+        bool normed = false;  // hn already holds this layer's normalised input
         for (uint32_t l = 0; l < n_layers; ++l) {
             const Layer &L = layers.at(list[l]);
             const bool first = l == 0;
@@ -1177,9 +1200,18 @@ class Engine {
                 st.res_off = s_off;
                 ffn_decode(list[l], n, hn.uav, 0, y_uav, y_off, 0, nullptr, st);
             } else if (path == GM_PATH_PREFILL) {
-                dispatch("moe_stack_norm",
-                         {s_uav, s_off, kNone, 0, w_srv, 0, hn.uav, 0, E, bits(L.norm_eps), kNone, 0}, n);
-                ffn_prefill(list[l], n, hn.uav, 0, y_uav, y_off, 0, nullptr, s_uav, s_off);
+                if (!normed)
+                    dispatch("moe_stack_norm",
+                             {s_uav, s_off, kNone, 0, w_srv, 0, hn.uav, 0, E, bits(L.norm_eps), kNone, 0}, n);
+                NormNext nn;
+                const bool fuse = stack_norm_fused && l + 1 < n_layers;
+                if (fuse) {
+                    const Layer &N = layers.at(list[l + 1]);
+                    nn.w_srv = N.has_norm ? N.norm.srv : kNone;
+                    nn.eps_bits = bits(N.norm_eps);
+                }
+                ffn_prefill(list[l], n, hn.uav, 0, y_uav, y_off, 0, nullptr, s_uav, s_off, fuse ? &nn : nullptr);
+                normed = fuse;
             } else {
                 dispatch("moe_stack_norm", {s_uav, s_off, first ? kNone : out.uav, 0, w_srv, 0, hn.uav, 0, E,
                                             bits(L.norm_eps), y_uav, y_off},

@@ -155,3 +155,45 @@ def test_stack_rejects_bad_layer_list():
             eng.forward_stack([], x, PATH_REFERENCE)
     finally:
         eng.close()
+
+
+STACK_NORM_CASES = [
+    # layers, E, F, experts, top-k, tokens, make_stack extras, layer without a norm weight
+    (4, 2048, 512, 256, 8, 64, {}, 2),
+    (3, 4096, 256, 32, 4, 33, {}, None),
+    (3, 1024, 512, 64, 8, 40, {"SF": 256}, 1),
+    (2, 2560, 640, 64, 10, 17, {}, None),
+]
+
+
+@pytest.mark.parametrize("nl,E,F,NE,U,n,kw,bare", STACK_NORM_CASES,
+                         ids=[f"{c[0]}x-E{c[1]}-F{c[2]}-x{c[3]}-top{c[4]}-n{c[5]}" + "".join(f"-{k}" for k in c[6])
+                              for c in STACK_NORM_CASES])
+def test_stack_prefill_fused_norm(oracle_mod, monkeypatch, nl, E, F, NE, U, n, kw, bare):
+    """On the prefill path every layer's combine but the last also writes the next layer's
+    RMSNorm (moe_prefill_combine_norm), so only the first layer runs moe_stack_norm. The final
+    stream must equal, bit for bit, the one of an engine created with GYRO_STACK_NORM_FUSED=0
+    (moe_stack_norm before every layer), with a bf16 shared expert (its gate dot reads the
+    normalised rows the kernel overwrites), a layer without a norm weight and hidden sizes up to
+    4096; gm_run_stack equals gm_forward_stack; the stream is within the oracle's bar."""
+    layers = synth.make_stack(4860 + E // 256 + n, nl, E=E, F=F, n_expert=NE, n_used=U, **kw)
+    if bare is not None:
+        layers[bare].norm_weight = None
+    x = synth.make_tokens(4861 + n, n, E)
+    outs = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("GYRO_STACK_NORM_FUSED", fused)
+        eng, ids = make_engine(layers, n)
+        try:
+            print(f"prefill stack {nl} layers E={E} F={F} experts={NE} top-{U} n={n} {kw} fused norm {fused}",
+                  flush=True)
+            outs[fused] = eng.forward_stack(ids, x, PATH_PREFILL)
+            if fused == "1":
+                eng.set_tokens(x)
+                eng.run_stack(PATH_PREFILL, n, 1, ids)
+                np.testing.assert_array_equal(eng.read_outputs(n).view(np.uint32), outs[fused].view(np.uint32))
+        finally:
+            eng.close()
+    np.testing.assert_array_equal(outs["1"].view(np.uint32), outs["0"].view(np.uint32))
+    ref, clear = oracle_stack(oracle_mod, layers, x)
+    check(oracle_mod, f"fused-norm prefill stack E={E}", ref, outs["1"], clear, min_clear=0.3)
