@@ -18,11 +18,23 @@ GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
     const float *lg = gd_buf<const float>(a, a.c[0]) + a.c[1] + (size_t)t * NE;
     float v[4];
     rf_load<4>(lg, NE, v);
-    for (uint32_t z = 1; z < S; ++z) {
-        float p[4];
-        rf_load<4>(lg + (size_t)z * a.c[10], NE, p);
+    // Planes 1 .. 15 (the router's K split is at most 16): every load issued before the first
+    // add, then the sum in plane order.
+    float p[15][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] += p[j];
+    for (int z = 1; z < 16; ++z)
+        if ((uint32_t)z < S) rf_load<4>(lg + (size_t)z * a.c[10], NE, p[z - 1]);
+#pragma unroll
+    for (int z = 1; z < 16; ++z)
+        if ((uint32_t)z < S) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] += p[z - 1][j];
+        }
+    for (uint32_t z = 16; z < S; ++z) {
+        float q[4];
+        rf_load<4>(lg + (size_t)z * a.c[10], NE, q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] += q[j];
     }
     const uint32_t U = a.c[11] ? a.c[11] : 8u;  // uniform, <= 16
     uint32_t ids[16];
