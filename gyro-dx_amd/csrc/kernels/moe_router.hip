@@ -155,6 +155,16 @@ GD_PIPELINE_NAMED(moe_router, 256) {
                 }
             }
         const uint32_t *XU = reinterpret_cast<const uint32_t *>(X) + x_off + tid * 4u;
+        // Every token's inputs are loaded before the first token's sums, so the tokens' load
+        // latencies overlap instead of following one another.
+        float4 xt[ROUTER_MAX_TOK][PER];
+#pragma unroll
+        for (int t = 0; t < ROUTER_MAX_TOK; ++t)
+            if ((uint32_t)t < n_tok) {
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    if (tid * 4u + 1024u * j < E) xt[t][j] = rt_f4(*gd_global4(XU + t * x_stride + 1024u * j));
+            }
 #pragma unroll
         for (int t = 0; t < ROUTER_MAX_TOK; ++t) {
             if ((uint32_t)t < n_tok) {
@@ -162,7 +172,7 @@ GD_PIPELINE_NAMED(moe_router, 256) {
 #pragma unroll
                 for (int j = 0; j < PER; ++j)
                     if (tid * 4u + 1024u * j < E) {
-                        const float4 v = rt_f4(*gd_global4(XU + t * x_stride + 1024u * j));
+                        const float4 v = xt[t][j];
                         if (dot) acc += (w[j].x * v.x + w[j].y * v.y) + (w[j].z * v.z + w[j].w * v.w);
                         if (norm) ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
                     }
