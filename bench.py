@@ -14,10 +14,6 @@ Reported beside the throughput:
                 2 x 278,528 packed bytes per launch) timed by its own dispatch start and end
                 (gd_dispatch_timed) over a second timed pass; HBM traffic per launch from the
                 committed rocprofv3 counter summary when present.
-  single_launch_path  the same tokens on moe_decode_fused, the whole batch-1 layer in one launch
-                (an engine created with GYRO_DECODE_FUSED=2; 8,798,208 bytes per launch: the fp32
-                router matrix, 8 experts x 3 x 278,528 packed bytes, the input and output rows),
-                with its dispatch time. It is slower than the three-kernel path on MI355X.
   cpu_baseline  the CPU oracle (a C restatement of src/engine.zig ffn and its thread pool) on a
                 bounded sample of the same tokens, on this host's cores.
   parity        rel-RMS and cosine of the GPU outputs against that CPU sample.
@@ -61,8 +57,6 @@ PROJ_BYTES = F * (E // 128) * 34  # 278,528 packed bytes per expert projection
 EXPERT_BYTES_PER_TOKEN = TOP_K * 3 * PROJ_BYTES  # 6,684,672
 GU_BYTES_PER_LAUNCH = TOP_K * 2 * PROJ_BYTES  # 4,456,448
 ROUTER_BYTES = N_EXPERT * E * 4  # fp32 router matrix read per layer and step
-# moe_decode_fused per launch: router matrix, routed experts, input and output rows.
-FUSED_BYTES_PER_LAUNCH = ROUTER_BYTES + EXPERT_BYTES_PER_TOKEN + 2 * E * 4  # 8,798,208
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
 GEMM_COUNTERS_FILE = ROOT / "profiles" / "moe_prefill_gemm_counters.md"
 # How the synthetic expert blocks are drawn (gyrodx.synth.random_blocks): trellis stream bytes
@@ -77,44 +71,8 @@ BUNDLE_BYTES = 3 * PROJ_BYTES                                   # 835,584 per ex
 COPY_WORDS = 8 << 20  # calibration copy of the traffic probe: 32 MiB read, 32 MiB written
 
 
-def decode_engine(mode: str, max_tok: int):
-    """An engine whose batch-1 decode mode is `mode` (GYRO_DECODE_FUSED, read when the engine is
-    created: "2" the single-launch kernel or an error, "0" the three-kernel path)."""
-    from gyrodx.engine import Engine
-    saved = os.environ.get("GYRO_DECODE_FUSED")
-    os.environ["GYRO_DECODE_FUSED"] = mode
-    try:
-        return Engine(max_tok=max_tok)
-    finally:
-        if saved is None:
-            os.environ.pop("GYRO_DECODE_FUSED", None)
-        else:
-            os.environ["GYRO_DECODE_FUSED"] = saved
-
-
-def single_launch_decode(layer, tokens, gpu_out, args):
-    """The timed decode steps again in one moe_decode_fused launch per token, with its dispatch
-    time and its outputs' relative RMS distance from the three-kernel path's."""
-    from gyrodx.engine import PATH_DECODE
-    eng = decode_engine("2", 1)
-    layers = [eng.add_layer(layer) for _ in range(args.copies)]
-    eng.set_tokens(tokens)
-    eng.run(PATH_DECODE, 1, args.warmup, layers, first=0)
-    _, wall_ms, _ = eng.run(PATH_DECODE, 1, args.steps, layers, first=args.warmup)
-    out = eng.read_outputs(args.warmup + args.steps)[args.warmup:]
-    _, _, us = eng.run(PATH_DECODE, 1, args.steps, layers, bracket=2, first=args.warmup)
-    eng.close()
-    gbs = FUSED_BYTES_PER_LAUNCH / (us * 1e-6) / 1e9
-    return {"kernel": "moe_decode_fused", "tok_s": round(args.steps / (wall_ms / 1e3), 1),
-            "ms_per_step": round(wall_ms / args.steps, 5), "kernel_us": round(us, 3),
-            "bytes_per_launch": FUSED_BYTES_PER_LAUNCH, "achieved_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "rel_rms_vs_three_kernel_path": float(np.sqrt(np.mean((out.astype(np.float64) - gpu_out) ** 2) /
-                                                          np.mean(gpu_out.astype(np.float64) ** 2)))}
-
-
 def read_traffic():
-    """HBM bytes per moe_decode_fused launch from the committed counter summary (its
+    """HBM bytes per moe_decode_gu launch from the committed counter summary (its
     `bytes_per_launch:` line), or None when no summary is present."""
     if not TRAFFIC_FILE.exists():
         return None
@@ -481,8 +439,8 @@ def coder_decode_kernels(layer, ids_of, x, steps, eng, names):
 
 def coder_bench(args):
     """The real model's routed-expert shape (hidden 2560, 256 experts, top-10, F 640) in TQ2_T
-    (batch-1 decode on moe_router / moe_decode_gu_g / moe_decode_down_g; the single launch
-    moe_decode_fused beside it) and in a 64-step type, GGUF 148 (decode on moe_router /
+    (batch-1 decode on moe_router / moe_decode_gu_g / moe_decode_down_g) and in a 64-step type,
+    GGUF 148 (decode on moe_router /
     moe_decode_gu_xg / moe_decode_down_xg): batch-1 decode over cycled layer copies, a
     1024-token prefill, per-kernel times, and parity of 16 decode tokens with the oracle."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -494,7 +452,7 @@ def coder_bench(args):
     out = {}
     for type_id in (144, 148):
         layer = synth.make_layer(args.seed + type_id, E=cE, F=cF, n_expert=cNE, n_used=cU, type_id=type_id)
-        eng = decode_engine("0", PREFILL_TOKENS)
+        eng = Engine(max_tok=PREFILL_TOKENS)
         ids = [eng.add_layer(layer) for _ in range(args.copies)]
         steps = args.mixed_steps
         x = synth.make_tokens(args.seed + type_id + 1, steps + 16, E=cE)
@@ -505,16 +463,6 @@ def coder_bench(args):
         suffix = "g" if type_id == 144 else "xg"
         kus = coder_decode_kernels(layer, ids, x, steps, eng, (("moe_router", 1), (f"moe_decode_gu_{suffix}", 2),
                                                                 (f"moe_decode_down_{suffix}", 3)))
-        single = None
-        if type_id == 144:
-            one = decode_engine("2", 1)
-            oids = [one.add_layer(layer) for _ in range(args.copies)]
-            one.set_tokens(x)
-            one.run(PATH_DECODE, 1, 16, oids, first=0)
-            _, owall, _ = one.run(PATH_DECODE, 1, steps, oids, first=16)
-            ok = coder_decode_kernels(layer, oids, x, steps, one, (("moe_decode_fused", 2),))
-            one.close()
-            single = {"us_per_token": round(owall / steps * 1e3, 2), "kernel_us": ok}
         expert_bytes = []
         for t in range(32):
             eng.forward(ids[0], x[16 + t:17 + t], PATH_DECODE)
@@ -526,8 +474,6 @@ def coder_bench(args):
                           "kernel_us": kus, "bytes_per_token": int(per_tok),
                           "hbm_gbs": round(per_tok / step_s / 1e9, 1),
                           "roofline": {"bound": "hbm", "frac": round(per_tok / step_s / 1e9 / HBM_PEAK_GBS, 4)}}}
-        if single:
-            rec["decode"]["single_launch_path"] = single
         calls = 8
         xp = synth.make_tokens(args.seed + type_id + 2, PREFILL_TOKENS * calls, E=cE, bf16=True)
         eng.set_tokens(xp)
@@ -606,7 +552,7 @@ def main() -> int:
         return 0
     n_tok = args.warmup + args.steps
     tokens = synth.make_tokens(args.seed + 1, n_tok)
-    eng = decode_engine("0", PREFILL_TOKENS)  # batch 1 on the three-kernel path
+    eng = Engine(max_tok=PREFILL_TOKENS)
     layers = [eng.add_layer(layer) for _ in range(args.copies)]
     eng.set_tokens(tokens)
 
@@ -642,7 +588,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "tq2_t weights, fp16 activations (gate/up) / fp32 (down), fp32 accumulate",
+        "dtype": "tq2_t weights (fp32 block scale x fp32 codebook value), fp32 activations, fp32 accumulate",
         "data": "synthetic (seeded TQ2_T bytes, N(0,0.02) router, N(0,1) tokens)",
         "config": {"workload": "single MoE layer, batch-1 decode", "hidden": E, "experts": N_EXPERT,
                    "top_k": TOP_K, "ffn": F, "expert_type": "TQ2_T (GGUF 144)", "tokens": args.steps,
@@ -655,7 +601,6 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": GU_BYTES_PER_LAUNCH},
     }
-    line["single_launch_path"] = single_launch_decode(layer, tokens, gpu_out, args)
     if not args.no_cpu:
         line["cpu_baseline"], line["parity"] = cpu_baseline(layer, tokens[args.warmup:], gpu_out, args.cpu_budget,
                                                             args.seed)

@@ -137,6 +137,22 @@ __device__ __forceinline__ float tq2_block_dot_h(const uint32_t q[8], const uint
     return acc0 + acc1;
 }
 
+// Rotated fp32 activations staged in LDS as 16-byte chunks, chunk c of 128-block bx at
+// bx * 32 + (c + bx) % 32: the eight blocks that a wave's lanes read at one chunk index then sit
+// in eight different bank groups. x32_stage_index gives the position of chunk c of block bx;
+// x32_from_lds copies block b's 128 values into registers (x[i] = activation i of the block).
+__device__ __forceinline__ uint32_t x32_stage_index(uint32_t bx, uint32_t c) { return bx * 32u + ((c + bx) & 31u); }
+__device__ __forceinline__ void x32_from_lds(const uint4 *xl, uint32_t b, float x[128]) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint4 v = xl[x32_stage_index(b, (uint32_t)j)];
+        x[4 * j] = gd_bits_f32(v.x);
+        x[4 * j + 1] = gd_bits_f32(v.y);
+        x[4 * j + 2] = gd_bits_f32(v.z);
+        x[4 * j + 3] = gd_bits_f32(v.w);
+    }
+}
+
 // The 9 words from the 4-byte-aligned start of the 34-byte block at byte `off` (even) of `base`.
 __device__ __forceinline__ void tq2_load_block(const uint8_t *base, uint64_t off, uint32_t d[9]) {
     gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(base + (off & ~uint64_t(3))));

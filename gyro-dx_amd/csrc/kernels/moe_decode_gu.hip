@@ -3,17 +3,18 @@
 // Every wave computes the token's top-8 from the router logits (route_fast.h), so no separate
 // routing launch exists. A group of eight waves owns 64 rows of one projection (gate or up) of
 // one selected expert over one K-part of 8 Gyro blocks (1024 columns); lane l of wave w decodes
-// block l % 8 of row 8 w + l / 8 (32 trellis steps, two v_dot2_f32_f16 per step, codebook pairs
-// from LDS) and the 8-lane groups add their blocks with DPP ((b0 + b1) + (b2 + b3)) +
-// ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook and the
-// part's 1024 binary16 activations (both into LDS, one barrier, then each lane keeps its block's
-// 128 activations in registers). Once routing names the expert, every lane loads the 9 words of
-// its own block straight from HBM, so no further barrier is needed.
+// block l % 8 of row 8 w + l / 8 (32 trellis steps, two codebook pairs per step gathered
+// from LDS, four v_fma_mix_f32 per step: fp32(codebook) x fp32 activation, accumulated in fp32 as
+// src/kernels.zig:161-183 does) and the 8-lane groups add their blocks with DPP ((b0 + b1) +
+// (b2 + b3)) + ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook
+// and the part's 1024 fp32 activations (both into LDS, one barrier, then each lane keeps its
+// block's 128 activations in registers). Once routing names the expert, every lane loads the 9
+// words of its own block straight from HBM, so no further barrier is needed.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 weights_uav 8 weights_off 9 xh16_uav 10 xh16_off (words) 11 base_lo 12 base_hi
+// 6 ids_off 7 weights_uav 8 weights_off 9 xh_uav (fp32 [n_tok][E]) 10 xh_off (words) 11 base_lo 12 base_hi
 // 13 slot_stride 14 proj_bytes 15 codebook_srv 16 gu_uav 17 gu_off 18 E 19 F 20 n_tok.
 // Requires TQ2_T experts, E a multiple of 1024, n_expert <= 256, top-8 and F a multiple of 64.
 #include "gyro_fast.h"
@@ -25,7 +26,7 @@
 
 GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint4 xpart[128];  // the part's 1024 activations as binary16 pairs
+    __shared__ uint4 xpart[256];  // the part's 1024 fp32 activations (x32_stage_index order)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[18], F = a.c[19], n_tok = a.c[20];
     const uint32_t slot = blockIdx.z, t = slot / GU_U, k = slot - t * GU_U;
@@ -37,19 +38,17 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
     const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
-    const uint32_t xw = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + part * 512u)[tid];
+    // Thread tid stages words 2 tid, 2 tid + 1 of the part: half (tid & 1) of chunk (tid >> 1) % 32
+    // of block tid / 64.
+    gd_guint *xg = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * E + part * 1024u + 2u * tid);
+    const uint32_t xw0 = xg[0], xw1 = xg[1];
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    // Chunk c (16 bytes) of block bx at position bx * 16 + (c + bx) % 16: the 8 blocks that a
-    // wave reads at one chunk index sit in 8 different bank groups.
-    const uint32_t bx = tid >> 6, cx = (tid >> 2) & 15u;
-    reinterpret_cast<uint32_t *>(xpart)[(bx * 16u + ((cx + bx) & 15u)) * 4u + (tid & 3u)] = xw;
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    xst[0] = xw0;
+    xst[1] = xw1;
     __syncthreads();
-    uint32_t xs[64];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint4 v = xpart[b * 16u + ((j + b) & 15u)];
-        xs[4 * j] = v.x; xs[4 * j + 1] = v.y; xs[4 * j + 2] = v.z; xs[4 * j + 3] = v.w;
-    }
+    float xf[128];
+    x32_from_lds(xpart, b, xf);
 
     // Routing: this group needs the expert of rank k only, so it stops after round k; the one
     // group that records the token's ids and weights runs all rounds and forms the weights once
@@ -96,7 +95,7 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     float sc;
     uint32_t q[8];
     tq2_unpack(d, (b & 1u) != 0u, sc, q);
-    float v = sc * tq2_block_dot_h(q, reinterpret_cast<const uint32_t *>(book4), xs);
+    float v = sc * tq2_block_dot(q, reinterpret_cast<const uint32_t *>(book4), xf);
     v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
     v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2
     v = v + gd_dpp_f<0x104>(v);  // row_shl:4: + lane + 4 (read by lanes b < 4)

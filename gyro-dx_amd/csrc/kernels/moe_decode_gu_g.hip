@@ -6,18 +6,19 @@
 // rows, one run per group, so one launch round covers a token on the whole GPU whatever the
 // shape (RPG <= F: a run touches at most two slots and two tokens).
 //  - Independent loads first: each token's logits, the codebook and each token's rotated input
-//    (binary16, staged in LDS with block b's 16-byte chunk c at b * 16 + (c + b) % 16).
+//    (fp32, staged in LDS with block b's 16-byte chunk c at b * 32 + (c + b) % 32).
 //  - Routing (route_fast.h, unrolled rounds): wave 0 selects the first token's experts up to the
 //    last rank the run needs, wave 1 the second token's; a group whose run holds a token's first
 //    row runs all rounds for that token and stores its ids and weights.
 //  - Item (row, block), up to GG_ITEMS per thread: the row's gate and up blocks, each loaded
-//    straight from HBM (9 words each) and decoded against the block's 128 activations, read once
-//    from LDS for both (tq2_block_dot_h); each row's gate and up sums in block order through LDS.
+//    straight from HBM (9 words each) and decoded against the block's 128 fp32 activations, read
+//    once from LDS for both (tq2_block_dot: fp32(codebook) x activation accumulated in fp32, as
+//    src/kernels.zig:161-199); each row's gate and up sums in block order through LDS.
 //  - act[(t n_used + k) F + f] = silu(g) * u.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
 // Grid: ceil(n_tok n_used F / RPG) groups; 512 threads.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 weights_uav 8 weights_off 9 xh16_uav 10 xh16_off (words) 11 base_lo 12 base_hi
+// 6 ids_off 7 weights_uav 8 weights_off 9 xh_uav (fp32 [n_tok][E]) 10 xh_off (words) 11 base_lo 12 base_hi
 // 13 slot_stride 14 proj_bytes 15 codebook_srv 16 act_uav 17 act_off 18 E 19 F 20 n_tok 21 RPG
 // (22 xtab_srv: the generic form).
 // Requires TQ2_T experts (any types in the generic form), E a multiple of 256 up to 4096,
@@ -92,7 +93,7 @@ GG_DEFINE(GG_PIPELINE, 512) {
 #if GG_GENERIC
     __shared__ gd_u32x4 xdesc[2 * 256];  // the expert table: {gate, up}, {down, types, pad} per expert
 #endif
-    __shared__ uint4 xh4[2][4096 / 8];  // the run's (up to) two tokens' rotated inputs
+    __shared__ uint4 xh4[2][4096 / 4];  // the run's (up to) two tokens' rotated fp32 inputs
     __shared__ float gred[2 * GG_ITEMS * 512];  // (row, projection) block dots
     __shared__ float gsum[2 * GG_MAX_RPG];
     __shared__ uint32_t sid[2];  // experts of the run's first and second slot
@@ -116,10 +117,10 @@ GG_DEFINE(GG_PIPELINE, 512) {
     if (tid < 2u * NE) xdesc[tid] = xdv;
 #endif
     const uint32_t *XH = gd_buf<const uint32_t>(a, a.c[9]) + a.c[10];
-    for (uint32_t q = tid; q < (t1 != t0 ? 2u : 1u) * (E / 8u); q += 512u) {  // uint4 chunks
-        const uint32_t ti = q / (E / 8u), c16 = q - ti * (E / 8u), b = c16 >> 4, c = c16 & 15u;
-        const gd_u32x4 v = gd_global4(XH + (size_t)(ti ? t1 : t0) * (E / 2u))[c16];
-        xh4[ti][b * 16u + ((c + b) & 15u)] = make_uint4(v[0], v[1], v[2], v[3]);
+    for (uint32_t q = tid; q < (t1 != t0 ? 2u : 1u) * (E / 4u); q += 512u) {  // uint4 chunks
+        const uint32_t ti = q / (E / 4u), c16 = q - ti * (E / 4u);
+        const gd_u32x4 v = gd_global4(XH + (size_t)(ti ? t1 : t0) * E)[c16];
+        xh4[ti][x32_stage_index(c16 >> 5, c16 & 31u)] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 
     // Routing.
@@ -190,12 +191,8 @@ GG_DEFINE(GG_PIPELINE, 512) {
         if (j < n_items) {
             const uint32_t rr = j / nb, b = j - rr * nb;
             const uint32_t ti = (row0 + rr) / UF != t0 ? 1u : 0u;
-            uint32_t xs[64];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const uint4 v = xh4[ti][b * 16u + (((uint32_t)c + b) & 15u)];
-                xs[4 * c] = v.x; xs[4 * c + 1] = v.y; xs[4 * c + 2] = v.z; xs[4 * c + 3] = v.w;
-            }
+            float xf[128];
+            x32_from_lds(xh4[ti], b, xf);
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 float v = 0.f;
@@ -205,7 +202,7 @@ GG_DEFINE(GG_PIPELINE, 512) {
         float sc;                                                         \
         uint32_t q[gyro_nw<ID>()];                                        \
         gyro_unpack<ID>(dw[s][p], odd[s][p], sc, q);                      \
-        v = sc * gyro_block_dot_h<ID>(q, book, xs);                       \
+        v = sc * gyro_block_dot<ID>(q, book, xf);                         \
     }
                 GYRO_TYPE_SWITCH(ty[s][p], GG_CASE)
 #undef GG_CASE
@@ -213,7 +210,7 @@ GG_DEFINE(GG_PIPELINE, 512) {
                 float sc;
                 uint32_t q[8];
                 tq2_unpack(dw[s][p], odd[s][p], sc, q);
-                v = sc * tq2_block_dot_h(q, book, xs);
+                v = sc * tq2_block_dot(q, book, xf);
 #endif
                 gred[(2u * rr + (uint32_t)p) * nb + b] = v;
             }

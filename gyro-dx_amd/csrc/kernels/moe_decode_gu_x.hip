@@ -10,7 +10,7 @@
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
-// 6 ids_off 7 w_uav 8 w_off 9 xh16_uav 10 xh16_off (words) 11 xtab_srv 12 codebook_srv 13 gu_uav
+// 6 ids_off 7 w_uav 8 w_off 9 xh_uav (fp32 [n_tok][E]) 10 xh_off (words) 11 xtab_srv 12 codebook_srv 13 gu_uav
 // 14 gu_off 15 E 16 F 17 n_tok.
 // Requires E a multiple of 1024, n_expert <= 256, top-8 and F a multiple of 64.
 #include "gyro_fast.h"
@@ -21,9 +21,10 @@
 #define GX_U 8
 
 // Block b of the part row at `row` (bytes): its NW + 1 words from byte (b BB) & ~3, decoded
-// against the lane's 128 activations.
+// against the lane's 128 fp32 activations (fp32(codebook) x activation in fp32, as
+// src/kernels.zig:185-199 multiplies the decoded fp32 weights; the block scale after the sum).
 template <int ID>
-__device__ __forceinline__ float gx_block(const uint8_t *row, uint32_t b, const uint32_t *book, const uint32_t xs[64]) {
+__device__ __forceinline__ float gx_block(const uint8_t *row, uint32_t b, const uint32_t *book, const float x[128]) {
     constexpr int BB = GyroT<ID>::BB, NW = gyro_nw<ID>();
     const uint32_t off = b * BB;  // even
     gd_guint *rw = gd_global(reinterpret_cast<const uint32_t *>(row + (off & ~3u)));
@@ -33,12 +34,12 @@ __device__ __forceinline__ float gx_block(const uint8_t *row, uint32_t b, const 
     float sc;
     uint32_t w[NW];
     gyro_unpack<ID>(d, (off & 2u) != 0u, sc, w);
-    return sc * gyro_block_dot_h<ID>(w, book, xs);
+    return sc * gyro_block_dot<ID>(w, book, x);
 }
 
 GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint4 xpart[128];  // the part's 1024 activations as binary16 pairs, bank-rotated
+    __shared__ uint4 xpart[256];  // the part's 1024 fp32 activations (x32_stage_index order)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[15], F = a.c[16], n_tok = a.c[17];
     const uint32_t slot = blockIdx.z, t = slot / GX_U, k = slot - t * GX_U;
@@ -50,19 +51,16 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
     const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[12]))[tid];
-    const uint32_t xw = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * (E / 2u) + part * 512u)[tid];
+    // Thread tid stages words 2 tid, 2 tid + 1 of the part (moe_decode_gu's layout).
+    gd_guint *xg = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * E + part * 1024u + 2u * tid);
+    const uint32_t xw0 = xg[0], xw1 = xg[1];
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    // Chunk c (16 bytes) of block bx at position bx * 16 + (c + bx) % 16: the 8 blocks that a
-    // wave reads at one chunk index sit in 8 different bank groups.
-    const uint32_t bx = tid >> 6, cx = (tid >> 2) & 15u;
-    reinterpret_cast<uint32_t *>(xpart)[(bx * 16u + ((cx + bx) & 15u)) * 4u + (tid & 3u)] = xw;
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    xst[0] = xw0;
+    xst[1] = xw1;
     __syncthreads();
-    uint32_t xs[64];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint4 v = xpart[b * 16u + ((j + b) & 15u)];
-        xs[4 * j] = v.x; xs[4 * j + 1] = v.y; xs[4 * j + 2] = v.z; xs[4 * j + 3] = v.w;
-    }
+    float xf[128];
+    x32_from_lds(xpart, b, xf);
 
     // Routing to this group's rank k only; the recording group runs every round (moe_decode_gu).
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
@@ -104,7 +102,7 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     const uint8_t *row = reinterpret_cast<const uint8_t *>(addr) + (uint64_t)(row0 + r) * row_bytes + part * 8u * bb;
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
     float v = 0.f;
-#define GX_CASE(ID) v = gx_block<ID>(row, b, book, xs)
+#define GX_CASE(ID) v = gx_block<ID>(row, b, book, xf)
     GYRO_TYPE_SWITCH(type_id, GX_CASE)
 #undef GX_CASE
     v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1

@@ -112,9 +112,13 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 1024) {
     __syncthreads();
     if (tid <= NE) meta[tid] = start[tid];
     if (tid == 0) meta[1023] = tstart[NE];
-    if (a.c[8]) {  // the persistent GEMM's queue word, give-up word and per-tile counters
+    if (a.c[8]) {
+        // The persistent GEMM's queue words and per-tile counters. Word 1, its give-up word, is
+        // sticky: only the host clears it, after reading it, so a give-up in any call of a run or
+        // layer of a stack stays visible until then.
         uint32_t *sched = gd_buf<uint32_t>(a, a.c[8]);
-        for (uint32_t i = tid; i < 64u + 2u * tstart[NE]; i += 1024u) sched[i] = 0u;
+        for (uint32_t i = tid; i < 64u + 2u * tstart[NE]; i += 1024u)
+            if (i != 1u) sched[i] = 0u;
     }
     // Cursors: segment start plus the counts of earlier runs.
     if (tid < NE) {

@@ -5,19 +5,17 @@
 // x[t] is replaced by h[t] = x[t] * s[t] * w with s[t] = 1 / sqrt(mean(x[t]^2) + eps). Every
 // group accumulates mean(x[t]^2) beside its dot product from the same loads; the logit is then
 // s[t] * ((W_r[r] * w) . x[t]).
-// The rotated input is written as binary16 pairs (xh16[t][i/2] = x[i] | x[i+1] << 16), the
-// form the gate/up kernel keeps in scalar registers; a value outside the binary16 range sets
-// the range flag (constant 25).
+// The rotated input is written in fp32 (xh[t][i]), the precision of src/engine.zig:547-551, which
+// the gate/up kernels multiply by fp32 codebook values.
 // Grid: x = max(n_expert, E / 128); 256 threads. Group r < n_expert computes router row r;
 // groups r < E / 128 also rotate block r of every token (wave 0).
 // Constants: 0 x_uav 1 x_off 2 x_stride 3 n_tok 4 router_srv 5 router_off 6 n_expert 7 E
 // 8 bias_srv (0xffffffff: none) 9 bias_off 10 logits_uav 11 logits_off 12 signs_srv
-// (0xffffffff: copy) 13 signs_off 14 xh16_uav 15 xh16_off (words) 16 norm (0: none, 1: RMSNorm
+// (0xffffffff: copy) 13 signs_off 14 xh_uav (fp32 [n_tok][E]) 15 xh_off (words) 16 norm (0: none, 1: RMSNorm
 // without weight, 2: with weight; zero when the caller passes 16 constants) 17 norm_w_srv
 // 18 norm_w_off 19 eps (fp32 bits) 20 shared rows (2 SF; 0: no shared expert) 21 sh_w_srv (bf16
 // [2 SF][E]: gate rows then up rows) 22 sh_h_uav (fp32 [n][2 SF]) 23 sh_gate_srv (fp32 [E])
-// 24 sh_g_uav (fp32 [n]) 25 range flag (table index of a word set to 1 when a rotated value is
-// outside the binary16 range; 0: none). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 4 + 1
+// 24 sh_g_uav (fp32 [n]). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 4 + 1
 // further groups after the max(n_expert, E / 128) above: each of the first computes 4 bf16 rows
 // (one per wave) of W_sg x and W_su x on the unrotated input, the last the gate dot g . x. The
 // shared groups require E <= 2048.
@@ -256,17 +254,15 @@ GD_PIPELINE_NAMED(moe_router, 256) {
                 for (int j = 0; j < 8; ++j) v[j] *= GD_INV_SQRT128;
             }
             if (tv) {
-                gd_u32x4 o;
-                bool bad = false;
+                gd_u32x4 o0, o1;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    bad |= !gd_half_ok(v[2 * j]) || !gd_half_ok(v[2 * j + 1]);
-                    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
-                    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
-                    o[j] = h0 | (h1 << 16);
+                    o0[j] = gd_f32_bits(v[j]);
+                    o1[j] = gd_f32_bits(v[4 + j]);
                 }
-                *reinterpret_cast<gd_u32x4 *>(XH + t * (E / 2u) + row * 64u + l16 * 4u) = o;
-                gd_range_flag(a.table, a.c[25], bad);
+                gd_u32x4 *dst = reinterpret_cast<gd_u32x4 *>(XH + t * E + row * 128u + l16 * 8u);
+                dst[0] = o0;
+                dst[1] = o1;
             }
         }
     }

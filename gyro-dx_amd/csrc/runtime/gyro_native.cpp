@@ -17,6 +17,8 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <limits>
@@ -47,6 +49,12 @@ constexpr gd_result kDeviceRemoved = (gd_result)0x887A0005u;
 constexpr gd_result kUnexpected = (gd_result)0x8000FFFFu;
 
 constexpr uint32_t kTableCapacity = 1u << 16;
+// Every table entry that names no live buffer (index 0, indices never handed out, released ones)
+// points at a zeroed device block of this size instead of address 0. A dispatch given a wrong
+// table index then reads zeros and writes into the block instead of faulting the GPU; a context
+// created with gd_options.enable_debug (the reference's debug-layer switch) checks the block in
+// gd_wait_compute and reports such a write as E_FAIL.
+constexpr size_t kGuardBytes = 1u << 20;
 constexpr uint32_t kMaxConstants = 60;
 constexpr uint32_t kMaxTimestamps = 4096;
 constexpr uint32_t kInfinite = 0xFFFFFFFFu;
@@ -140,6 +148,8 @@ struct gd_context {
     uint32_t queue_capacity = 1024;
     void *staging = nullptr;  // pinned host staging for file reads
     uint64_t *table = nullptr;  // device table of base pointers
+    void *guard = nullptr;      // the block unassigned table entries point at (kGuardBytes)
+    bool guard_check = false;   // enable_debug: gd_wait_compute checks the block
     std::vector<uint32_t> table_free;
     uint32_t table_next = 1;  // index 0 is never handed out
     std::vector<gd_buffer *> buffers;
@@ -206,6 +216,22 @@ struct gd_context {
         return kOk;
     }
 
+    // enable_debug: after the submissions up to `ticket` finished, any nonzero word of the
+    // guard block means a dispatch wrote through an unassigned table index. The block is zeroed
+    // again and the wait fails.
+    gd_result check_guard() {
+        if (!guard_check) return kOk;
+        std::vector<uint64_t> words(kGuardBytes / 8);
+        if (hipMemcpy(words.data(), guard, kGuardBytes, hipMemcpyDeviceToHost) != hipSuccess) return kFail;
+        for (uint64_t w : words)
+            if (w) {
+                std::fprintf(stderr, "gyro_native: a dispatch wrote through an unassigned table index\n");
+                if (hipMemset(guard, 0, kGuardBytes) != hipSuccess) return kDeviceRemoved;
+                return kFail;
+            }
+        return kOk;
+    }
+
     gd_result wait_storage(uint64_t ticket, uint32_t timeout) {
         if (ticket <= poll_storage()) return kOk;
         for (auto &t : storage_events)
@@ -234,7 +260,7 @@ struct gd_context {
     }
 
     gd_result set_index(uint32_t index, const void *ptr) {
-        uint64_t v = (uint64_t)(uintptr_t)ptr;
+        uint64_t v = (uint64_t)(uintptr_t)(ptr ? ptr : guard);
         // The table is read by kernels on the compute stream; order the update with them.
         GD_HIP(hipMemcpyAsync(table + index, &v, sizeof(v), hipMemcpyHostToDevice, compute));
         return hipStreamSynchronize(compute) == hipSuccess ? kOk : kFail;
@@ -284,7 +310,18 @@ extern "C" gd_result gd_create(const gd_options *options, gd_context **out) {
         GD_HIP(hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking));
         GD_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking));
         GD_HIP(hipMalloc(&c->table, kTableCapacity * sizeof(uint64_t)));
-        GD_HIP(hipMemsetAsync(c->table, 0, kTableCapacity * sizeof(uint64_t), c->compute));
+        GD_HIP(hipMalloc(&c->guard, kGuardBytes));
+        GD_HIP(hipMemset(c->guard, 0, kGuardBytes));
+        {
+            // Every entry names the guard block until a buffer takes it; read back to make sure
+            // the table holds that before any dispatch can use it.
+            std::vector<uint64_t> init(kTableCapacity, (uint64_t)(uintptr_t)c->guard);
+            GD_HIP(hipMemcpy(c->table, init.data(), kTableCapacity * sizeof(uint64_t), hipMemcpyHostToDevice));
+            std::vector<uint64_t> back(kTableCapacity, 0);
+            GD_HIP(hipMemcpy(back.data(), c->table, kTableCapacity * sizeof(uint64_t), hipMemcpyDeviceToHost));
+            if (back != init) return kFail;
+        }
+        c->guard_check = opts.enable_debug != 0;
         GD_HIP(hipHostMalloc(&c->staging, c->staging_bytes, hipHostMallocDefault));
         GD_HIP(hipStreamSynchronize(c->compute));
         size_t free_b = 0, total_b = 0;
@@ -841,7 +878,8 @@ extern "C" gd_result gd_submit(gd_context *c, uint64_t *ticket) {
 
 extern "C" gd_result gd_wait_compute(gd_context *c, uint64_t ticket, uint32_t timeout) {
     if (!c || ticket > c->next_compute) return kInvalidArg;
-    return c->wait_compute(ticket, timeout);
+    GD_TRY(c->wait_compute(ticket, timeout));
+    return c->check_guard();
 }
 
 extern "C" gd_result gd_read_timestamps(gd_context *c, uint32_t count, uint64_t *out, uint64_t *frequency) {
@@ -920,6 +958,7 @@ extern "C" gd_result gd_destroy(gd_context *c, uint32_t timeout) {
     for (hipEvent_t e : c->free_events) hipEventDestroy(e);
     for (hipEvent_t e : c->ts_pool) hipEventDestroy(e);
     hipFree(c->table);
+    hipFree(c->guard);
     hipHostFree(c->staging);
     hipStreamDestroy(c->compute);
     hipStreamDestroy(c->copy);

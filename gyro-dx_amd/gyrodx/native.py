@@ -11,6 +11,7 @@ LIB_PATH = BUILD_DIR / "libgyro_native.so"
 E_INVALIDARG = -2147024809  # 0x80070057
 ERROR_INVALID_DATA = -2147024883  # 0x8007000D
 E_ILLEGAL_METHOD_CALL = -2147483634  # 0x8000000E
+E_FAIL = -2147467259  # 0x80004005
 
 # Every symbol the header declares (native/include/gyro_native.h:71-137 of the reference).
 SYMBOLS = [

@@ -208,11 +208,9 @@ constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
 void *scratch_ptr[kMaxDevices] = {};
 
-// `first` is set for the first lookup on a device (the caller clears what must start at zero).
-void *scratch_address(uint32_t device, bool &first) {
+void *scratch_address(uint32_t device) {
     if (device >= (uint32_t)kMaxDevices) throw NativeError(-1, "device ordinal out of range for the scratch table");
     std::lock_guard<std::mutex> lock(scratch_mutex);
-    first = !scratch_ptr[device];
     if (!scratch_ptr[device]) {
         hipError_t rc = hipSetDevice((int)device);
         if (rc != hipSuccess) throw NativeError(-1, std::string("hipSetDevice: ") + hipGetErrorString(rc));
@@ -231,26 +229,8 @@ void *scratch_address(uint32_t device, bool &first) {
 constexpr uint64_t kNoallocShH = 0, kNoallocShHBytes = 64u << 10;
 constexpr uint64_t kNoallocShG = kNoallocShHBytes, kNoallocShGBytes = 256;
 
-// Exchange area of moe_decode_fused, in words. One layout for every layer shape, so an area that
-// engines of different shapes share (the scratch array) never holds data where a later call
-// expects a counter; counters are zero between calls and every tagged word is rewritten by each
-// call that polls it.
-namespace xch {
-constexpr uint32_t kCtl = 0;                          // EP, error tag (+ 32), sticky error word (+ 64)
-constexpr uint32_t kMaxGroups = 512, kMaxSlots = 16, kMaxActBlocks = 128;
-constexpr uint32_t kLog = 128;                        // logit and arrival words, one per 128-byte line
-constexpr uint32_t kRoute = kLog + 32 * kMaxGroups;   // 2 x 16 route words (64-bit)
-constexpr uint32_t kCnt = kRoute + 128;               // slot counters, 32 words apart
-constexpr uint32_t kFlag = kCnt + 32 * kMaxSlots;     // slot flags, 32 words apart
-constexpr uint32_t kAct = kFlag + 32 * kMaxSlots;     // [16][1024] SwiGLU outputs
-constexpr uint32_t kWords = kAct + kMaxSlots * 1024;
-constexpr uint32_t kSpinLimit = 1u << 16;             // polls (about 64 ms) before a wait gives up
-}  // namespace xch
-
-constexpr uint64_t kNoallocXch = 128u << 10, kNoallocXchBytes = 160u << 10;
-constexpr uint64_t kNoallocBase = kNoallocXch + kNoallocXchBytes;
-static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocXch, "scratch regions overlap");
-static_assert(xch::kWords * 4ull <= kNoallocXchBytes, "exchange area exceeds its scratch region");
+constexpr uint64_t kNoallocBase = 128u << 10;
+static_assert(kNoallocShG + kNoallocShGBytes <= kNoallocBase, "scratch regions overlap");
 
 }  // namespace
 
@@ -266,12 +246,6 @@ struct DecodeBufs {
     uint32_t logits, logits_off, ids, ids_off, weights, weights_off, xh, xh_off, gu, gu_off;
     uint32_t sh_h, sh_g;  // the fused shared expert's rows and gate dots (offset 0)
     SharedBufs shared;    // the shared expert outside the fused kernels
-    uint32_t xch;         // moe_decode_fused's exchange area (offset 0)
-};
-
-// Work split of moe_decode_fused: G groups, FB rows per gate/up unit, RB rows per down unit.
-struct FusedSplit {
-    uint32_t G = 0, FB = 0, RB = 0;
 };
 
 // Residual stream of a stack step: the layer input is normalised by the layer's RMSNorm inside
@@ -295,25 +269,9 @@ class Engine {
     bool direct = false;
     void *direct_stream = nullptr;
     Buffer na_base, na_shh, na_shg, na_x, na_out;  // table entries into `scratch` and for the caller's x, out
-    Buffer na_xch;                                 // the scratch array's moe_decode_fused exchange area
-    // Single-launch decode (moe_decode_fused): its exchange area, the group count (compute units),
-    // the mode (environment GYRO_DECODE_FUSED: 1 takes batch-1 calls on it where it fits, 2 makes
-    // a batch-1 decode call that it cannot take an error; otherwise 0, the three-kernel path, which
-    // is faster on MI355X) and the polls a wait makes before it gives up (GYRO_DECODE_SPIN_LIMIT,
-    // default 65536).
-    Buffer xch_area;
+    // Compute units of the device (the persistent GEMM's two groups per unit, the decode
+    // kernels' target group count).
     uint32_t cus = 0;
-    uint32_t fused_mode = 0;
-    uint32_t spin_limit = xch::kSpinLimit;
-    // Router and gate/up in one launch (moe_decode_rgu) for the tuned TQ2_T shapes when the
-    // environment sets GYRO_DECODE_RGU=1 (measured no faster than the three-kernel path on MI355X):
-    // its logit words (8 tokens x 256 experts, 64-bit, 128 bytes apart) and the call epoch, never
-    // 0, that tags them. A wait that gives up stores the sticky error word of xch_area, as
-    // moe_decode_fused does.
-    bool rgu_on = false;
-    uint32_t rgu_epoch = 0;
-    Buffer rgu_area;
-    static constexpr uint32_t kRguTokens = 8, kRguExperts = 256;
     // Prefill GEMMs of uniform TQ2_T layers: one persistent launch over both (moe_prefill_gemm)
     // unless the environment sets GYRO_PREFILL_FUSED=0 (then moe_prefill_gu and moe_prefill_down);
     // the polls a down unit makes for a ready tile before it gives up (GYRO_PREFILL_SPIN_LIMIT,
@@ -351,7 +309,7 @@ class Engine {
     Buffer staging, codebook, zeros;
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
     Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
-    // Activation range guard: word 0 of range_flag (set by moe_router, moe_prefill_router and
+    // Activation range guard: word 0 of range_flag (set by moe_prefill_router and
     // moe_prefill_shared) and word kMetaRangeFlag of meta (set by the prefill gate/up GEMMs) become
     // 1 when an activation rounded to binary16 is outside its range.
     Buffer range_flag;
@@ -464,22 +422,15 @@ class Engine {
         fill_zero(range_flag);
         // Table entries of the no-allocation entry point: into this GPU's scratch array, and two
         // whose addresses each call sets (the caller's input and output).
-        bool first_use = false;
-        uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter, first_use));
+        uint8_t *sp = static_cast<uint8_t *>(scratch_address(adapter));
         na_base = dev.wrap(sp, GM_NOALLOC_SCRATCH_BYTES);
         na_shh = dev.wrap(sp + kNoallocShH, kNoallocShHBytes);
         na_shg = dev.wrap(sp + kNoallocShG, kNoallocShGBytes);
-        na_xch = dev.wrap(sp + kNoallocXch, kNoallocXchBytes);
         na_x = dev.wrap(nullptr, 0);
         na_out = dev.wrap(nullptr, 0);
-        if (first_use) fill_zero(na_xch);
-        // The single-launch decode kernel: one group per compute unit, its exchange area zeroed.
         int cu = 0;
         if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, (int)adapter) != hipSuccess) cu = 0;
         cus = (uint32_t)std::max(cu, 0);
-        const char *fe = std::getenv("GYRO_DECODE_FUSED");
-        fused_mode = fe && fe[0] == '1' ? 1u : fe && fe[0] == '2' ? 2u : 0u;
-        if (const char *sl = std::getenv("GYRO_DECODE_SPIN_LIMIT")) spin_limit = (uint32_t)std::strtoul(sl, nullptr, 10);
         const char *pf = std::getenv("GYRO_PREFILL_FUSED");
         prefill_fused = !(pf && pf[0] == '0');
         const char *psm = std::getenv("GYRO_PREFILL_SMALL");
@@ -488,18 +439,12 @@ class Engine {
         stack_norm_fused = !(snf && snf[0] == '0');
         if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
-        xch_area = dev.buffer(xch::kWords * 4ull, Kind::device);
-        fill_zero(xch_area);
-        const char *rg = std::getenv("GYRO_DECODE_RGU");
-        rgu_on = rg && rg[0] == '1';
-        rgu_area = dev.buffer((uint64_t)kRguTokens * kRguExperts * 128u, Kind::device);
-        fill_zero(rgu_area);
     }
 
     // The decode path's own intermediate buffers.
     DecodeBufs engine_bufs() const {
         return {router_out.uav, 0, ids.uav, 0, weights.uav, 0, xh.uav, 0, gu_part.uav, 0, sh_h.uav, sh_g.uav,
-                engine_shared(), xch_area.uav};
+                engine_shared()};
     }
 
     void allocate_activations() {
@@ -851,61 +796,7 @@ class Engine {
     // Layers other than uniform TQ2_T (or with the fused shared expert) take the type-generic kernels.
     bool decode_generic_types(const Layer &L) const { return L.type_id != 144 || decode_fused_shared(L); }
 
-    // moe_decode_fused takes batch-1 calls of uniform TQ2_T layers without a shared expert when
-    // every group's gate/up units (FB rows of one slot) and down units (RB rows of every slot)
-    // fit its per-thread items: at most 4 units of each kind per group, 2 FB E / 128 items per
-    // gate/up unit and 2 U RB F / 128 per down unit, 2048 items, 512 output rows and 2048
-    // (row, slot) sums per group, and U F / 128 rotated down-input blocks in LDS.
-    FusedSplit fused_split(const Layer &L, uint32_t n) const {
-        FusedSplit fs;
-        if (!fused_mode || n != 1 || L.type_id != 144 || L.SF || E % 256 || E > 4096 || F % 128 || F > 1024 || U < 1 ||
-            U > xch::kMaxSlots || NE > xch::kMaxGroups || U * (F / 128) > xch::kMaxActBlocks)
-            return fs;
-        const uint32_t G = std::min(cus, xch::kMaxGroups), nb = E / 128, nbF = F / 128;
-        if (G == 0) return fs;
-        auto per_group = [G](uint32_t units) { return (units + G - 1) / G; };
-        // Down units: the smallest row count that divides E with at most one unit per group.
-        uint32_t RB = (E + G - 1) / G;
-        while (E % RB) ++RB;
-        const uint32_t nd = per_group(E / RB);
-        if (nd > 4 || nd * U * RB * 2 * nbF > 2048 || nd * RB > 512 || nd * RB * U > 2048) return fs;
-        for (uint32_t FB : {16u, 8u}) {
-            const uint32_t ng = per_group(U * (F / FB));
-            if (ng > 4 || ng * 2 * FB * nb > 2048) continue;
-            fs.G = G;
-            fs.FB = FB;
-            fs.RB = RB;
-            return fs;
-        }
-        return fs;
-    }
 
-    // Keeps decode on the three-kernel path (no moe_decode_fused, no moe_decode_rgu) for its
-    // lifetime (a recomputation).
-    struct UnfusedScope {
-        Engine *e;
-        uint32_t was;
-        bool was_rgu;
-        explicit UnfusedScope(Engine *eng) : e(eng), was(eng->fused_mode), was_rgu(eng->rgu_on) {
-            e->fused_mode = 0;
-            e->rgu_on = false;
-        }
-        ~UnfusedScope() {
-            e->fused_mode = was;
-            e->rgu_on = was_rgu;
-        }
-    };
-
-    // moe_decode_rgu takes the tuned TQ2_T shapes (hidden 1024 or 2048, F 512, top-8) without the
-    // fused shared expert, at most 8 tokens of at most 256 experts, when each of its first
-    // P = min(G, n_expert) groups computes at most two router rows; not the no-allocation entry
-    // point (its buffers are the caller's scratch).
-    bool rgu_fits(uint32_t n, const DecodeBufs *bufs) const {
-        if (!rgu_on || bufs || n == 0 || n > kRguTokens || NE > kRguExperts || NE == 0 || (E != 1024 && E != 2048))
-            return false;
-        const uint32_t G = (F / 64) * 2 * parts * n * U, P = std::min(G, NE);
-        return (NE + P - 1) / P <= 2;
-    }
 
     struct UnfusedPrefillScope {
         Engine *e;
@@ -925,20 +816,8 @@ class Engine {
         return true;
     }
 
-    // Reads and clears the sticky error word of the exchange area: set when a moe_decode_fused
-    // group gave up a wait (its groups were not all running within the spin limit).
-    bool take_fused_error(const Buffer &area) {
-        uint32_t w = 0;
-        check(gd_readback(dev.ctx, area.handle, (xch::kCtl + 64) * 4, 4, &w, kTimeoutMs), "gd_readback");
-        if (!w) return false;
-        const uint32_t zero = 0;
-        upload(area, (xch::kCtl + 64) * 4, &zero, 4);
-        return true;
-    }
 
-    // MI355X decode path: router + rotation, routed gate/up, down + combine; at batch 1, when the
-    // engine was created with GYRO_DECODE_FUSED=1 or 2 and fused_split allows, one launch of
-    // moe_decode_fused instead.
+    // MI355X decode path: router + rotation, routed gate/up, down + combine.
     void ffn_decode(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
                     int bracket = 0, std::vector<uint32_t> *marks = nullptr, StackStep st = {},
                     const DecodeBufs *bufs = nullptr) {
@@ -948,22 +827,6 @@ class Engine {
             throw NativeError(-1, "decode path needs <= 256 experts, n <= 8, E a multiple of 256 up to 4096, F a "
                                   "multiple of 128 up to 1024 and top-1..16 (or, for other than uniform TQ2_T "
                                   "experts, E a multiple of 1024 with F 512 and top-8)");
-        const FusedSplit fs = fused_split(L, n);
-        if (!fs.G && n == 1 && fused_mode == 2)
-            throw NativeError(-1, "GYRO_DECODE_FUSED=2: this batch-1 decode call cannot take moe_decode_fused");
-        if (fs.G) {
-            const uint32_t norm = st.on ? (L.has_norm ? 2u : 1u) : 0u;
-            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_fused",
-                                 {x_uav, x_off, L.router.srv, L.has_bias ? L.bias.srv : kNone, L.signs.srv,
-                                  (L.has_gate_signs ? 1u : 0u) | (L.has_down_signs ? 2u : 0u), B.xch, xch::kLog,
-                                  xch::kRoute, xch::kAct, xch::kCnt, xch::kFlag, out_uav, out_off,
-                                  (uint32_t)L.base, (uint32_t)(L.base >> 32), slot_stride, L.gate_bytes, codebook.srv, E,
-                                  F, NE, U, bits(L.scale), xch::kCtl, B.ids, B.ids_off, B.weights, B.weights_off,
-                                  st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, flag_uav(), spin_limit,
-                                  norm, fs.FB, fs.RB, L.has_norm ? L.norm.srv : 0u, bits(L.norm_eps)},
-                                 fs.G);
-            return;
-        }
         const bool fused_sh = decode_fused_shared(L);
         if (L.SF && !fused_sh) {
             // The shared expert first; its gated output (plus a stack's stream) is the residual
@@ -979,30 +842,12 @@ class Engine {
         const uint32_t rsf = fused_sh ? L.SF : 0u;  // shared rows computed inside moe_router
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const bool generic = decode_generic_types(L);
-        if (!generic && decode_tuned_tq2() && rgu_fits(n, bufs)) {
-            // Router, rotation, routing and gate/up in one launch, then the down kernel.
-            rgu_epoch = rgu_epoch + 1u == 0u ? 1u : rgu_epoch + 1u;
-            dispatch_maybe_timed(bracket == 2, marks, "moe_decode_rgu",
-                                 {x_uav, x_off, E, n, L.router.srv, L.has_bias ? L.bias.srv : kNone, NE, E, F,
-                                  L.has_gate_signs ? L.signs.srv : kNone, st.on ? (L.has_norm ? 2u : 1u) : 0u,
-                                  L.has_norm ? L.norm.srv : 0u, bits(L.norm_eps), rgu_area.uav, rgu_epoch, spin_limit,
-                                  B.xch, xch::kCtl + 64, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off,
-                                  base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, flag_uav()},
-                                 F / 64, 2 * parts, n * U);
-            dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down",
-                                 {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, base_lo, base_hi, slot_stride,
-                                  2 * L.gate_bytes, codebook.srv, L.has_down_signs ? L.signs.srv : kNone, E, out_uav,
-                                  out_off, E, F, U, n, parts, NE, st.res_uav != kNone ? 1u : 0u, st.res_uav,
-                                  st.res_off},
-                                 E / 8, n);
-            return;
-        }
         dispatch_maybe_timed(bracket == 1, marks, "moe_router",
                              {x_uav, x_off, E, n, L.router.srv, 0, NE, E, L.has_bias ? L.bias.srv : kNone, 0,
                               B.logits, B.logits_off, L.has_gate_signs ? L.signs.srv : kNone, 0, B.xh, B.xh_off,
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
                               bits(L.norm_eps), 2 * rsf, rsf ? L.sh_gu.srv : 0u, rsf ? B.sh_h : 0u,
-                              rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u, flag_uav()},
+                              rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u},
                              std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
         if (!generic || !decode_generic_tuned()) {
             if (!generic && decode_tuned_tq2()) {
@@ -1060,10 +905,16 @@ class Engine {
     // moe_prefill_down, other layers the type-generic moe_prefill_gu_x / moe_prefill_down_x.
     // A shared expert runs as moe_prefill_shared (SF a multiple of 64).
     // F a multiple of 128 (an odd block count per down row is handled), top-U for U <= 16.
-    bool prefill_supported(const Layer &L) const {
+    bool prefill_supported(const Layer &L) const { return prefill_shape_ok(L) && prefill_range_ok(L); }
+    bool prefill_shape_ok(const Layer &L) const {
         return L.SF % 64 == 0 && (L.SF == 0 || E <= 4096) && E % 256 == 0 && F % 128 == 0 && F >= 256 && U >= 1 &&
-               U <= 16 && NE <= 256 && L.max_scale * max_codebook < 65504.0f;
+               U <= 16 && NE <= 256;
     }
+    bool prefill_range_ok(const Layer &L) const { return L.max_scale * max_codebook < 65504.0f; }
+    // A layer of a prefill shape whose block scale x codebook products leave the binary16 range
+    // (one outlier block suffices) runs its prefill calls on the generic path, which keeps the
+    // reference's fp32 weights, instead of being refused.
+    bool prefill_on_generic(const Layer &L) const { return prefill_shape_ok(L) && !prefill_range_ok(L); }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
     // down GEMMs (one persistent launch for uniform TQ2_T layers), shared expert, combine.
@@ -1159,6 +1010,8 @@ class Engine {
             ffn_reference(il, n, x_uav, x_off, out_uav, out_off);
         else if (path == GM_PATH_DECODE)
             ffn_decode(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
+        else if (path == GM_PATH_PREFILL && prefill_on_generic(layers.at(il)))
+            ffn_generic(il, n, x_uav, x_off, out_uav, out_off);
         else if (path == GM_PATH_PREFILL)
             ffn_prefill(il, n, x_uav, x_off, out_uav, out_off, bracket, marks);
         else if (path == GM_PATH_GENERIC)
@@ -1179,6 +1032,15 @@ class Engine {
     void stack(const uint32_t *list, uint32_t n_layers, uint32_t path, uint32_t n, uint32_t x_uav, uint32_t x_off,
                uint32_t y_uav, uint32_t y_off) {
         if (E > 4096) throw NativeError(-1, "stack RMSNorm covers E <= 4096");
+        // A prefill stack with a layer whose weights leave the binary16 range (see
+        // prefill_on_generic) runs every layer on the generic path: the prefill layers' fused
+        // residual and the generic layers' deferred one do not mix within one pass.
+        if (path == GM_PATH_PREFILL)
+            for (uint32_t l = 0; l < n_layers; ++l)
+                if (prefill_on_generic(layers.at(list[l]))) {
+                    path = GM_PATH_GENERIC;
+                    break;
+                }
         bool normed = false;  // hn already holds this layer's normalised input
         for (uint32_t l = 0; l < n_layers; ++l) {
             const Layer &L = layers.at(list[l]);
@@ -1229,9 +1091,10 @@ class Engine {
             if (list[l] >= layers.size()) throw NativeError(-1, "layer index out of range");
     }
 
-    // A fast path (decode, prefill) whose activations left the binary16 range is recomputed on
-    // the generic path, which keeps them in fp32.
-    static bool fast_path(uint32_t path) { return path == GM_PATH_DECODE || path == GM_PATH_PREFILL; }
+    // The prefill path rounds activations to binary16 for its MFMA products; a call whose
+    // activations left the binary16 range is recomputed on the generic path, which keeps them in
+    // fp32. (The decode path keeps every activation in fp32.)
+    static bool fast_path(uint32_t path) { return path == GM_PATH_PREFILL; }
 
     void forward_stack(const uint32_t *list, uint32_t n_layers, uint32_t path, const float *x, uint32_t n, float *y) {
         if (n == 0 || n > max_tok) throw NativeError(-1, "token count exceeds max_tok");
@@ -1240,13 +1103,6 @@ class Engine {
         dev.begin();
         stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
         dev.wait(dev.submit());
-        if (path == GM_PATH_DECODE && take_fused_error(xch_area)) {
-            UnfusedScope unfused{this};
-            upload(x_in, 0, x, (uint64_t)n * E * 4);
-            dev.begin();
-            stack(list, n_layers, path, n, x_in.uav, 0, x_in.uav, 0);
-            dev.wait(dev.submit());
-        }
         if (path == GM_PATH_PREFILL && take_gemm_error()) {
             UnfusedPrefillScope unfused{this};
             upload(x_in, 0, x, (uint64_t)n * E * 4);
@@ -1297,12 +1153,11 @@ class Engine {
         B.logits_off = take((uint64_t)n * NE * 4);
         B.ids_off = take((uint64_t)n * U * 4);
         B.weights_off = take((uint64_t)n * U * 4);
-        B.xh_off = take((uint64_t)n * E * 2);
+        B.xh_off = take((uint64_t)n * E * 4);
         B.gu_off = take((uint64_t)parts * n * U * 2 * F * 4);
         B.sh_h = na_shh.uav;
         B.sh_g = na_shg.uav;
         B.shared = {};
-        B.xch = na_xch.uav;
         if (L.SF && !decode_fused_shared(L)) {
             SharedBufs &S = B.shared;
             S.h = S.a = S.o = S.g = S.s = na_base.uav;
@@ -1336,12 +1191,6 @@ class Engine {
         dev.begin();
         ffn(path, il, n, x_in.uav, 0, out.uav, 0);
         dev.wait(dev.submit());
-        if (path == GM_PATH_DECODE && take_fused_error(xch_area)) {
-            UnfusedScope unfused{this};
-            dev.begin();
-            ffn(path, il, n, x_in.uav, 0, out.uav, 0);
-            dev.wait(dev.submit());
-        }
         if (path == GM_PATH_PREFILL && take_gemm_error()) {
             UnfusedPrefillScope unfused{this};
             dev.begin();
@@ -1522,14 +1371,11 @@ extern "C" int gm_run_bracketed(gm_engine *g, uint32_t path, uint32_t batch, uin
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
         if (bracket_us) *bracket_us = br_n ? br / (double)br_n : 0.0;
-        if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
-            throw gyro::NativeError(-1, "a decode call in one launch (moe_decode_fused or moe_decode_rgu) gave up waiting for its workgroups: the "
-                                        "outputs of this run are invalid (gm_forward recomputes such calls on the three-kernel path)");
         if (path == GM_PATH_PREFILL && e.take_gemm_error())
             throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
                                         "this run are invalid (gm_forward recomputes such calls with two GEMM launches)");
         if (Engine::fast_path(path) && e.take_range_flag())
-            throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
+            throw gyro::NativeError(-1, "an activation left the binary16 range on the prefill path: the outputs of this run "
                                         "are invalid (gm_forward recomputes such calls on GM_PATH_GENERIC)");
     });
 }
@@ -1567,14 +1413,11 @@ extern "C" int gm_run_stack(gm_engine *g, uint32_t path, uint32_t batch, uint32_
         }
         *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *device_ms = dev;
-        if (path == GM_PATH_DECODE && e.take_fused_error(e.xch_area))
-            throw gyro::NativeError(-1, "a decode call in one launch (moe_decode_fused or moe_decode_rgu) gave up waiting for its workgroups: the "
-                                        "outputs of this run are invalid (gm_forward_stack recomputes such calls on the three-kernel path)");
         if (path == GM_PATH_PREFILL && e.take_gemm_error())
             throw gyro::NativeError(-1, "a prefill GEMM unit gave up waiting for its tile's gate/up rows: the outputs of "
                                         "this run are invalid (gm_forward_stack recomputes such calls with two GEMM launches)");
         if (Engine::fast_path(path) && e.take_range_flag())
-            throw gyro::NativeError(-1, "an activation left the binary16 range on the fast path: the outputs of this run "
+            throw gyro::NativeError(-1, "an activation left the binary16 range on the prefill path: the outputs of this run "
                                         "are invalid (gm_forward_stack recomputes such calls on GM_PATH_GENERIC)");
     });
 }

@@ -43,7 +43,9 @@ typedef int32_t gd_result;
 /* 20 bytes (src/native_abi.zig:89). */
 typedef struct gd_options {
     uint32_t adapter_index;  /* HIP device ordinal */
-    uint32_t enable_debug;   /* ignored */
+    uint32_t enable_debug;   /* nonzero: gd_wait_compute fails (E_FAIL) when a finished dispatch
+                                wrote through a table index that names no buffer (such indices
+                                point at a zeroed guard block, never at address 0) */
     uint32_t require_linalg; /* fail creation if MFMA fp16 is unavailable */
     uint32_t staging_bytes;  /* pinned staging per file read (>= 4096; default 32 MiB) */
     uint32_t queue_capacity; /* power of two in [128, 65536]; bounds ranges per read */
@@ -138,7 +140,8 @@ GD_API gd_result gd_barrier(gd_context *context);
 GD_API gd_result gd_timestamp(gd_context *context, uint32_t *out_index);
 /* Replaces gd_submit (:919-934). */
 GD_API gd_result gd_submit(gd_context *context, uint64_t *out_compute_ticket);
-/* Replaces gd_wait_compute (:936-939). */
+/* Replaces gd_wait_compute (:936-939). With gd_options.enable_debug, also E_FAIL when a dispatch
+ * finished by `ticket` wrote through an unassigned table index (the guard block is then cleared). */
 GD_API gd_result gd_wait_compute(gd_context *context, uint64_t ticket, uint32_t timeout_ms);
 /* Replaces gd_read_timestamps (:941-951): ticks of the last completed submission's marks, in
  * nanoseconds relative to its first mark (frequency 1e9). */

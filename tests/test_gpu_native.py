@@ -200,3 +200,44 @@ def test_stream_file_ranges(ctx):
         native.check(L.gd_release_file(ctx, fh, TIMEOUT))
     finally:
         os.unlink(path)
+
+
+def test_unassigned_table_index_is_a_host_error():
+    """Every table entry that names no buffer (index 0 among them) points at a zeroed 1 MiB guard
+    block, never at address 0 (gd_create reads the table back to make sure), so a dispatch given a
+    wrong table index writes into that block instead of faulting the GPU. A context created with
+    enable_debug reports such a write from gd_wait_compute as E_FAIL and clears the block: the
+    next wait on clean work succeeds. Here a bit-exact copy of 1024 words (4 KiB, inside the
+    block) targets index 0 as if the caller had dropped a constant."""
+    L = native.lib()
+    opts = native.Options(0, 1, 0, 32 << 20, 1024)  # enable_debug
+    h = C.c_void_p()
+    native.check(L.gd_create(C.byref(opts), C.byref(h)), "gd_create")
+    try:
+        pipe = C.c_void_p()
+        ew = code("ew")
+        native.check(L.gd_create_pipeline(h, ew, len(ew), C.byref(pipe)))
+        src, sinfo = make_resource(h, 4096, 1)
+        dst, dinfo = make_resource(h, 4096, 0)
+        data = (np.arange(1024, dtype=np.uint32) | 1).astype(np.uint32)  # every word nonzero
+        C.memmove(sinfo.mapped, data.ctypes.data, 4096)
+        ticket = C.c_uint64()
+
+        def copy_to(index):
+            native.check(L.gd_begin(h, TIMEOUT))
+            cst = (C.c_uint32 * 12)(sinfo.uav_index, 0, 0, sinfo.uav_index, 0, 0, index, 0, 0, 1024, 1, 5)
+            native.check(L.gd_dispatch(h, pipe, cst, 12, 4, 1, 1))
+            native.check(L.gd_submit(h, C.byref(ticket)))
+            return L.gd_wait_compute(h, ticket, TIMEOUT)
+
+        assert copy_to(dinfo.uav_index) == 0
+        assert copy_to(0) == native.E_FAIL  # the write landed in the guard block
+        assert copy_to(dinfo.uav_index) == 0  # the block was cleared
+        back = np.zeros(1024, np.uint32)
+        native.check(L.gd_readback(h, dst, 0, 4096, back.ctypes.data, TIMEOUT))
+        np.testing.assert_array_equal(back, data)
+        native.check(L.gd_release_buffer(h, dst, TIMEOUT))
+        native.check(L.gd_release_buffer(h, src, TIMEOUT))
+        native.check(L.gd_release_pipeline(h, pipe, TIMEOUT))
+    finally:
+        native.check(L.gd_destroy(h, TIMEOUT), "gd_destroy")

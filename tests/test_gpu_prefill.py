@@ -138,14 +138,34 @@ def test_prefill_without_rotations(oracle_mod):
     run_case(oracle_mod, layer, synth.make_tokens(52, 70, layer.E), 128, "no signs")
 
 
-def test_prefill_refuses_fp16_overflowing_scales():
-    """Blocks whose scale x codebook product overflows binary16 are refused, not computed."""
+def test_prefill_falls_back_on_fp16_overflowing_scales(oracle_mod):
+    """A block whose scale x codebook products overflow binary16 (scale 60000 in one gate block of
+    expert 3) keeps the layer off the fp16 grouped GEMMs: gm_forward on the prefill path runs the
+    generic path's fp32 kernels instead of refusing, and so does a prefill stack holding the
+    layer. Outputs against the oracle, with the outlier expert among the routes."""
     layer = synth.make_layer(61, E=1024, F=256, n_expert=16, n_used=8)
     layer.gate[3][5, 0:2] = np.frombuffer(np.float16(60000.0).tobytes(), np.uint8)
-    eng = Engine(max_tok=8)
+    x = synth.make_tokens(62, 16, layer.E)
+    ref = oracle_mod.OracleLayer(layer).forward(x)
+    eng = Engine(max_tok=16)
     try:
         eng.add_layer(layer)
-        with pytest.raises(RuntimeError, match="binary16-finite"):
-            eng.forward(0, synth.make_tokens(62, 4, layer.E), PATH_PREFILL)
+        out = eng.forward(0, x, PATH_PREFILL)
+        ids, _ = eng.last_routes(16)
+        assert (ids == 3).any(), "no token routed to the outlier expert"
+        r, c = oracle_mod.rel_rms(ref, out), oracle_mod.cosine(ref, out)
+        print(f"prefill with an overflowing block scale: rel_rms {r:.3e} cosine {c:.8f}", flush=True)
+        assert r <= REL_RMS and c >= COSINE
+        # A two-layer stack: the outlier layer second, a plain layer first.
+        S = synth.make_stack(63, 2, E=1024, F=256, n_expert=16, n_used=8)
+        S[1].gate[3][5, 0:2] = np.frombuffer(np.float16(60000.0).tobytes(), np.uint8)
+        sids = [eng.add_layer(L) for L in S]
+        h = x.copy()
+        for L in S:
+            h = h + oracle_mod.OracleLayer(L).forward(oracle_mod.rms_norm(h, L.norm_weight, L.norm_eps))
+        got = eng.forward_stack(sids, x, PATH_PREFILL)
+        r = oracle_mod.rel_rms(h, got)
+        print(f"prefill stack with the outlier layer: rel_rms {r:.3e}", flush=True)
+        assert r <= REL_RMS
     finally:
         eng.close()

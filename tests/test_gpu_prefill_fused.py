@@ -83,33 +83,48 @@ def test_persistent_gemm_matches_two_launches(oracle_mod, E, F, NE, U, n, kw):
     assert r <= REL_RMS and c >= COSINE
 
 
+
+
 def test_persistent_gemm_give_up_recomputes():
-    """With a spin limit of zero polls a down unit whose tile is not finished gives up at once;
-    gm_forward then recomputes the call with two launches, so its result is unchanged. gm_run
-    reports such a call as invalid instead."""
-    L = synth.make_layer(1560, zipf=1.1)
+    """With a spin limit of zero polls a down unit whose tile is not finished gives up at once.
+    The give-up word is sticky: the sort of a later call or layer does not clear it, only the host
+    does after reading it. So gm_forward and gm_forward_stack (two layers) recompute with two
+    launches and return the two-launch engine's outputs bit for bit, and gm_run over two calls
+    either reports the give-up or returns those outputs bit for bit."""
     n = 1024
+    L = synth.make_layer(1560, zipf=1.1)
+    S = synth.make_stack(1562, 2, zipf=1.1)
     x = synth.make_tokens(1561, 2 * n, bf16=True)
     ref_eng = make_engine(n, False)
     try:
         ref_eng.add_layer(L)
+        sids = [ref_eng.add_layer(s) for s in S]
         ref = ref_eng.forward(0, x[:n], PATH_PREFILL)
+        ref_stack = ref_eng.forward_stack(sids, x[:n], PATH_PREFILL)
+        ref_eng.set_tokens(x)
+        ref_eng.run(PATH_PREFILL, n, 2, [0])
+        ref_run = ref_eng.read_outputs(2 * n)
     finally:
         ref_eng.close()
     eng = make_engine(n, True, spin_limit=0)
     try:
         eng.add_layer(L)
-        print("persistent prefill GEMM, spin limit 0", flush=True)
+        sids = [eng.add_layer(s) for s in S]
+        print("persistent prefill GEMM, spin limit 0: gm_forward", flush=True)
         out = eng.forward(0, x[:n], PATH_PREFILL)
         np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+        print("  gm_forward_stack over 2 layers", flush=True)
+        out = eng.forward_stack(sids, x[:n], PATH_PREFILL)
+        np.testing.assert_array_equal(out.view(np.uint32), ref_stack.view(np.uint32))
         eng.set_tokens(x)
         try:
             eng.run(PATH_PREFILL, n, 2, [0])
-            print("  gm_run: no unit gave up", flush=True)
+            got = eng.read_outputs(2 * n)
+            np.testing.assert_array_equal(got.view(np.uint32), ref_run.view(np.uint32))
+            print("  gm_run: no unit gave up; outputs equal the two-launch run", flush=True)
         except RuntimeError as err:
             assert "gave up waiting" in str(err), err
             print("  gm_run reported the give-up", flush=True)
-        # The give-up word is cleared: a call with a normal limit on a fresh engine is clean.
     finally:
         eng.close()
 

@@ -1,9 +1,10 @@
-"""The activation range guard of the fast paths, through the C ABI: the decode and prefill paths
-round activations to binary16 (the rotated input in moe_router / moe_prefill_router, the SwiGLU
+"""The activation range guard of the prefill path, through the C ABI: the prefill path rounds
+activations to binary16 for its MFMA products (the rotated input in moe_prefill_router, the SwiGLU
 output in the prefill gate/up GEMMs and the shared expert); a value outside the binary16 range
 sets a flag, gm_forward then recomputes the call on GM_PATH_GENERIC (fp32 activations, the
-reference's own arithmetic), and a timed gm_run raises. Outputs must match the CPU oracle, which
-keeps every activation in fp32 (src/engine.zig:520-653)."""
+reference's own arithmetic), and a timed gm_run raises. The decode path keeps every activation in
+fp32, so the same inputs run through it directly. Outputs must match the CPU oracle, which keeps
+every activation in fp32 (src/engine.zig:520-653)."""
 import numpy as np
 import pytest
 
@@ -35,12 +36,15 @@ def test_outlier_token_recomputed_on_fp32_path(oracle_mod, layer):
         eng.add_layer(layer)
         close(oracle_mod, ref[:4], eng.forward(0, x[:4], PATH_DECODE), "decode with an outlier token")
         close(oracle_mod, ref, eng.forward(0, x, PATH_PREFILL), "prefill with an outlier token")
-        # A timed run over the same tokens refuses its outputs; the flag is then clear again.
+        # A timed prefill run over the same tokens refuses its outputs; the flag is then clear
+        # again. A timed decode run keeps fp32 activations and returns the oracle's outputs.
         eng.set_tokens(x)
         with pytest.raises(RuntimeError, match="binary16 range"):
-            eng.run(PATH_DECODE, 1, 4, [0])
-        eng.run(PATH_DECODE, 1, 3, [0])  # tokens 0..2: in range
-        close(oracle_mod, ref[:3], eng.read_outputs(3), "decode run after the refusal")
+            eng.run(PATH_PREFILL, 4, 1, [0])
+        eng.run(PATH_PREFILL, 3, 1, [0])  # tokens 0..2: in range
+        close(oracle_mod, ref[:3], eng.read_outputs(3), "prefill run after the refusal")
+        eng.run(PATH_DECODE, 1, 4, [0])
+        close(oracle_mod, ref[:4], eng.read_outputs(4), "decode run over the outlier token")
     finally:
         eng.close()
 

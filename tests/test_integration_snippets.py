@@ -88,7 +88,6 @@ def evaluate(call, ns):
 
 # The sequences: snippet blocks by the kernels they dispatch, and how a sequence combines them.
 DECODE_TQ2 = ("moe_router", "moe_decode_gu", "moe_decode_down")
-DECODE_RGU = ("moe_decode_rgu", "moe_decode_down")
 DECODE_G = ("moe_decode_gu_g", "moe_decode_down_g")
 DECODE_X = ("moe_router", "moe_decode_gu_x", "moe_decode_down_x")
 DECODE_XG = ("moe_decode_gu_xg", "moe_decode_down_xg")
@@ -102,8 +101,6 @@ PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm", "moe_prefill_gemm_s")
 def sequence(kind: str, ns):
     if kind == "decode_tq2":
         return block(*DECODE_TQ2)
-    if kind == "decode_rgu":
-        return block(*DECODE_RGU)
     if kind == "decode_g":
         # The document's rule: moe_decode_down_gl when n_used F / 128 > 64.
         gu, down = block(*DECODE_G)
@@ -129,9 +126,6 @@ def sequence(kind: str, ns):
 CASES = [
     ("decode_tq2", 2048, 512, 64, 8, 5, {"zipf": 1.1}),
     ("decode_tq2", 1024, 512, 32, 8, 8, {"signs": False}),
-    ("decode_rgu", 2048, 512, 256, 8, 1, {}),
-    ("decode_rgu", 1024, 512, 256, 8, 3, {"zipf": 1.1}),
-    ("decode_rgu", 2048, 512, 64, 8, 8, {"signs": False}),
     ("decode_g", 2560, 640, 64, 10, 3, {}),
     ("decode_g", 256, 1024, 32, 16, 2, {}),
     ("decode_x", 2048, 512, 64, 8, 4, {"mixed_types": True, "SF": 256}),
@@ -222,18 +216,13 @@ def names(L, n: int, cus: int, buffer):
     # Call buffers, each sized for nt >= n tokens (whole 64-token tiles and one more) so that no
     # kernel's tile rounding can reach past a buffer.
     nt = -(-n // 64) * 64 + 64
-    sizes = dict(x=(X_OFF + nt * E) * 4, out=(OUT_OFF + nt * E) * 4, logits=16 * nt * NE * 4, xh16=nt * E * 2,
+    sizes = dict(x=(X_OFF + nt * E) * 4, out=(OUT_OFF + nt * E) * 4, logits=16 * nt * NE * 4, xh=nt * E * 4, xh16=nt * E * 2,
                  ids=nt * U * 4, weights=nt * U * 4, gu=ns.parts * nt * U * 2 * F * 4, act=nt * U * F * 4,
                  order=nt * U * 4, meta=(1024 + 4 * (ns.tiles + 64)) * 4, act16=nt * U * F * 2,
                  down32=nt * U * E * 4, sh_h=nt * 2 * max(SF, 1) * 4, sh_g=nt * 4, x16=nt * E * 2,
                  sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4, sched=(64 + 2 * ns.tiles + 64) * 4)
     for k, v in sizes.items():
         setattr(ns, k, buffer(v, None))
-    # moe_decode_rgu: its logit words (one per 128-byte line) and error word zeroed, the first
-    # call's epoch.
-    ns.lgx = buffer(nt * NE * 128, bytes(nt * NE * 128))
-    ns.err = buffer(64, bytes(64))
-    ns.epoch, ns.spin_limit = 1, 1 << 16
     return ns
 
 
@@ -391,7 +380,6 @@ def test_snippets_replay(oracle_mod, case):
         out = dev.read(ns.out, OUT_OFF * 4, n * E * 4, np.float32).reshape(n, E)
         ids = dev.read(ns.ids, 0, n * U * 4, np.uint32).reshape(n, U)
         w = dev.read(ns.weights, 0, n * U * 4, np.float32).reshape(n, U)
-        assert dev.read(ns.err, 0, 4, np.uint32)[0] == 0, "a wait of moe_decode_rgu gave up"
     finally:
         dev.close()
 
