@@ -6,14 +6,22 @@ Workload (the decode configuration the metric is quoted on): one synthetic MoE l
 TQ2_T packed trellis weights; batch-1 decode of `--steps` tokens with fresh seeded N(0, 1)
 activations, every input resident in HBM before the timed region. A step is one token's pass
 through the layer (router and rotation, routed gate/up, SwiGLU and down rotation, down and
-combine). Four byte-identical copies of the layer are cycled so that consecutive tokens never
-find their experts in the 256 MB Infinity Cache.
+combine). Twelve byte-identical copies of the layer (2.57 GB of experts) are cycled, so that under
+uniform routing less than a tenth of a token's expert reads can find their lines still in the
+256 MB Infinity Cache. Parity is checked on at least 1000 tokens of the configuration (the timed
+tokens first) whatever --steps is.
 
 Reported beside the throughput:
   roofline      the dominant kernel (moe_decode_gu: the routed gate/up dequant-GEMV, 8 experts x
                 2 x 278,528 packed bytes per launch) timed by its own dispatch start and end
-                (gd_dispatch_timed) over a second timed pass; HBM traffic per launch from the
-                committed rocprofv3 counter summary when present.
+                (gd_dispatch_timed) over a second timed pass; beside it the kernel-trace average
+                of the committed rocprofv3 summary, HBM traffic per launch from the committed
+                counter summary, and a second roof: the codebook-gather ceiling of the decode,
+                measured in the same run by decode_gather_probe (moe_decode_gu's block dot on
+                register-resident blocks, LDS codebook gathers only): the time the launch's
+                131,072 blocks take at the chip's measured block rate.
+  mixed, stack  the mixed-quant layer and the 48-layer stack (see --mixed and --stack below), as
+                objects of the same line unless --no-mixed / --no-stack.
   cpu_baseline  the CPU oracle (a C restatement of src/engine.zig ffn and its thread pool) on a
                 bounded sample of the same tokens, on this host's cores.
   parity        rel-RMS and cosine of the GPU outputs against that CPU sample.
@@ -28,7 +36,7 @@ Reported beside the throughput:
                 packed-byte and FLOP rooflines, and the CPU oracle on a sample. Decode runs the
                 decode path's type-generic kernels, prefill the prefill path's type-generic
                 grouped GEMMs and shared-expert GEMMs.
-  prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (four cycled
+  prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (cycled
                 copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
                 and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
                 16-bit MFMA peak, for the grouped GEMMs alone and for the whole layer; the CPU
@@ -58,6 +66,10 @@ EXPERT_BYTES_PER_TOKEN = TOP_K * 3 * PROJ_BYTES  # 6,684,672
 GU_BYTES_PER_LAUNCH = TOP_K * 2 * PROJ_BYTES  # 4,456,448
 ROUTER_BYTES = N_EXPERT * E * 4  # fp32 router matrix read per layer and step
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
+TRACE_FILE = ROOT / "profiles" / "moe_decode_kernels_b1.md"
+GU_BLOCKS_PER_LAUNCH = TOP_K * 2 * F * (E // 128)  # 131,072 TQ2_T blocks of 128 weights
+CUS = 256
+PARITY_TOKENS = 1000
 GEMM_COUNTERS_FILE = ROOT / "profiles" / "moe_prefill_gemm_counters.md"
 # How the synthetic expert blocks are drawn (gyrodx.synth.random_blocks): trellis stream bytes
 # uniform; block scales binary16 with a random sign, exponent field 7..11 and a uniform mantissa.
@@ -78,6 +90,78 @@ def read_traffic():
         return None
     m = re.search(r"^bytes_per_launch:\s*(\d+)", TRAFFIC_FILE.read_text(), re.M)
     return int(m.group(1)) if m else None
+
+
+def read_trace_us(kernel: str):
+    """Average kernel-trace duration (us) of `kernel` from the committed rocprofv3 summary of the
+    decode bench (its table row `| kernel | calls | avg us | ...`), or None when absent."""
+    if not TRACE_FILE.exists():
+        return None
+    m = re.search(rf"^\|\s*{re.escape(kernel)}\s*\|\s*\d+\s*\|\s*([0-9.]+)\s*\|", TRACE_FILE.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def gather_probe(groups: int = CUS, iters: int = 256):
+    """The chip's rate of moe_decode_gu's block dot with every operand on chip (decode_gather_probe,
+    one group of 512 threads per compute unit, `iters` blocks per thread): decoded blocks per
+    second over the span from the first group's start to the last group's end (100 MHz counter),
+    the shader clock (shader-clock cycles over real-time ticks, median over groups) and blocks
+    per clock per compute unit. The second launch of two is the one measured."""
+    import ctypes as C
+    from gyrodx import CODEBOOK, KERNEL_DIR, native
+    L = native.lib()
+    opts = native.Options(0, 0, 0, 32 << 20, 1024)
+    ctx = C.c_void_p()
+    native.check(L.gd_create(C.byref(opts), C.byref(ctx)), "gd_create")
+    code = (KERNEL_DIR / "decode_gather_probe.co").read_bytes()
+    pipe = C.c_void_p()
+    native.check(L.gd_create_pipeline(ctx, code, len(code), C.byref(pipe)), "gd_create_pipeline")
+    g = np.random.default_rng(5)
+    blocks = g.integers(0, 1 << 32, (512, 9), dtype=np.uint64).astype(np.uint32)
+    blocks[:, 0] = (blocks[:, 0] & 0xFFFF0000) | 0x2800  # even blocks: scale 2^-5
+    blocks[:, 0] = (blocks[:, 0] & 0x0000FFFF) | (0x2800 << 16)  # odd blocks: the same
+    data = {"blocks": blocks.tobytes(), "book": Path(CODEBOOK).read_bytes(),
+            "x": g.standard_normal(8 * 128).astype(np.float32).tobytes(),
+            "out": bytes(8 * 4 * groups), "sums": bytes(512 * 4 * groups)}
+    bufs = {}
+    for name, raw in data.items():
+        h, info = C.c_void_p(), native.BufferInfo()
+        native.check(L.gd_create_resource(ctx, len(raw), 1, C.byref(h), C.byref(info)), "gd_create_resource")
+        C.memmove(info.mapped, raw, len(raw))
+        bufs[name] = (h, info)
+    cst = (C.c_uint32 * 6)(bufs["blocks"][1].srv_index, bufs["book"][1].srv_index, bufs["x"][1].srv_index,
+                           bufs["out"][1].uav_index, bufs["sums"][1].uav_index, iters)
+    ticket = C.c_uint64()
+    for _ in range(2):
+        native.check(L.gd_begin(ctx, 60000), "gd_begin")
+        native.check(L.gd_dispatch(ctx, pipe, cst, 6, groups, 1, 1), "gd_dispatch")
+        native.check(L.gd_submit(ctx, C.byref(ticket)), "gd_submit")
+        native.check(L.gd_wait_compute(ctx, ticket, 60000), "gd_wait_compute")
+    out = np.frombuffer(C.string_at(bufs["out"][1].mapped, 8 * 4 * groups), np.uint32).reshape(groups, 8)
+    sums = np.frombuffer(C.string_at(bufs["sums"][1].mapped, 512 * 4 * groups), np.float32)
+    for h, _ in bufs.values():
+        native.check(L.gd_release_buffer(ctx, h, 60000), "gd_release_buffer")
+    native.check(L.gd_release_pipeline(ctx, pipe, 60000), "gd_release_pipeline")
+    native.check(L.gd_destroy(ctx, 60000), "gd_destroy")
+    w = out.astype(np.uint64)
+    r0, r1, c0, c1 = (w[:, 0] | w[:, 1] << 32), (w[:, 2] | w[:, 3] << 32), (w[:, 4] | w[:, 5] << 32), (w[:, 6] | w[:, 7] << 32)
+    span_s = float(r1.max() - r0.min()) / 1e8
+    ghz = float(np.median((c1 - c0).astype(np.float64) / (r1 - r0).astype(np.float64))) * 0.1
+    blocks_per_s = groups * 512.0 * iters / span_s
+    return {"blocks_per_s": blocks_per_s, "clock_ghz": round(ghz, 3),
+            "blocks_per_clk_per_cu": round(blocks_per_s / (CUS * ghz * 1e9), 4),
+            "finite": bool(np.isfinite(sums).all())}
+
+
+def gather_roof(kernel_us: float, probe):
+    """The codebook-gather ceiling of moe_decode_gu: its launch's 131,072 blocks at the probe's
+    chip-wide block rate, and the fraction of the measured launch time that ceiling accounts for."""
+    ceiling_us = GU_BLOCKS_PER_LAUNCH / probe["blocks_per_s"] * 1e6
+    return {"bound": "lds codebook gathers", "blocks_per_launch": GU_BLOCKS_PER_LAUNCH,
+            "blocks_per_clk_per_cu": probe["blocks_per_clk_per_cu"], "clock_ghz": probe["clock_ghz"],
+            "ceiling_us": round(ceiling_us, 3), "frac": round(ceiling_us / kernel_us, 4),
+            "probe": "decode_gather_probe: moe_decode_gu's block dot, register-resident blocks and "
+                     "activations, LDS codebook gathers; one group of 512 threads per compute unit"}
 
 
 def read_gemm_counters():
@@ -166,7 +250,7 @@ def cpu_baseline(layer, tokens, gpu_out, budget_s: float, seed: int):
 
 
 def prefill_bench(eng, layer, args):
-    """1024-token prefill of the layer with a Zipf(1.1) router bias over four cycled copies;
+    """1024-token prefill of the layer with a Zipf(1.1) router bias over the cycled copies;
     `args.prefill_calls` timed calls on distinct bf16 token batches already in HBM."""
     import dataclasses
     from gyrodx import synth
@@ -506,7 +590,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--copies", type=int, default=4, help="layer copies cycled to defeat the Infinity Cache")
+    ap.add_argument("--copies", type=int, default=12, help="layer copies cycled to defeat the Infinity Cache")
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
@@ -522,6 +606,8 @@ def main() -> int:
     ap.add_argument("--coder", action="store_true",
                     help="the real model's expert shape (2560 / 640 / top-10) in TQ2_T and GGUF 148; prints its own JSON line")
     ap.add_argument("--stack-batches", default="1,8,32,64,4096", help="sweep points of --stack (of 1,8,32,64,4096)")
+    ap.add_argument("--no-mixed", action="store_true", help="leave the mixed-quant object out of the default line")
+    ap.add_argument("--no-stack", action="store_true", help="leave the 48-layer stack object out of the default line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
                          "copies of 32 MiB; prints the probe's shape and no benchmark line")
@@ -551,7 +637,8 @@ def main() -> int:
         print(json.dumps({"prefill": pre}), flush=True)
         return 0
     n_tok = args.warmup + args.steps
-    tokens = synth.make_tokens(args.seed + 1, n_tok)
+    n_par = max(args.steps, PARITY_TOKENS)  # parity tokens: the timed ones first
+    tokens = synth.make_tokens(args.seed + 1, args.warmup + n_par)
     eng = Engine(max_tok=PREFILL_TOKENS)
     layers = [eng.add_layer(layer) for _ in range(args.copies)]
     eng.set_tokens(tokens)
@@ -568,7 +655,9 @@ def main() -> int:
                           "copy_launches": 20}), flush=True)
         return 0
     dev_ms, wall_ms, _ = eng.run(PATH_DECODE, 1, args.steps, layers, first=args.warmup)
-    gpu_out = eng.read_outputs(n_tok)[args.warmup:]
+    if n_par > args.steps:  # untimed: the parity tokens past the timed ones
+        eng.run(PATH_DECODE, 1, n_par - args.steps, layers, first=n_tok)
+    gpu_out = eng.read_outputs(args.warmup + n_par)[args.warmup:]
     # Roofline pass: the same steps, the dominant kernel timed by its own dispatch start and end.
     _, _, gu_us = eng.run(PATH_DECODE, 1, args.steps, layers, bracket=2, first=args.warmup)
     _, _, down_us = eng.run(PATH_DECODE, 1, args.steps, layers, bracket=3, first=args.warmup)
@@ -577,6 +666,7 @@ def main() -> int:
     value = args.steps / (wall_ms / 1e3)
     achieved = GU_BYTES_PER_LAUNCH / (gu_us * 1e-6) / 1e9
     traffic = read_traffic()
+    trace_us = read_trace_us("moe_decode_gu")
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -599,7 +689,11 @@ def main() -> int:
                       "moe_decode_down": round(down_us, 3)},
         "roofline": {"bound": "hbm", "kernel": "moe_decode_gu", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "bytes_per_launch": GU_BYTES_PER_LAUNCH},
+                     "traffic": traffic, "bytes_per_launch": GU_BYTES_PER_LAUNCH,
+                     "dispatch_us": round(gu_us, 3), "trace_us": trace_us,
+                     "frac_trace": round(GU_BYTES_PER_LAUNCH / (trace_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                     if trace_us else None,
+                     "second_roof": gather_roof(trace_us or gu_us, gather_probe())},
     }
     if not args.no_cpu:
         line["cpu_baseline"], line["parity"] = cpu_baseline(layer, tokens[args.warmup:], gpu_out, args.cpu_budget,
@@ -610,6 +704,11 @@ def main() -> int:
             pre["cpu_baseline"], pre["parity"] = prefill_cpu(zl, px, pout)
         line["prefill"] = pre
     eng.close()
+    if not args.no_mixed:
+        line["mixed"] = mixed_bench(args)
+        print("bench: mixed-quant layer done", file=sys.stderr, flush=True)
+    if not args.no_stack:
+        line["stack"] = stack_bench(args)
     print(json.dumps(line), flush=True)
     return 0
 
