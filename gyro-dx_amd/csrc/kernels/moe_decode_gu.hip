@@ -9,7 +9,9 @@
 // (b2 + b3)) + ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook
 // and the part's 1024 fp32 activations (both into LDS, one barrier, then each lane keeps its
 // block's 128 activations in registers). Once routing names the expert, every lane loads the 9
-// words of its own block straight from HBM, so no further barrier is needed.
+// words of its own block straight from HBM. The routing runs as soon as the logits have landed and
+// the weight loads are issued before the codebook and activations go through LDS, so the expert
+// blocks' HBM latency overlaps the staging and its barrier.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
@@ -37,18 +39,12 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     // Independent loads first, all in flight together (global loads, which no LDS store orders).
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
+    __builtin_amdgcn_sched_barrier(0);  // the logits issue first: the routing waits for them only
     const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[15]))[tid];
     // Thread tid stages words 2 tid, 2 tid + 1 of the part: half (tid & 1) of chunk (tid >> 1) % 32
     // of block tid / 64.
     gd_guint *xg = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * E + part * 1024u + 2u * tid);
     const uint32_t xw0 = xg[0], xw1 = xg[1];
-    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
-    xst[0] = xw0;
-    xst[1] = xw1;
-    __syncthreads();
-    float xf[128];
-    x32_from_lds(xpart, b, xf);
 
     // Routing: this group needs the expert of rank k only, so it stops after round k; the one
     // group that records the token's ids and weights runs all rounds and forms the weights once
@@ -77,6 +73,14 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     uint32_t d[9];
 #pragma unroll
     for (int j = 0; j < 9; ++j) d[j] = w[j];
+    // Codebook and activations through LDS while the blocks are in flight.
+    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    xst[0] = xw0;
+    xst[1] = xw1;
+    __syncthreads();
+    float xf[128];
+    x32_from_lds(xpart, b, xf);
     if (writer && wave == 0u) {
         float wts[GU_U];
         rf_weights<GU_U>(top, gd_bits_f32(a.c[4]), wts);

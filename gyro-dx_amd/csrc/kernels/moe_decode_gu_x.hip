@@ -5,8 +5,10 @@
 // of wave w decodes block l % 8 of row 8 w + l / 8 and the 8-lane groups add their blocks with
 // DPP. The expert's rows and their type come from the layer's expert table (ExpertDesc); the
 // type is uniform per group, so one instantiation of the block decoder runs (gyro_fast.h), and
-// every lane loads the NW + 1 words of its own block (from the block's 4-byte-aligned start)
-// straight from HBM.
+// every lane loads its own block straight from HBM as the widest type's 15 words from the block's
+// 4-byte-aligned start (the arena's 256 bytes of slack cover the words past a row's last block).
+// As in moe_decode_gu, the routing runs as soon as the logits have landed and the blocks are
+// loaded before the codebook and activations go through LDS.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
@@ -20,20 +22,14 @@
 #define GX_ROWS 64
 #define GX_U 8
 
-// Block b of the part row at `row` (bytes): its NW + 1 words from byte (b BB) & ~3, decoded
-// against the lane's 128 fp32 activations (fp32(codebook) x activation in fp32, as
+// A block of type ID from the words d (its 4-byte-aligned start; odd: the block starts 2 bytes
+// into d[0]) against the lane's 128 fp32 activations (fp32(codebook) x activation in fp32, as
 // src/kernels.zig:185-199 multiplies the decoded fp32 weights; the block scale after the sum).
 template <int ID>
-__device__ __forceinline__ float gx_block(const uint8_t *row, uint32_t b, const uint32_t *book, const float x[128]) {
-    constexpr int BB = GyroT<ID>::BB, NW = gyro_nw<ID>();
-    const uint32_t off = b * BB;  // even
-    gd_guint *rw = gd_global(reinterpret_cast<const uint32_t *>(row + (off & ~3u)));
-    uint32_t d[NW + 1];
-#pragma unroll
-    for (int j = 0; j <= NW; ++j) d[j] = rw[j];
+__device__ __forceinline__ float gx_block(const uint32_t *d, bool odd, const uint32_t *book, const float x[128]) {
     float sc;
-    uint32_t w[NW];
-    gyro_unpack<ID>(d, (off & 2u) != 0u, sc, w);
+    uint32_t w[gyro_nw<ID>()];
+    gyro_unpack<ID>(d, odd, sc, w);
     return sc * gyro_block_dot<ID>(w, book, x);
 }
 
@@ -50,17 +46,11 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     // Independent loads first, all in flight together (global loads, which no LDS store orders).
     float lv[4];
     rf_load<4>(gd_buf<const float>(a, a.c[0]) + a.c[1] + t * NE, NE, lv);
+    __builtin_amdgcn_sched_barrier(0);  // the logits issue first: the routing waits for them only
     const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[12]))[tid];
     // Thread tid stages words 2 tid, 2 tid + 1 of the part (moe_decode_gu's layout).
     gd_guint *xg = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * E + part * 1024u + 2u * tid);
     const uint32_t xw0 = xg[0], xw1 = xg[1];
-    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
-    xst[0] = xw0;
-    xst[1] = xw1;
-    __syncthreads();
-    float xf[128];
-    x32_from_lds(xpart, b, xf);
 
     // Routing to this group's rank k only; the recording group runs every round (moe_decode_gu).
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
@@ -100,9 +90,22 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     const uint64_t addr = proj ? xt[e].up : xt[e].gate;
     const uint32_t bb = gt.block_bytes, row_bytes = E / 128u * bb;
     const uint8_t *row = reinterpret_cast<const uint8_t *>(addr) + (uint64_t)(row0 + r) * row_bytes + part * 8u * bb;
+    const uint32_t off = b * bb;  // even
+    gd_guint *rw = gd_global(reinterpret_cast<const uint32_t *>(row + (off & ~3u)));
+    uint32_t d[15];
+#pragma unroll
+    for (int j = 0; j < 15; ++j) d[j] = rw[j];
+    // Codebook and activations through LDS while the blocks are in flight.
+    reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    xst[0] = xw0;
+    xst[1] = xw1;
+    __syncthreads();
+    float xf[128];
+    x32_from_lds(xpart, b, xf);
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
     float v = 0.f;
-#define GX_CASE(ID) v = gx_block<ID>(row, b, book, xf)
+#define GX_CASE(ID) v = gx_block<ID>(d, (off & 2u) != 0u, book, xf)
     GYRO_TYPE_SWITCH(type_id, GX_CASE)
 #undef GX_CASE
     v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1

@@ -29,7 +29,8 @@
 // expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words) 18 S (0 or
 // 1: no split; plane z at logits_off + z n n_expert; the bias enters plane 0) 19 range flag
 // (table index of a word set to 1 when a value written as binary16 is outside its range; 0:
-// none).
+// none) 20 hist_uav (0: none) 21 hist_off (words) 22 hist_words: the rotation waves zero these
+// words of moe_prefill_topk's chunk histogram.
 #include "ggemm.h"
 #include "fwht.h"
 
@@ -247,6 +248,12 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
             }
         }
         gd_range_flag(a.table, a.c[19], bad);
+        // The chunk histogram that moe_prefill_topk counts into, zeroed for this call: word
+        // range of this rotation wave.
+        if (a.c[20]) {
+            uint32_t *H = gd_buf<uint32_t>(a, a.c[20]) + a.c[21];
+            for (uint32_t i = first * 64u + lane; i < a.c[22]; i += waves * 64u) H[i] = 0u;
+        }
     }
     __syncthreads();
     const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;

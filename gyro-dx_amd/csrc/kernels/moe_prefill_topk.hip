@@ -6,7 +6,9 @@
 // 1 <= n_used <= 16.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_tok 4 scale (fp32 bits) 5 ids_uav
 // 6 ids_off 7 weights_uav 8 weights_off 9 S (0 or 1: one plane) 10 plane stride (floats)
-// 11 n_used (0: 8, so that a caller passing 11 constants gets top-8).
+// 11 n_used (0: 8, so that a caller passing 11 constants gets top-8) 12 hist_uav (0: none) 13 hist_off
+// (words): every selected slot s = t n_used + k adds 1 to hist[s / 256][id] (device-scope
+// atomics; the chunk histogram moe_prefill_sort places from, zeroed beforehand by the router).
 #include "route_fast.h"
 
 GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
@@ -76,5 +78,10 @@ GD_PIPELINE_NAMED(moe_prefill_topk, 256) {
         }
         gd_buf<uint32_t>(a, a.c[5])[a.c[6] + t * U + lane] = id;
         gd_buf<float>(a, a.c[7])[a.c[8] + t * U + lane] = w;
+        if (a.c[12]) {
+            const uint32_t s = t * U + lane;
+            __hip_atomic_fetch_add(gd_buf<uint32_t>(a, a.c[12]) + a.c[13] + (s >> 8) * NE + min(id, NE - 1u), 1u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }

@@ -309,6 +309,11 @@ class Engine {
     Buffer staging, codebook, zeros;
     Buffer x_in, router_out, ids, weights, table, xh, gu, gu_part, act, down, out;
     Buffer order, meta;  // prefill: sorted slots; segment starts, tile count and tile list
+    // Prefill: per chunk of 256 slots, the slots that chose each expert ([chunk][n_expert]; the
+    // router zeroes it, the top-k counts into it, the sort places each chunk from it).
+    Buffer hist;
+    static constexpr uint32_t kSortChunk = 256;
+    uint32_t hist_words(uint32_t n) const { return (n * U + kSortChunk - 1) / kSortChunk * NE; }
     // Activation range guard: word 0 of range_flag (set by moe_prefill_router and
     // moe_prefill_shared) and word kMetaRangeFlag of meta (set by the prefill gate/up GEMMs) become
     // 1 when an activation rounded to binary16 is outside its range.
@@ -463,6 +468,8 @@ class Engine {
         out = dev.buffer(T * E * f, Kind::device);
         hn = dev.buffer(T * E * f, Kind::device);
         order = dev.buffer(T * U * 4, Kind::device);
+        hist = dev.buffer((uint64_t)hist_words(std::min<uint32_t>(max_tok, 32768u / U + 1u)) * 4, Kind::device);
+        fill_zero(hist);
         meta = dev.buffer((1024 + 4ull * max_tiles(max_tok)) * 4, Kind::device);
         fill_zero(meta);
         gemm_sched = dev.buffer((kSchedWords + 2ull * max_tiles(max_tok)) * 4ull, Kind::device);
@@ -940,14 +947,17 @@ class Engine {
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
-                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks, flag_uav()},
+                              L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks, flag_uav(), hist.uav, 0, hist_words(n)},
                              (n + 31) / 32, (NE + 31) / 32, ks);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
-                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U},
+                             {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U,
+                              hist.uav, 0},
                              (n + 3) / 4);
         const bool fused = prefill_fused && L.type_id == 144;
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
-                             {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows, fused ? gemm_sched.uav : 0u}, 1);
+                             {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows, fused ? gemm_sched.uav : 0u,
+                              hist.uav, 0},
+                             (n * U + kSortChunk - 1) / kSortChunk);
         if (fused) {
             // Both GEMMs in one persistent launch of two groups per compute unit (bracket 2).
             const bool small = use_small(n);

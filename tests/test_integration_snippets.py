@@ -211,6 +211,8 @@ def names(L, n: int, cus: int, buffer):
         S *= 2
     ns.S = S
     ns.tiles = -(-n * U // 128) + min(NE, n * U)
+    ns.n_chunks = -(-n * U // 256)
+    ns.hist_words = ns.n_chunks * NE
     ns.cus = cus
     ns.small_rows = 0 if E % 512 or F % 512 else (16 if E <= 2048 else (8 if E <= 4096 else 0))
     # Call buffers, each sized for nt >= n tokens (whole 64-token tiles and one more) so that no
@@ -219,7 +221,7 @@ def names(L, n: int, cus: int, buffer):
     sizes = dict(x=(X_OFF + nt * E) * 4, out=(OUT_OFF + nt * E) * 4, logits=16 * nt * NE * 4, xh=nt * E * 4, xh16=nt * E * 2,
                  ids=nt * U * 4, weights=nt * U * 4, gu=ns.parts * nt * U * 2 * F * 4, act=nt * U * F * 4,
                  order=nt * U * 4, meta=(1024 + 4 * (ns.tiles + 64)) * 4, act16=nt * U * F * 2,
-                 down32=nt * U * E * 4, sh_h=nt * 2 * max(SF, 1) * 4, sh_g=nt * 4, x16=nt * E * 2,
+                 down32=nt * U * E * 4, hist=(-(-nt * U // 256)) * NE * 4, sh_h=nt * 2 * max(SF, 1) * 4, sh_g=nt * 4, x16=nt * E * 2,
                  sh_a16=nt * max(SF, 1) * 2, sh_o=nt * E * 4, sched=(64 + 2 * ns.tiles + 64) * 4)
     for k, v in sizes.items():
         setattr(ns, k, buffer(v, None))
