@@ -153,6 +153,63 @@ __device__ __forceinline__ void x32_from_lds(const uint4 *xl, uint32_t b, float 
     }
 }
 
+// Rotated fp32 activations staged in LDS with one 16-byte chunk of padding per 128-block: chunk c
+// of block bx at bx * 33 + c. Block b's 128 values stay contiguous (uint4 33 b ..), so they are
+// read at constant offsets from one base, and the eight blocks that a wave's lanes read at one
+// chunk index still sit in eight different bank groups.
+__device__ __forceinline__ uint32_t x33_stage_index(uint32_t bx, uint32_t c) { return bx * 33u + c; }
+// Block's 128 values (starting at xb) into registers: x[i] = activation i of the block.
+__device__ __forceinline__ void x33_from_lds(const uint4 *xb, float x[128]) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint4 v = xb[j];
+        x[4 * j] = gd_bits_f32(v.x);
+        x[4 * j + 1] = gd_bits_f32(v.y);
+        x[4 * j + 2] = gd_bits_f32(v.z);
+        x[4 * j + 3] = gd_bits_f32(v.w);
+    }
+}
+
+// tq2_block_dot of the block whose 128 activations start at xb (LDS, the x33 layout), in two
+// halves: the 64 activations of steps 0-15 go into registers, then those of steps 16-31, so the
+// dot holds 64 of them at a time (64 VGPRs in all, against 156 for the whole block). The products
+// and their order are tq2_block_dot's, so the result is the same bit for bit.
+__device__ __forceinline__ float tq2_block_dot_halves(const uint32_t q[8], const uint32_t *book, const uint4 *xb) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float x[64];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint4 v = xb[16 * h + j];
+            x[4 * j] = gd_bits_f32(v.x);
+            x[4 * j + 1] = gd_bits_f32(v.y);
+            x[4 * j + 2] = gd_bits_f32(v.z);
+            x[4 * j + 3] = gd_bits_f32(v.w);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * h + ii;
+            const uint32_t qp = q[(i + 7) & 7];
+            const uint32_t p01 = tq2_pair01(q[i], qp), p23 = tq2_pair23(q[i]);
+            const uint32_t s[4] = {p01 & 0x7fffu, __builtin_amdgcn_ubfe(p01, 16, 15), p23 & 0x7fffu,
+                                   __builtin_amdgcn_ubfe(p23, 16, 15)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t a0, a1;
+                cb_addr(s[j], a0, a1);
+                const uint32_t w0 = lds_word(book, a0), w1 = lds_word(book, a1);
+                const float *xs = x + (ii * 4 + j) * 4;
+                acc0 = fma_lo(w0, xs[0], acc0);
+                acc1 = fma_hi(w0, xs[1], acc1);
+                acc0 = fma_lo(w1, xs[2], acc0);
+                acc1 = fma_hi(w1, xs[3], acc1);
+            }
+        }
+    }
+    return acc0 + acc1;
+}
+
 // The 9 words from the 4-byte-aligned start of the 34-byte block at byte `off` (even) of `base`.
 __device__ __forceinline__ void tq2_load_block(const uint8_t *base, uint64_t off, uint32_t d[9]) {
     gd_guint *w = gd_global(reinterpret_cast<const uint32_t *>(base + (off & ~uint64_t(3))));

@@ -7,11 +7,15 @@
 // from LDS, four v_fma_mix_f32 per step: fp32(codebook) x fp32 activation, accumulated in fp32 as
 // src/kernels.zig:161-183 does) and the 8-lane groups add their blocks with DPP ((b0 + b1) +
 // (b2 + b3)) + ((b4 + b5) + (b6 + b7)). The independent loads go first: the logits, the codebook
-// and the part's 1024 fp32 activations (both into LDS, one barrier, then each lane keeps its
-// block's 128 activations in registers). Once routing names the expert, every lane loads the 9
-// words of its own block straight from HBM. The routing runs as soon as the logits have landed and
-// the weight loads are issued before the codebook and activations go through LDS, so the expert
-// blocks' HBM latency overlaps the staging and its barrier.
+// and the part's 1024 fp32 activations. Once routing names the expert, every lane loads the 9
+// words of its own block straight from HBM; the routing runs as soon as the logits have landed.
+// The codebook and the activations then go into LDS while the blocks are in flight (one barrier),
+// so the expert blocks' HBM latency overlaps the staging.
+// Two builds of this source: moe_decode_gu (batch 1) copies the block's 128 activations into
+// registers at once, right after the barrier, so no read of them waits inside the dot (156
+// VGPRs: one group per compute unit, which batch 1's 256 groups need anyway); moe_decode_gu_b
+// (batches 2-8: 256 groups per token) reads them one half block at a time (64 VGPRs), so that
+// up to four groups share a compute unit. Both compute the same products in the same order.
 // Expert e's rows are at base + e * slot_stride (+ proj_bytes for up): no table lookup.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
@@ -23,12 +27,17 @@
 #include "fwht.h"
 #include "route_fast.h"
 
+#ifndef GU_PIPELINE
+#define GU_PIPELINE moe_decode_gu
+#define GU_HALVES 0  // 1: the block's activations read into registers one half at a time
+#endif
+#define GU_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
 #define GU_ROWS 64
 #define GU_U 8
 
-GD_PIPELINE_NAMED(moe_decode_gu, 512) {
+GU_DEFINE(GU_PIPELINE, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint4 xpart[256];  // the part's 1024 fp32 activations (x32_stage_index order)
+    __shared__ uint4 xpart[8 * 33];  // the part's 1024 fp32 activations (x33_stage_index order)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[18], F = a.c[19], n_tok = a.c[20];
     const uint32_t slot = blockIdx.z, t = slot / GU_U, k = slot - t * GU_U;
@@ -75,12 +84,14 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     for (int j = 0; j < 9; ++j) d[j] = w[j];
     // Codebook and activations through LDS while the blocks are in flight.
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x33_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
     xst[0] = xw0;
     xst[1] = xw1;
     __syncthreads();
+#if !GU_HALVES
     float xf[128];
-    x32_from_lds(xpart, b, xf);
+    x33_from_lds(xpart + b * 33u, xf);
+#endif
     if (writer && wave == 0u) {
         float wts[GU_U];
         rf_weights<GU_U>(top, gd_bits_f32(a.c[4]), wts);
@@ -99,7 +110,12 @@ GD_PIPELINE_NAMED(moe_decode_gu, 512) {
     float sc;
     uint32_t q[8];
     tq2_unpack(d, (b & 1u) != 0u, sc, q);
-    float v = sc * tq2_block_dot(q, reinterpret_cast<const uint32_t *>(book4), xf);
+    const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
+#if GU_HALVES
+    float v = sc * tq2_block_dot_halves(q, book, xpart + b * 33u);
+#else
+    float v = sc * tq2_block_dot(q, book, xf);
+#endif
     v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
     v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2
     v = v + gd_dpp_f<0x104>(v);  // row_shl:4: + lane + 4 (read by lanes b < 4)

@@ -776,7 +776,8 @@ class Engine {
         dispatch("moe_combine", {down.uav, 0, weights.uav, 0, out_uav, out_off, U, E, sh, 0, shg, 0}, (E + 255) / 256, n);
     }
 
-    // Routed experts: uniform TQ2_T layers take moe_decode_gu and moe_decode_down (E 1024 or 2048,
+    // Routed experts: uniform TQ2_T layers take moe_decode_gu (one token) or moe_decode_gu_b (2-8)
+    // and moe_decode_down (E 1024 or 2048,
     // F 512, top-8) or moe_decode_gu_g and moe_decode_down_g / _gl (E a multiple of 256 up to 4096,
     // F a multiple of 128 up to 1024, top-1..16); other layers the type-generic kernels (_x for E
     // a multiple of 1024, F 512, top-8; _xg otherwise).
@@ -858,7 +859,9 @@ class Engine {
                              std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
         if (!generic || !decode_generic_tuned()) {
             if (!generic && decode_tuned_tq2()) {
-                dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu",
+                // One token: the build that holds a block's activations in registers at once;
+                // more: the half-block build, which lets four groups share a compute unit.
+                dispatch_maybe_timed(bracket == 2, marks, n == 1 ? "moe_decode_gu" : "moe_decode_gu_b",
                                      {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh,
                                       B.xh_off, base_lo, base_hi, slot_stride, L.gate_bytes, codebook.srv, B.gu, B.gu_off, E, F, n},
                                      F / 64, 2 * parts, n * U);

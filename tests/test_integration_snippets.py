@@ -100,7 +100,11 @@ PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm", "moe_prefill_gemm_s")
 
 def sequence(kind: str, ns):
     if kind == "decode_tq2":
-        return block(*DECODE_TQ2)
+        # The document's rule: moe_decode_gu_b, same constants and grid, for 2 to 8 tokens.
+        router, gu, down = block(*DECODE_TQ2)
+        if ns.n > 1:
+            gu = ("moe_decode_gu_b",) + gu[1:]
+        return [router, gu, down]
     if kind == "decode_g":
         # The document's rule: moe_decode_down_gl when n_used F / 128 > 64.
         gu, down = block(*DECODE_G)
