@@ -487,14 +487,13 @@ def mixed_bench(args):
     pout = eng.read_outputs(512)
     us = {}
     for name, br in (("moe_prefill_router", 1), ("moe_prefill_topk", 4), ("moe_prefill_sort", 5),
-                     ("moe_prefill_gu_x", 2), ("moe_prefill_down_x", 3), ("moe_prefill_shared gate/up", 7),
+                     ("moe_prefill_gemm_x (gate/up + down, one launch)", 2), ("moe_prefill_shared gate/up", 7),
                      ("moe_prefill_shared down", 8), ("moe_prefill_combine", 6)):
         us[name] = round(eng.run(PATH_PREFILL, 512, calls, ids, bracket=br, first=0)[2], 3)
     call_s = wall_ms / calls * 1e-3
     dev_s = dev_ms / calls * 1e-3
     flops = 512 * (LAYER_FLOPS_PER_TOKEN + 3 * 2 * E * SHARED_F)
-    res["prefill"] = {"path": "prefill (router, top-k, sort, moe_prefill_gu_x, moe_prefill_down_x, "
-                              "moe_prefill_shared x2, combine)",
+    res["prefill"] = {"path": "prefill (router, top-k, sort, moe_prefill_gemm_x, moe_prefill_shared x2, combine)",
                       "tokens": 512, "calls": calls, "tok_s": round(512 / call_s, 1),
                       "us_per_call": round(call_s * 1e6, 2), "device_us_per_call": round(dev_s * 1e6, 2),
                       "kernel_us": us, "flops_per_call": flops, "tflops": round(flops / dev_s / 1e12, 2),
@@ -566,7 +565,7 @@ def coder_bench(args):
         flops = PREFILL_TOKENS * cU * 3 * 2 * cE * cF
         dev_s = pdev / calls * 1e-3
         pus = {}
-        one = type_id == 144 and os.environ.get("GYRO_PREFILL_FUSED", "1") != "0"  # TQ2_T: one GEMM launch
+        one = os.environ.get("GYRO_PREFILL_FUSED", "1") != "0"  # one GEMM launch (moe_prefill_gemm or _x)
         gemms = (("gate/up + down (one launch)", 2),) if one else (("gate/up", 2), ("down", 3))
         for name, br in (("router", 1), ("topk", 4), ("sort", 5), *gemms, ("combine", 6)):
             pus[name] = round(eng.run(PATH_PREFILL, PREFILL_TOKENS, calls, ids, bracket=br, first=0)[2], 3)

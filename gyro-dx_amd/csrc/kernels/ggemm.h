@@ -350,8 +350,9 @@ __device__ __forceinline__ void gx_run(GxLds &sm, const GxState &t, uint32_t typ
 //     at K-step s holds H[16 s + 8 h + e][j] for e = 0..7, the lane's fixed pattern
 //     (-1)^popcount(e & j) times (-1)^popcount((16 s + 8 h) & j). Scaled rows go to activation
 //     buffer 0 (same layout).
-// (4) Rows of 128 binary16 values (16 swizzled chunks) to out[row0 + i][fb * 128 ..].
-template <class LDS, int NRB>
+// (4) Rows of 128 binary16 values (16 swizzled chunks) to out[row0 + i][fb * 128 ..]; COHERENT:
+//     as device-scope stores, for readers on other XCDs within the same launch.
+template <class LDS, int NRB, bool COHERENT = false>
 __device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB], uint32_t wave, uint32_t m,
                                                uint32_t h, const float *signs, uint32_t *out, uint32_t row0,
                                                uint32_t rows, uint32_t fb, uint32_t F, uint32_t *flag) {
@@ -413,8 +414,16 @@ __device__ __forceinline__ void gg_gu_epilogue(LDS &sm, const f32x16 (&acc)[NRB]
     const gd_u32x4 *rows_src = signs ? &sm.a[0][0] : &sm.a[2][0];
     for (uint32_t idx = threadIdx.x; idx < rows * 16u; idx += 512u) {
         const uint32_t i = idx >> 4, c = idx & 15u;
-        *reinterpret_cast<gd_u32x4 *>(out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u) =
-            rows_src[i * 16u + (c ^ (i & 15u))];
+        const gd_u32x4 v = rows_src[i * 16u + (c ^ (i & 15u))];
+        uint32_t *dst = out + (size_t)(row0 + i) * (F / 2u) + fb * 64u + c * 4u;
+        if constexpr (COHERENT) {
+            __attribute__((address_space(1))) uint64_t *d =
+                (__attribute__((address_space(1))) uint64_t *)(uintptr_t)dst;
+            __hip_atomic_store(d, (uint64_t)v[0] | ((uint64_t)v[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(d + 1, (uint64_t)v[2] | ((uint64_t)v[3] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            *reinterpret_cast<gd_u32x4 *>(dst) = v;
+        }
     }
 }
 

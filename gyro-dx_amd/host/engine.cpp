@@ -272,8 +272,9 @@ class Engine {
     // Compute units of the device (the persistent GEMM's two groups per unit, the decode
     // kernels' target group count).
     uint32_t cus = 0;
-    // Prefill GEMMs of uniform TQ2_T layers: one persistent launch over both (moe_prefill_gemm)
-    // unless the environment sets GYRO_PREFILL_FUSED=0 (then moe_prefill_gu and moe_prefill_down);
+    // Prefill GEMMs: one persistent launch over both (moe_prefill_gemm for uniform TQ2_T layers,
+    // moe_prefill_gemm_x for the others) unless the environment sets GYRO_PREFILL_FUSED=0 (then
+    // moe_prefill_gu and moe_prefill_down, or moe_prefill_gu_x and moe_prefill_down_x);
     // the polls a down unit makes for a ready tile before it gives up (GYRO_PREFILL_SPIN_LIMIT,
     // default 2^20); its queue words, give-up word, tile counters and ready list.
     bool prefill_fused = true;
@@ -812,7 +813,7 @@ class Engine {
         explicit UnfusedPrefillScope(Engine *eng) : e(eng), was(eng->prefill_fused) { e->prefill_fused = false; }
         ~UnfusedPrefillScope() { e->prefill_fused = was; }
     };
-    // Reads and clears the give-up word of moe_prefill_gemm: set when a down unit stopped waiting
+    // Reads and clears the give-up word of the persistent GEMMs: set when a down unit stopped waiting
     // for its tile's gate/up rows (the call's outputs are then invalid).
     bool take_gemm_error() {
         if (!gemm_sched.handle) return false;
@@ -927,7 +928,7 @@ class Engine {
     bool prefill_on_generic(const Layer &L) const { return prefill_shape_ok(L) && !prefill_range_ok(L); }
 
     // MI355X prefill path: router GEMM + rotation, top-k, counting sort, grouped gate/up and
-    // down GEMMs (one persistent launch for uniform TQ2_T layers), shared expert, combine.
+    // down GEMMs (one persistent launch), shared expert, combine.
     // bracket: 1 router, 2 gate/up (the persistent launch: both GEMMs), 3 down (none with the
     // persistent launch), 4 top-k, 5 sort, 6 combine, 7 shared gate/up, 8 shared down.
     void ffn_prefill(uint32_t il, uint32_t n, uint32_t x_uav, uint32_t x_off, uint32_t out_uav, uint32_t out_off,
@@ -956,12 +957,19 @@ class Engine {
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U,
                               hist.uav, 0},
                              (n + 3) / 4);
-        const bool fused = prefill_fused && L.type_id == 144;
+        const bool fused = prefill_fused;  // both GEMMs in one persistent launch
         dispatch_maybe_timed(bracket == 5, marks, "moe_prefill_sort",
                              {ids.uav, 0, n * U, NE, order.uav, 0, meta.uav, kTileRows, fused ? gemm_sched.uav : 0u,
                               hist.uav, 0},
                              (n * U + kSortChunk - 1) / kSortChunk);
-        if (fused) {
+        if (fused && L.type_id != 144) {
+            // Layers of other or mixed types: one persistent launch of one group per compute unit
+            // (152.5 KB of LDS; bracket 2).
+            dispatch_maybe_timed(bracket == 2, marks, "moe_prefill_gemm_x",
+                                 {meta.uav, order.uav, 0, xh.uav, 0, L.xtab.srv, codebook.srv, signs, E, act.uav, 0, E,
+                                  F, U, 1u, down.uav, 0, gemm_sched.uav, prefill_spin_limit},
+                                 cus_or(256));
+        } else if (fused) {
             // Both GEMMs in one persistent launch of two groups per compute unit (bracket 2).
             const bool small = use_small(n);
             dispatch_maybe_timed(bracket == 2, marks, small ? "moe_prefill_gemm_s" : "moe_prefill_gemm",

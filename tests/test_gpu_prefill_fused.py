@@ -10,6 +10,12 @@ down row, top-10), the widest hidden (4096, sixteen down units per tile) with to
 top-6, and batches of 1 and 33 tokens (one and a few tiles). The forced give-up (a spin limit of
 zero polls) must leave gm_forward's result unchanged: the call is recomputed with two launches.
 
+moe_prefill_gemm_x is the same queue over the type-generic units (moe_prefill_gu_x,
+moe_prefill_down_x) for layers whose experts and projections mix Gyro types or use one type other
+than TQ2_T: against its two launches bit for bit and against the oracle, on the mixed-quant layer
+with its bf16 shared expert, the real model's expert shape in GGUF 148 with a Zipf router, and a
+mixed layer at F 384 / top-6; its forced give-up is recomputed as above.
+
 moe_prefill_gemm_s is the same launch with small-tile units for sort tiles of at most 16 rows (8
 past hidden 2048); the engine takes it when the average expert segment is short (tokens x top-k
 at most 8 x experts) and the shape has them (hidden and F multiples of 512, hidden at most 4096).
@@ -164,3 +170,70 @@ def test_small_units_match(oracle_mod, E, F, NE, U, n, kw):
     r, c = oracle_mod.rel_rms(ref, outs["moe_prefill_gemm_s"]), oracle_mod.cosine(ref, outs["moe_prefill_gemm_s"])
     print(f"  bit-equal; rel_rms {r:.3e} cosine {c:.8f}", flush=True)
     assert r <= REL_RMS and c >= COSINE
+
+
+X_SHAPES = [
+    # E, F, experts, top-k, tokens, extra make_layer arguments
+    (2048, 512, 256, 8, 512, {"mixed_types": True, "SF": 1024}),
+    (2560, 640, 64, 10, 300, {"type_id": 148, "zipf": 1.1}),
+    (1024, 384, 32, 6, 100, {"mixed_types": True, "signs": False}),
+    (1024, 256, 32, 4, 1, {"type_id": 151}),
+]
+
+
+@pytest.mark.parametrize("E,F,NE,U,n,kw", X_SHAPES,
+                         ids=[f"E{s[0]}-F{s[1]}-x{s[2]}-top{s[3]}-n{s[4]}" + "".join(f"-{k}{v}" for k, v in s[5].items())
+                              for s in X_SHAPES])
+def test_persistent_gemm_x_matches_two_launches(oracle_mod, E, F, NE, U, n, kw):
+    L = synth.make_layer(1700 + E // 128 + F // 64 + U, E=E, F=F, n_expert=NE, n_used=U, **kw)
+    x = synth.make_tokens(1701 + n, n, E, bf16=True)
+    outs = {}
+    for fused in (True, False):
+        eng = make_engine(max(n, 64), fused)
+        try:
+            eng.add_layer(L)
+            print(f"prefill E={E} F={F} experts={NE} top-{U} n={n} {kw} "
+                  f"{'moe_prefill_gemm_x' if fused else 'moe_prefill_gu_x + moe_prefill_down_x'}", flush=True)
+            outs[fused] = eng.forward(0, x, PATH_PREFILL)
+        finally:
+            eng.close()
+    np.testing.assert_array_equal(outs[True].view(np.uint32), outs[False].view(np.uint32))
+    ref = oracle_mod.OracleLayer(L).forward(x)
+    r, c = oracle_mod.rel_rms(ref, outs[True]), oracle_mod.cosine(ref, outs[True])
+    print(f"  bit-equal to the two-launch path; rel_rms {r:.3e} cosine {c:.8f}", flush=True)
+    assert r <= REL_RMS and c >= COSINE
+
+
+def test_persistent_gemm_x_give_up_recomputes():
+    """moe_prefill_gemm_x with a spin limit of zero polls: gm_forward recomputes with the two
+    type-generic launches and returns their outputs bit for bit; gm_run over two calls either
+    reports the give-up or returns the two-launch run's outputs bit for bit."""
+    n = 512
+    L = synth.make_layer(1760, mixed_types=True, zipf=1.1)
+    x = synth.make_tokens(1761, 2 * n, bf16=True)
+    ref_eng = make_engine(n, False)
+    try:
+        ref_eng.add_layer(L)
+        ref = ref_eng.forward(0, x[:n], PATH_PREFILL)
+        ref_eng.set_tokens(x)
+        ref_eng.run(PATH_PREFILL, n, 2, [0])
+        ref_run = ref_eng.read_outputs(2 * n)
+    finally:
+        ref_eng.close()
+    eng = make_engine(n, True, spin_limit=0)
+    try:
+        eng.add_layer(L)
+        print("moe_prefill_gemm_x, spin limit 0: gm_forward", flush=True)
+        out = eng.forward(0, x[:n], PATH_PREFILL)
+        np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+        eng.set_tokens(x)
+        try:
+            eng.run(PATH_PREFILL, n, 2, [0])
+            got = eng.read_outputs(2 * n)
+            np.testing.assert_array_equal(got.view(np.uint32), ref_run.view(np.uint32))
+            print("  gm_run: no unit gave up; outputs equal the two-launch run", flush=True)
+        except RuntimeError as err:
+            assert "gave up waiting" in str(err), err
+            print("  gm_run reported the give-up", flush=True)
+    finally:
+        eng.close()

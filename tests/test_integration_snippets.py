@@ -96,6 +96,7 @@ PREFILL = ("moe_prefill_router", "moe_prefill_topk", "moe_prefill_sort", "moe_pr
 PREFILL_X = ("moe_prefill_gu_x", "moe_prefill_down_x")
 PREFILL_SH = ("moe_prefill_router", "moe_prefill_shared", "moe_prefill_shared", "moe_prefill_combine")
 PREFILL_ONE = ("moe_prefill_sort", "moe_prefill_gemm", "moe_prefill_gemm_s")
+PREFILL_ONE_X = ("moe_prefill_sort", "moe_prefill_gemm_x")
 
 
 def sequence(kind: str, ns):
@@ -119,6 +120,13 @@ def sequence(kind: str, ns):
     if kind in ("prefill_gemm", "prefill_gemm_s"):  # the sort with the queue buffer, both GEMMs in one launch
         sort, gemm, gemm_s = block(*PREFILL_ONE)
         return [*p[:2], sort, gemm_s if kind == "prefill_gemm_s" else gemm, p[5]]
+    if kind == "prefill_gemm_x":  # the type-generic pair in one launch, the sort with the queue buffer
+        sort, gemm = block(*PREFILL_ONE_X)
+        mid = [gemm]
+        if ns.SF:
+            sh = block(*PREFILL_SH)
+            return [sh[0], p[1], sort, *mid, *sh[1:]]
+        return [*p[:2], sort, *mid, p[5]]
     mid = block(*PREFILL_X) if ns.mixed else p[3:5]
     if ns.SF:
         sh = block(*PREFILL_SH)
@@ -145,6 +153,9 @@ CASES = [
     ("prefill_gemm", 2560, 640, 64, 10, 70, {"zipf": 1.1}),
     ("prefill_gemm_s", 2048, 512, 256, 8, 40, {}),
     ("prefill_gemm_s", 4096, 1024, 64, 6, 9, {"signs": False}),
+    ("prefill_gemm_x", 1024, 384, 32, 6, 50, {"mixed_types": True}),
+    ("prefill_gemm_x", 2560, 640, 64, 10, 70, {"mixed_types": True, "zipf": 1.1}),
+    ("prefill_gemm_x", 1024, 256, 16, 4, 30, {"mixed_types": True, "SF": 128, "signs": False}),
 ]
 IDS = [f"{c[0]}-E{c[1]}-F{c[2]}-x{c[3]}-top{c[4]}-n{c[5]}" + "".join(f"-{k}" for k in c[6]) for c in CASES]
 
