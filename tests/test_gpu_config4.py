@@ -11,8 +11,14 @@ near-tie in the top-8), so each layer is checked teacher-forced: it receives the
 residual stream x_l, the stack path computes x_l + MoE_l(RMSNorm_l(x_l)) through gm_forward_stack
 on that one layer, and its MoE contribution is compared with the oracle's to rel-RMS 2e-3 and
 cosine 0.9999 over the tokens whose routing at that layer is separable (8th/9th fp64 probability
-gap above 1e-5 relative). Decode at batch 1 and 8, prefill at batch 64; gm_run_stack over all 48
-layers equals gm_forward_stack bit for bit.
+gap above 1e-5 relative). Decode at batch 1 and 8, prefill at batch 32 (the small-tile GEMM
+launch) and 64; gm_run_stack over all 48 layers equals gm_forward_stack bit for bit.
+
+The sweep's 4096-token prefill (32,768 slots per layer, the largest call) is checked on the GPU's
+own stream: one gm_forward_stack over all 48 layers must equal the 48 one-layer calls chained on
+the GPU's outputs bit for bit, and at every layer the MoE contribution of 64 sampled tokens must
+match the oracle's layer computed from that same stream (the oracle on all 4096 tokens x 48 layers
+would take minutes; each token's result depends on its own row only).
 """
 import numpy as np
 import pytest
@@ -28,7 +34,7 @@ N_LAYERS = 48
 def stack48():
     print("config 4: generating 48 layers", flush=True)
     layers = synth.make_stack(4900, N_LAYERS)
-    eng = Engine(max_tok=64)
+    eng = Engine(max_tok=4096)
     print("config 4: uploading 10.27 GB of experts", flush=True)
     ids = [eng.add_layer(L) for L in layers]
     assert ids == list(range(N_LAYERS))
@@ -82,6 +88,37 @@ def test_stack48_decode_batch1_and_8(oracle_mod, stack48):
 def test_stack48_prefill_batch64(oracle_mod, stack48):
     layers, eng = stack48
     teacher_forced(oracle_mod, layers, eng, PATH_PREFILL, 64, 4903, "stack48 prefill n=64")
+
+
+def test_stack48_prefill_batch32(oracle_mod, stack48):
+    layers, eng = stack48
+    teacher_forced(oracle_mod, layers, eng, PATH_PREFILL, 32, 4905, "stack48 prefill n=32")
+
+
+def test_stack48_prefill_4096(oracle_mod, stack48):
+    layers, eng = stack48
+    n = 4096
+    x = synth.make_tokens(4906, n, bf16=True)
+    print("stack48 prefill n=4096: one call over 48 layers", flush=True)
+    full = eng.forward_stack(list(range(N_LAYERS)), x, PATH_PREFILL)
+    idx = np.arange(0, n, n // 64)
+    cur = np.ascontiguousarray(x, np.float32)
+    worst_r, worst_c, excluded = 0.0, 1.0, 0
+    for l, L in enumerate(layers):
+        nxt = eng.forward_stack([l], cur, PATH_PREFILL)
+        xs = cur[idx]
+        got = nxt[idx].astype(np.float64) - xs.astype(np.float64)
+        ref = oracle_mod.OracleLayer(L).forward(oracle_mod.rms_norm(xs, L.norm_weight, L.norm_eps))
+        sep = separable(oracle_mod, L, xs)
+        excluded += int((~sep).sum())
+        r, c = oracle_mod.rel_rms(ref[sep], got[sep]), oracle_mod.cosine(ref[sep], got[sep])
+        worst_r, worst_c = max(worst_r, r), min(worst_c, c)
+        assert r <= 2e-3 and c >= 0.9999, ("stack48 prefill n=4096", l, r, c)
+        cur = nxt
+    np.testing.assert_array_equal(full.view(np.uint32), cur.view(np.uint32))
+    print(f"stack48 prefill n=4096: one call equals 48 chained calls; 64 sampled tokens per layer, worst "
+          f"rel_rms={worst_r:.3e} worst cosine={worst_c:.8f}, {excluded} token-layers near a routing tie "
+          f"excluded", flush=True)
 
 
 def test_stack48_reference_path_far_arena(oracle_mod, stack48):
