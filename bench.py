@@ -20,8 +20,10 @@ Reported beside the throughput:
                 measured in the same run by decode_gather_probe (moe_decode_gu's block dot on
                 register-resident blocks, LDS codebook gathers only): the time the launch's
                 131,072 blocks take at the chip's measured block rate.
-  mixed, stack  the mixed-quant layer and the 48-layer stack (see --mixed and --stack below), as
-                objects of the same line unless --no-mixed / --no-stack.
+  mixed, stack, coder
+                the mixed-quant layer, the 48-layer stack and the real model's expert shape (see
+                --mixed, --stack and --coder below), as objects of the same line unless
+                --no-mixed / --no-stack / --no-coder.
   cpu_baseline  the CPU oracle (a C restatement of src/engine.zig ffn and its thread pool) on a
                 bounded sample of the same tokens, on this host's cores.
   parity        rel-RMS and cosine of the GPU outputs against that CPU sample.
@@ -35,7 +37,11 @@ Reported beside the throughput:
                 width 1024; batch-1 decode and a 512-token prefill, with
                 packed-byte and FLOP rooflines, and the CPU oracle on a sample. Decode runs the
                 decode path's type-generic kernels, prefill the prefill path's type-generic
-                grouped GEMMs and shared-expert GEMMs.
+                grouped GEMMs (one persistent launch) and shared-expert GEMMs.
+  --coder       (its own JSON line) the real model's routed-expert shape, hidden 2560, 256
+                experts, top-10, F 640, in TQ2_T and in GGUF 148: batch-1 decode over cycled layer
+                copies and a 1024-token prefill, with rooflines, and decode parity with the oracle
+                on 16 tokens.
   prefill       1024-token prefill of the same layer with a Zipf(1.1) router bias (cycled
                 copies, distinct bf16 N(0, 1) token batches): tok/s, per-kernel dispatch times,
                 and routed-expert FLOPs (51,539,607,552 per call) against the 2.5 PFLOP/s dense
@@ -607,6 +613,7 @@ def main() -> int:
     ap.add_argument("--stack-batches", default="1,8,32,64,4096", help="sweep points of --stack (of 1,8,32,64,4096)")
     ap.add_argument("--no-mixed", action="store_true", help="leave the mixed-quant object out of the default line")
     ap.add_argument("--no-stack", action="store_true", help="leave the 48-layer stack object out of the default line")
+    ap.add_argument("--no-coder", action="store_true", help="leave the real-model shape object out of the default line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for counter passes: the warm-up and timed decode steps, then 20 calibration "
                          "copies of 32 MiB; prints the probe's shape and no benchmark line")
@@ -708,6 +715,9 @@ def main() -> int:
         print("bench: mixed-quant layer done", file=sys.stderr, flush=True)
     if not args.no_stack:
         line["stack"] = stack_bench(args)
+        print("bench: 48-layer stack done", file=sys.stderr, flush=True)
+    if not args.no_coder:
+        line["coder"] = coder_bench(args)
     print(json.dumps(line), flush=True)
     return 0
 
