@@ -60,8 +60,8 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
 // Dot of one TQ2_T block's 32 steps with 128 activations, given the 8 stream words; returns
-// the unscaled sum of codebook * x. X is either a uniform cfloat* (scalar loads) or an LDS
-// pointer.
+// the unscaled sum of codebook * x. X is a uniform cfloat* (scalar loads), an LDS pointer or a
+// register array.
 template <typename XP>
 __device__ __forceinline__ float tq2_block_dot(const uint32_t q[8], const uint32_t *book, XP x) {
     float acc0 = 0.f, acc1 = 0.f;
@@ -108,30 +108,6 @@ __device__ __forceinline__ float tq2_half_dot(const uint32_t q[8], uint32_t half
             acc1 = fma_hi(w0, xs[1], acc1);
             acc0 = fma_lo(w1, xs[2], acc0);
             acc1 = fma_hi(w1, xs[3], acc1);
-        }
-    }
-    return acc0 + acc1;
-}
-
-// As tq2_block_dot with activations as 64 packed binary16 pairs held in scalar registers
-// (xs[2t] = x[4t], x[4t+1]; xs[2t+1] = x[4t+2], x[4t+3]): two v_dot2_f32_f16 per step, fp32
-// accumulation of exact fp16 products.
-__device__ __forceinline__ float tq2_block_dot_h(const uint32_t q[8], const uint32_t *book, const uint32_t xs[64]) {
-    float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t qp = q[(i + 7) & 7];
-        const uint32_t p01 = tq2_pair01(q[i], qp), p23 = tq2_pair23(q[i]);
-        const uint32_t s[4] = {p01 & 0x7fffu, __builtin_amdgcn_ubfe(p01, 16, 15), p23 & 0x7fffu,
-                               __builtin_amdgcn_ubfe(p23, 16, 15)};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t a0, a1;
-            cb_addr(s[j], a0, a1);
-            const uint32_t w0 = lds_word(book, a0), w1 = lds_word(book, a1);
-            const int st = i * 4 + j;
-            acc0 = __builtin_amdgcn_fdot2(as_half2(w0), as_half2(xs[2 * st]), acc0, false);
-            acc1 = __builtin_amdgcn_fdot2(as_half2(w1), as_half2(xs[2 * st + 1]), acc1, false);
         }
     }
     return acc0 + acc1;
@@ -274,38 +250,10 @@ __device__ __forceinline__ uint32_t gyro_kstate(const uint32_t (&w)[gyro_nw<ID>(
     return __builtin_amdgcn_alignbit(w[i1], w[i], (uint32_t)(off & 31)) & 0x7fffu;
 }
 
-// Unscaled dot of one block with its activations held as binary16 pairs in xs (pair j =
-// elements 2j, 2j+1): 32-step types give two codebook pairs per step (weights 4t .. 4t+3),
-// 64-step types one (weights 2t, 2t+1).
-template <int ID>
-__device__ __forceinline__ float gyro_block_dot_h(const uint32_t (&w)[gyro_nw<ID>()], const uint32_t *book,
-                                                  const uint32_t xs[64]) {
-    if constexpr (ID == 144) {
-        return tq2_block_dot_h(w, book, xs);
-    } else {
-        float acc0 = 0.f, acc1 = 0.f;
-        if constexpr (GyroT<ID>::S == 32) {
-#pragma unroll
-            for (int t = 0; t < 32; ++t) {
-                uint32_t a0, a1;
-                cb_addr(gyro_kstate<ID>(w, t), a0, a1);
-                acc0 = __builtin_amdgcn_fdot2(as_half2(lds_word(book, a0)), as_half2(xs[2 * t]), acc0, false);
-                acc1 = __builtin_amdgcn_fdot2(as_half2(lds_word(book, a1)), as_half2(xs[2 * t + 1]), acc1, false);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 64; t += 2) {
-                const uint32_t b0 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t)));
-                const uint32_t b1 = lds_word(book, cb_addr0(gyro_kstate<ID>(w, t + 1)));
-                acc0 = __builtin_amdgcn_fdot2(as_half2(b0), as_half2(xs[t]), acc0, false);
-                acc1 = __builtin_amdgcn_fdot2(as_half2(b1), as_half2(xs[t + 1]), acc1, false);
-            }
-        }
-        return acc0 + acc1;
-    }
-}
-
-// As gyro_block_dot_h with fp32 activations x[128] (an LDS or uniform pointer).
+// Unscaled dot of one block with its 128 fp32 activations x (an LDS, register or uniform
+// pointer): fp32(codebook value) x fp32 activation, accumulated in fp32 (v_fma_mix_f32).
+// 32-step types give two codebook pairs per step (weights 4t .. 4t+3), 64-step types one
+// (weights 2t, 2t+1).
 template <int ID, typename XP>
 __device__ __forceinline__ float gyro_block_dot(const uint32_t (&w)[gyro_nw<ID>()], const uint32_t *book, XP x) {
     if constexpr (ID == 144) {

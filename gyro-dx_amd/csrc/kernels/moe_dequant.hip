@@ -1,7 +1,7 @@
 // Dequantises rows of one expert projection with the decoders the fast paths run, so tests can
 // compare them bit for bit with the strict decoder (src/gyro.zig:81-105), for every Gyro type:
 //   mode 0: the decode path's block decoders (tq2_unpack and the TQ2_T state pairs of
-//           tq2_block_dot_h; gyro_unpack and gyro_kstate of gyro_block_dot_h), fp32 scale x
+//           tq2_block_dot; gyro_unpack and gyro_kstate of gyro_block_dot), fp32 scale x
 //           codebook value;
 //   mode 1: the prefill GEMMs' B-operand decoders (gg_gather for TQ2_T; gx_half_stream and
 //           gx_gather_piece for the k-bit types), lane half h giving k = 16 s + 8 h .. + 7 of
