@@ -139,6 +139,14 @@ __device__ __forceinline__ gd_gu32x4 *gd_global4(const uint32_t *p) { return (gd
 // accesses across it.
 __device__ __forceinline__ void gd_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// v as rounded to fp32, opaque to the compiler: a product passed through it is not fused with a
+// later add. (Under fp-contract=fast the compiler may turn `v = a * b; v + w` into fma(a, b, w)
+// in one build of a kernel and not in another, which changes the last bits of the sum.)
+__device__ __forceinline__ float gd_rounded(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // Activation range guard: an activation rounded to binary16 must be finite and at most 65504 in
 // magnitude (false for NaN and infinities). A kernel that rounds one outside stores 1 to the
 // flag word at table index `flag` (0: no flag); the host reads it and recomputes on the fp32 path.

@@ -163,8 +163,8 @@ GD_PIPELINE_NAMED(moe_decode_down, 512) {
     float sc;
     uint32_t q[8];
     tq2_unpack(d, (off & 2u) != 0u, sc, q);
-    float sum = sc * tq2_half_dot(q, hf, reinterpret_cast<const uint32_t *>(book4),
-                                  act + (k * DN_NB + bb) * DN_BLOCK_STRIDE + 64u * hf);
+    float sum = gd_rounded(sc * tq2_half_dot(q, hf, reinterpret_cast<const uint32_t *>(book4),
+                                             act + (k * DN_NB + bb) * DN_BLOCK_STRIDE + 64u * hf));
     sum = sum + gd_dpp_f<0xB1>(sum);   // the two halves of a block
     sum = sum + gd_dpp_f<0x4E>(sum);   // b0 + b1, b2 + b3
     sum = sum + gd_dpp_f<0x104>(sum);  // row_shl:4: (b0 + b1) + (b2 + b3) in lane 8 k

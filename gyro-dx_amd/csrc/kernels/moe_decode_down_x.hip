@@ -45,7 +45,7 @@ __device__ __forceinline__ float dx_unit(const uint32_t *rows_k, uint32_t r, uin
     float sc;
     uint32_t w[NW];
     gyro_unpack<ID>(d, (off & 2u) != 0u, sc, w);
-    return sc * gyro_block_dot<ID>(w, book, x);
+    return gd_rounded(sc * gyro_block_dot<ID>(w, book, x));
 }
 
 GD_PIPELINE_NAMED(moe_decode_down_x, 512) {

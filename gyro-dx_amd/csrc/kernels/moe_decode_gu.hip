@@ -112,9 +112,9 @@ GU_DEFINE(GU_PIPELINE, 512) {
     tq2_unpack(d, (b & 1u) != 0u, sc, q);
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
 #if GU_HALVES
-    float v = sc * tq2_block_dot_halves(q, book, xpart + b * 33u);
+    float v = gd_rounded(sc * tq2_block_dot_halves(q, book, xpart + b * 33u));
 #else
-    float v = sc * tq2_block_dot(q, book, xf);
+    float v = gd_rounded(sc * tq2_block_dot(q, book, xf));
 #endif
     v = v + gd_dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: + lane ^ 1
     v = v + gd_dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: + lane ^ 2

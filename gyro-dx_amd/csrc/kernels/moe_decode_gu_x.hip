@@ -8,7 +8,10 @@
 // every lane loads its own block straight from HBM as the widest type's 15 words from the block's
 // 4-byte-aligned start (the arena's 256 bytes of slack cover the words past a row's last block).
 // As in moe_decode_gu, the routing runs as soon as the logits have landed and the blocks are
-// loaded before the codebook and activations go through LDS.
+// loaded before the codebook and activations go through LDS. Two builds of this source, as for
+// moe_decode_gu: moe_decode_gu_x (batch 1) copies the block's 128 activations into registers at
+// once; moe_decode_gu_xb (batches 2-8) reads them from LDS step by step, with fewer VGPRs, so
+// that several groups share a compute unit. Both compute the same products in the same order.
 // Grid: x = F / 64, y = 2 * parts (projection-major), z = n_tok * 8; 512 threads.
 // Output partials gu[part][slot][proj][F]; the down kernel adds the parts.
 // Constants: 0 logits_uav 1 logits_off 2 n_expert 3 n_used (8) 4 scale (fp32 bits) 5 ids_uav
@@ -19,23 +22,28 @@
 #include "fwht.h"
 #include "route_fast.h"
 
+#ifndef GX_PIPELINE
+#define GX_PIPELINE moe_decode_gu_x
+#define GX_STEPWISE 0  // 1: the block dot reads the activations from LDS step by step
+#endif
+#define GX_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
 #define GX_ROWS 64
 #define GX_U 8
 
 // A block of type ID from the words d (its 4-byte-aligned start; odd: the block starts 2 bytes
 // into d[0]) against the lane's 128 fp32 activations (fp32(codebook) x activation in fp32, as
 // src/kernels.zig:185-199 multiplies the decoded fp32 weights; the block scale after the sum).
-template <int ID>
-__device__ __forceinline__ float gx_block(const uint32_t *d, bool odd, const uint32_t *book, const float x[128]) {
+template <int ID, typename XP>
+__device__ __forceinline__ float gx_block(const uint32_t *d, bool odd, const uint32_t *book, XP x) {
     float sc;
     uint32_t w[gyro_nw<ID>()];
     gyro_unpack<ID>(d, odd, sc, w);
-    return sc * gyro_block_dot<ID>(w, book, x);
+    return gd_rounded(sc * gyro_block_dot<ID>(w, book, x));
 }
 
-GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
+GX_DEFINE(GX_PIPELINE, 512) {
     __shared__ uint4 book4[512];
-    __shared__ uint4 xpart[256];  // the part's 1024 fp32 activations (x32_stage_index order)
+    __shared__ uint4 xpart[8 * 33];  // the part's 1024 fp32 activations (x33_stage_index order)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t NE = a.c[2], E = a.c[15], F = a.c[16], n_tok = a.c[17];
     const uint32_t slot = blockIdx.z, t = slot / GX_U, k = slot - t * GX_U;
@@ -97,12 +105,16 @@ GD_PIPELINE_NAMED(moe_decode_gu_x, 512) {
     for (int j = 0; j < 15; ++j) d[j] = rw[j];
     // Codebook and activations through LDS while the blocks are in flight.
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
-    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x32_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
+    uint32_t *xst = reinterpret_cast<uint32_t *>(xpart) + x33_stage_index(tid >> 6, (tid >> 1) & 31u) * 4u + 2u * (tid & 1u);
     xst[0] = xw0;
     xst[1] = xw1;
     __syncthreads();
+#if GX_STEPWISE
+    const float *xf = reinterpret_cast<const float *>(xpart + b * 33u);
+#else
     float xf[128];
-    x32_from_lds(xpart, b, xf);
+    x33_from_lds(xpart + b * 33u, xf);
+#endif
     const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
     float v = 0.f;
 #define GX_CASE(ID) v = gx_block<ID>(d, (off & 2u) != 0u, book, xf)

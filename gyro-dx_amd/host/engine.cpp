@@ -899,7 +899,7 @@ class Engine {
                                  E / R, n);
             return;
         }
-        dispatch_maybe_timed(bracket == 2, marks, "moe_decode_gu_x",
+        dispatch_maybe_timed(bracket == 2, marks, n == 1 ? "moe_decode_gu_x" : "moe_decode_gu_xb",
                              {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
                               L.xtab.srv, codebook.srv, B.gu, B.gu_off, E, F, n},
                              F / 64, 2 * parts, n * U);

@@ -93,6 +93,30 @@ def test_decode_batch_parity(engine, tokens, reference, oracle_mod):
     assert_close(oracle_mod, ref[:4], out, "decode batch 4")
 
 
+@pytest.mark.parametrize("kind", ["tq2_t", "type148", "mixed"])
+def test_decode_batch_builds_bit_equal(oracle_mod, kind):
+    """The decode gate/up kernels come in two builds of one source: one token per call runs
+    moe_decode_gu / moe_decode_gu_x (a block's activations copied into registers at once), 2 to 8
+    tokens run moe_decode_gu_b / moe_decode_gu_xb (read from LDS step by step, fewer VGPRs). Both
+    compute the same products in the same order and round the block scale's product explicitly,
+    so a batch of 8 must equal the 8 tokens run one at a time bit for bit (and meet the oracle
+    bar)."""
+    L = {"tq2_t": lambda: synth.make_layer(131),
+         "type148": lambda: synth.make_layer(132, type_id=148),
+         "mixed": lambda: synth.make_layer(133, mixed_types=True)}[kind]()
+    x = synth.make_tokens(134, 8)
+    eng = Engine(max_tok=8)
+    try:
+        eng.add_layer(L)
+        print(f"decode {kind}: batch 8 against 8 single-token calls", flush=True)
+        out8 = eng.forward(0, x, PATH_DECODE)
+        out1 = np.concatenate([eng.forward(0, x[t:t + 1], PATH_DECODE) for t in range(8)])
+    finally:
+        eng.close()
+    np.testing.assert_array_equal(out8.view(np.uint32), out1.view(np.uint32))
+    assert_close(oracle_mod, oracle_mod.OracleLayer(L).forward(x), out8, f"decode {kind} batch 8")
+
+
 def test_reference_path_batch_parity(engine, tokens, reference, oracle_mod):
     ref, tr = reference
     out = engine.forward(0, tokens, PATH_REFERENCE)

@@ -113,7 +113,11 @@ def sequence(kind: str, ns):
             down = ("moe_decode_down_gl",) + down[1:]
         return [block(*DECODE_TQ2)[0], gu, down]
     if kind == "decode_x":
-        return block(*DECODE_X)
+        # The document's rule: moe_decode_gu_xb, same constants and grid, for 2 to 8 tokens.
+        router, gu, down = block(*DECODE_X)
+        if ns.n > 1:
+            gu = ("moe_decode_gu_xb",) + gu[1:]
+        return [router, gu, down]
     if kind == "decode_xg":
         return [block(*DECODE_TQ2)[0], *block(*DECODE_XG)]
     p = block(*PREFILL)
