@@ -126,6 +126,22 @@ __device__ __forceinline__ float gd_wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Inclusive prefix sum of 32-bit integers over the wave's 64 lanes (lane i gets the sum of lanes
+// 0 .. i), by the DPP steps of gd_wave_sum_dpp: no LDS traffic.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t gd_dpp_add_step_u32(uint32_t v) {
+    return v + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ uint32_t gd_wave_scan_u32(uint32_t v) {
+    v = gd_dpp_add_step_u32<0x111, 0xf>(v);  // row_shr:1
+    v = gd_dpp_add_step_u32<0x112, 0xf>(v);  // row_shr:2
+    v = gd_dpp_add_step_u32<0x114, 0xf>(v);  // row_shr:4
+    v = gd_dpp_add_step_u32<0x118, 0xf>(v);  // row_shr:8: prefix sums within rows of 16
+    v = gd_dpp_add_step_u32<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = gd_dpp_add_step_u32<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 // Global-address-space views of table buffers. Loads through them are global_load, counted by
 // vmcnt only (a flat load also counts against lgkmcnt), so an LDS-only wait leaves them in flight.
 typedef uint32_t gd_u32x4 __attribute__((ext_vector_type(4)));

@@ -7,19 +7,23 @@
 // The slots form chunks of 256, and moe_prefill_topk has counted hist[c][e], the slots of chunk c
 // that chose expert e (device-scope atomics into a histogram the router zeroed; a chunk's counts
 // are contiguous, so a popular expert's atomics spread over one cache line per chunk). Group c
-// places chunk c:
-//  - thread e sums column e of the histogram: the expert's total, and its count in the chunks
-//    before c;
-//  - the group scans the totals over experts into order_start, so each expert's cursor for the
-//    chunk is order_start[e] plus its count in the earlier chunks;
-//  - wave 0 walks the chunk's slots in slot order, 64 per round, and places each slot at its
-//    expert's cursor plus its rank among the round's lanes of the same expert (one ballot per
-//    expert-id bit); the highest such lane advances the cursor.
+// places chunk c, its four waves side by side at every step:
+//  - the expert's total and its count in the chunks before c: thread e reads its histogram
+//    column itself when there are at most 8 chunks; otherwise wave w sums chunks w, w + 4, ... for
+//    experts 4 lane .. 4 lane + 3 (16-byte loads when rows are whole 16-byte words; every load
+//    issued before the sums) and thread e adds the four waves' partial sums;
+//  - wave scans (DPP) of the totals, the tile counts and the full-tile counts give order_start
+//    and each expert's cursor for the chunk: order_start[e] plus its count in the earlier chunks;
+//  - thread i holds slot 256 c + i; its rank among the wave's lanes of the same expert (one
+//    ballot per expert-id bit) plus the counts of that expert in the chunk's earlier waves puts
+//    it at its expert's cursor plus the slots of that expert before it in the chunk.
 // Tiles (group 0): each expert's segment is cut into tiles of at most tile_rows sorted rows. The
 // list holds the full tiles first (expert by expert), then the partial tiles by decreasing row
 // count (ties by expert), so that the grouped GEMMs, whose groups start in list order, begin with
-// the longest tiles and end with the shortest; wave 1 ranks the partial tiles by a histogram of
-// their sizes and stable ranks within each size.
+// the longest tiles and end with the shortest. A partial tile's rank is the number of larger
+// partial tiles (a scan over sizes of the size histogram) plus the number of earlier experts
+// whose partial tile has its size (its rank among its wave's lanes of that size plus the counts
+// of earlier waves).
 // Output meta (u32 words): [0, n_expert] order_start, [1023] tile count,
 // [1024 + 4 i ..] tile i = {expert, first sorted row, rows, 0}.
 // Grid: ceil(n_slots / 256); 256 threads. Requires n_expert <= 256, n_slots <= 32768,
@@ -34,99 +38,176 @@
 #define SORT_CHUNK 256
 #define SORT_MAX_E 256
 #define SORT_MAX_TM 256
+#define SORT_WAVES 4
+
+// Rank of this lane among the wave's valid lanes whose key has the same low `bits` bits (bits <=
+// 8, uniform), the number of such lanes, and whether this lane is the highest of them.
+__device__ __forceinline__ uint32_t sort_match(uint32_t key, uint32_t bits, bool valid, uint32_t &count,
+                                               bool &highest) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t peers = __builtin_amdgcn_ballot_w64(valid);
+#pragma unroll
+    for (uint32_t b = 0; b < 8u; ++b) {
+        if (b >= bits) break;  // uniform
+        const uint64_t bb = __builtin_amdgcn_ballot_w64(((key >> b) & 1u) != 0u);
+        peers &= ((key >> b) & 1u) ? bb : ~bb;
+    }
+    const uint64_t own = valid ? peers : 1ull;  // a valid lane is among its own peers
+    count = (uint32_t)__builtin_popcountll(peers);
+    highest = valid && lane == 63u - (uint32_t)__builtin_clzll(own);
+    return (uint32_t)__builtin_popcountll(peers & ((1ull << lane) - 1ull));
+}
+
+// Exclusive prefixes over the group's 256 threads of N values per thread, from the DPP wave
+// scans and the wave totals (one barrier for all N); total[i]: the sum of value i over all
+// threads. part: N x 4 words of LDS. Every thread of the group must call it.
+template <int N>
+__device__ __forceinline__ void sort_group_scan(const uint32_t (&v)[N], uint32_t (*part)[SORT_WAVES],
+                                                uint32_t (&excl)[N], uint32_t (&total)[N]) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t incl[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        incl[i] = gd_wave_scan_u32(v[i]);
+        if (lane == 63u) part[i][wave] = incl[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        uint32_t before = 0;
+        for (uint32_t w = 0; w < wave; ++w) before += part[i][w];
+        total[i] = (part[i][0] + part[i][1]) + (part[i][2] + part[i][3]);
+        excl[i] = before + incl[i] - v[i];
+    }
+}
 
 GD_PIPELINE_NAMED(moe_prefill_sort, 256) {
     __shared__ uint32_t start[SORT_MAX_E + 1], tstart[SORT_MAX_E + 1], fstart[SORT_MAX_E + 1];
-    __shared__ uint32_t cur[SORT_MAX_E], psz[SORT_MAX_E], rnk[SORT_MAX_E];
-    __shared__ uint32_t hsz[SORT_MAX_TM], seen[SORT_MAX_TM];
-    __shared__ uint32_t idc[SORT_CHUNK];
-    __shared__ uint32_t wsum[4][3];
+    __shared__ uint32_t cur[SORT_MAX_E], above[SORT_MAX_TM];
+    __shared__ uint32_t wtot[SORT_WAVES][SORT_MAX_E], wcol[SORT_WAVES][SORT_MAX_E];
+    __shared__ uint32_t wcnt[SORT_WAVES][SORT_MAX_E], wsz[SORT_WAVES][SORT_MAX_TM];
+    __shared__ uint32_t part[3][SORT_WAVES];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n_slots = a.c[2], NE = a.c[3], TM = a.c[7];
     const uint32_t c = blockIdx.x, nch = (n_slots + SORT_CHUNK - 1u) / SORT_CHUNK;
     const bool lead = c == 0u;  // uniform per group
     uint32_t *order = gd_buf<uint32_t>(a, a.c[4]) + a.c[5];
     uint32_t *meta = gd_buf<uint32_t>(a, a.c[6]);
-    // The chunk's expert ids and the histogram column, every load issued before the sums.
+
+    // The slot's expert id and the histogram partials, every load issued before the sums.
     const uint32_t s_mine = c * SORT_CHUNK + tid;
-    const uint32_t id_mine = s_mine < n_slots ? gd_global(gd_buf<const uint32_t>(a, a.c[0]) + a.c[1])[s_mine] : 0u;
-    uint32_t total = 0, colp = 0;
-    if (tid < NE) {
-        gd_guint *col = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + tid);
-#pragma unroll 8
-        for (uint32_t q = 0; q < nch; ++q) {
-            const uint32_t h = col[q * NE];
-            total += h;
-            colp += q < c ? h : 0u;
-        }
-    }
-    idc[tid] = min(id_mine, NE - 1u);
-    if (lead) {
-        hsz[tid] = 0u;
-        seen[tid] = 0u;
-    }
-    // Exclusive prefix over experts of the counts, the tile counts and the full-tile counts:
-    // each wave scans its 64 experts, then the wave totals are added.
-    const uint32_t tiles = (total + TM - 1u) / TM, full = total / TM;
-    uint32_t ic = total, it = tiles, iff = full;
-    if (tid < NE) psz[tid] = total - full * TM;
+    const bool valid = s_mine < n_slots;
+    const uint32_t id_mine = valid ? gd_global(gd_buf<const uint32_t>(a, a.c[0]) + a.c[1])[s_mine] : 0u;
+    const uint32_t *hist = gd_buf<const uint32_t>(a, a.c[9]) + a.c[10];
 #pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) {
-        const uint32_t pc = __shfl_up(ic, o, 64), pt = __shfl_up(it, o, 64), pf = __shfl_up(iff, o, 64);
-        if (lane >= o) {
-            ic += pc;
-            it += pt;
-            iff += pf;
+    for (int w = 0; w < SORT_WAVES; ++w) {
+        wcnt[w][tid] = 0u;
+        wsz[w][tid] = 0u;
+    }
+    // Thread e: the expert's total and its count in the chunks before c. Up to 8 chunks, thread e
+    // reads its column itself; more, wave w sums chunks w, w + 4, ... for experts 4 lane ..
+    // 4 lane + 3 and thread e adds the four waves' partial sums.
+    uint32_t total = 0, colp = 0;
+    if (nch <= 8u) {  // uniform
+        if (tid < NE) {
+            gd_guint *h1 = gd_global(hist) + tid;
+            uint32_t h[8];
+#pragma unroll
+            for (uint32_t q = 0; q < 8u; ++q) h[q] = q < nch ? h1[q * NE] : 0u;
+#pragma unroll
+            for (uint32_t q = 0; q < 8u; ++q) {
+                total += h[q];
+                colp += q < c ? h[q] : 0u;
+            }
+        }
+    } else {
+        uint32_t tot[4] = {0u, 0u, 0u, 0u}, col[4] = {0u, 0u, 0u, 0u};
+        if ((NE & 3u) == 0u && (a.c[10] & 3u) == 0u) {  // uniform: rows of whole 16-byte words
+            // Lane l reads experts 4 l .. 4 l + 3 of a row as one 16-byte load: a wave covers the
+            // row's contiguous words.
+            gd_gu32x4 *h4 = gd_global4(hist);
+            const uint32_t l4 = min(lane, NE / 4u - 1u);
+#pragma unroll 8
+            for (uint32_t q = wave; q < nch; q += SORT_WAVES) {
+                const gd_u32x4 h = h4[q * (NE / 4u) + l4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t hv = 4u * lane < NE ? h[j] : 0u;
+                    tot[j] += hv;
+                    col[j] += q < c ? hv : 0u;
+                }
+            }
+        } else {
+            gd_guint *h1 = gd_global(hist);
+#pragma unroll 8
+            for (uint32_t q = wave; q < nch; q += SORT_WAVES) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = 4u * lane + (uint32_t)j;
+                    const uint32_t h = h1[q * NE + min(e, NE - 1u)];
+                    const uint32_t hv = e < NE ? h : 0u;
+                    tot[j] += hv;
+                    col[j] += q < c ? hv : 0u;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wtot[wave][4u * lane + j] = tot[j];
+            wcol[wave][4u * lane + j] = col[j];
+        }
+        __syncthreads();
+        if (tid < NE) {
+#pragma unroll
+            for (int w = 0; w < SORT_WAVES; ++w) {
+                total += wtot[w][tid];
+                colp += wcol[w][tid];
+            }
         }
     }
-    if (lane == 63u) {
-        wsum[wave][0] = ic;
-        wsum[wave][1] = it;
-        wsum[wave][2] = iff;
-    }
-    __syncthreads();
-    uint32_t bc = 0, bt = 0, bf = 0;
-    for (uint32_t w = 0; w < wave; ++w) {
-        bc += wsum[w][0];
-        bt += wsum[w][1];
-        bf += wsum[w][2];
-    }
+
+    // Order_start, the tile starts and the full-tile starts as exclusive prefixes over experts.
+    const uint32_t tiles = (total + TM - 1u) / TM, full = total / TM;
+    const uint32_t scan_in[3] = {total, tiles, full};
+    uint32_t ex[3], all[3];
+    sort_group_scan<3>(scan_in, part, ex, all);
     if (tid < NE) {
-        start[tid] = bc + ic - total;
-        tstart[tid] = bt + it - tiles;
-        fstart[tid] = bf + iff - full;
-        cur[tid] = bc + ic - total + colp;
+        start[tid] = ex[0];
+        tstart[tid] = ex[1];
+        fstart[tid] = ex[2];
+        cur[tid] = ex[0] + colp;
     }
     if (tid == 0) {  // the grand totals
-        start[NE] = (wsum[0][0] + wsum[1][0]) + (wsum[2][0] + wsum[3][0]);
-        tstart[NE] = (wsum[0][1] + wsum[1][1]) + (wsum[2][1] + wsum[3][1]);
-        fstart[NE] = (wsum[0][2] + wsum[1][2]) + (wsum[2][2] + wsum[3][2]);
+        start[NE] = all[0];
+        tstart[NE] = all[1];
+        fstart[NE] = all[2];
     }
-    if (lead && tid < NE && psz[tid]) atomicAdd(&hsz[psz[tid]], 1u);
-    __syncthreads();
 
-    // Stable placement of the chunk, one round of 64 slots at a time (wave 0).
-    if (wave == 0u) {
-        const uint32_t nb = NE > 1u ? 32u - (uint32_t)__builtin_clz(NE - 1u) : 1u;
-#pragma unroll
-        for (uint32_t r = 0; r < SORT_CHUNK / 64u; ++r) {
-            const uint32_t s = c * SORT_CHUNK + r * 64u + lane;
-            const bool valid = s < n_slots;
-            const uint32_t e = idc[r * 64u + lane];
-            uint64_t peers = __builtin_amdgcn_ballot_w64(valid);
-#pragma unroll
-            for (uint32_t b = 0; b < 8u; ++b) {
-                if (b >= nb) break;  // uniform
-                const uint64_t bb = __builtin_amdgcn_ballot_w64(((e >> b) & 1u) != 0u);
-                peers &= ((e >> b) & 1u) ? bb : ~bb;
-            }
-            const uint32_t rank = (uint32_t)__builtin_popcountll(peers & ((1ull << lane) - 1ull));
-            if (valid) {
-                const uint32_t pos = cur[e] + rank;
-                if (pos < n_slots) order[pos] = s;  // always, for a histogram of these ids
-                if (lane == 63u - (uint32_t)__builtin_clzll(peers)) cur[e] += (uint32_t)__builtin_popcountll(peers);
-            }
-        }
+    // Stable placement of the chunk: each wave's lanes of one expert in lane order, after the
+    // chunk's earlier waves.
+    const uint32_t e_mine = min(id_mine, NE - 1u);
+    const uint32_t nb = NE > 1u ? 32u - (uint32_t)__builtin_clz(NE - 1u) : 1u;
+    uint32_t cnt;
+    bool highest;
+    const uint32_t rank = sort_match(e_mine, nb, valid, cnt, highest);
+    if (highest) wcnt[wave][e_mine] = cnt;
+    // Group 0 also ranks the partial tiles by decreasing size, ties by expert:
+    // rank = (partial tiles larger than p) + (earlier experts of size p). Here each wave's lanes
+    // of one size in expert order.
+    const uint32_t p_mine = tid < NE ? total - full * TM : 0u;
+    uint32_t srank = 0;
+    if (lead) {
+        const uint32_t nbs = 32u - (uint32_t)__builtin_clz(SORT_MAX_TM - 1u);
+        uint32_t scnt;
+        bool shighest;
+        srank = sort_match(p_mine, nbs, p_mine != 0u, scnt, shighest);
+        if (shighest) wsz[wave][p_mine] = scnt;
+    }
+    __syncthreads();  // cur, wcnt and wsz
+    if (valid) {
+        uint32_t pos = cur[e_mine] + rank;
+        for (uint32_t w = 0; w < wave; ++w) pos += wcnt[w][e_mine];
+        if (pos < n_slots) order[pos] = s_mine;  // always, for a histogram of these ids
     }
     if (!lead) return;  // uniform: the rest is group 0's
 
@@ -144,54 +225,23 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 256) {
         for (uint32_t i = tid; i < 64u + 2u * n_tiles; i += 256u)
             if (i != 1u) sched[i] = 0u;
     }
-    // Rank of each partial tile by decreasing size, ties by expert (wave 1):
-    // rank = (partial tiles larger than p) + (earlier experts of size p).
-    if (wave == 1u) {
-        // above[p] = sum of hsz[q] over q > p, p = 4 lane .. 4 lane + 3 (a scan over lanes from
-        // the top).
-        uint32_t h[4], hs = 0;
+    // Partial tiles larger than each size p (wave 0, lane l for sizes 4 l .. 4 l + 3: the size
+    // histogram from the four waves' counts, then a DPP scan over sizes).
+    if (wave == 0u) {
+        uint32_t hq[4], sum = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            h[j] = hsz[4u * lane + j];
-            hs += h[j];
+            const uint32_t p = 4u * lane + (uint32_t)j;
+            hq[j] = (wsz[0][p] + wsz[1][p]) + (wsz[2][p] + wsz[3][p]);
+            sum += hq[j];
         }
-        uint32_t suf = hs;  // inclusive suffix over lanes >= lane
+        const uint32_t incl = gd_wave_scan_u32(sum);
+        const uint32_t n_partial = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+        uint32_t run = incl - sum;  // partial tiles of sizes below 4 lane
 #pragma unroll
-        for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t v = __shfl_down(suf, o, 64);
-            if (lane + o < 64u) suf += v;
-        }
-        uint32_t ab = suf - hs;  // sizes above this lane's four
-#pragma unroll
-        for (int j = 3; j >= 0; --j) {
-            seen[4u * lane + j] = ab;  // "above" until the rounds start
-            ab += h[j];
-        }
-        // Stable ranks within a size: one round of 64 experts at a time.
-        const uint32_t nbs = 32u - (uint32_t)__builtin_clz(SORT_MAX_TM - 1u);
-        uint32_t above_p[SORT_MAX_E / 64];
-#pragma unroll
-        for (uint32_t r = 0; r < SORT_MAX_E / 64u; ++r) {
-            const uint32_t e = r * 64u + lane;
-            const uint32_t p = e < NE ? psz[e] : 0u;
-            above_p[r] = seen[p];
-        }
-        for (uint32_t i = lane; i < SORT_MAX_TM; i += 64u) seen[i] = 0u;
-#pragma unroll
-        for (uint32_t r = 0; r < SORT_MAX_E / 64u; ++r) {
-            if (r * 64u >= NE) break;  // uniform
-            const uint32_t e = r * 64u + lane;
-            const uint32_t p = e < NE ? psz[e] : 0u;
-            uint64_t peers = __builtin_amdgcn_ballot_w64(p != 0u);
-#pragma unroll
-            for (uint32_t b = 0; b < nbs; ++b) {
-                const uint64_t bb = __builtin_amdgcn_ballot_w64(((p >> b) & 1u) != 0u);
-                peers &= ((p >> b) & 1u) ? bb : ~bb;
-            }
-            if (p) {
-                rnk[e] = above_p[r] + seen[p] + (uint32_t)__builtin_popcountll(peers & ((1ull << lane) - 1ull));
-                if (lane == 63u - (uint32_t)__builtin_clzll(peers)) seen[p] += (uint32_t)__builtin_popcountll(peers);
-            }
+        for (int j = 0; j < 4; ++j) {
+            run += hq[j];
+            above[4u * lane + j] = n_partial - run;
         }
     }
     __syncthreads();
@@ -199,8 +249,12 @@ GD_PIPELINE_NAMED(moe_prefill_sort, 256) {
     // tile of each expert at the full-tile total plus its rank.
     if (consistent && tid < NE) {
         uint4 *list = reinterpret_cast<uint4 *>(meta + 1024u);
-        const uint32_t cnt = start[tid + 1] - start[tid], nf = cnt / TM, p = cnt - nf * TM;
+        const uint32_t cnt_e = start[tid + 1] - start[tid], nf = cnt_e / TM, p = cnt_e - nf * TM;
         for (uint32_t j = 0; j < nf; ++j) list[fstart[tid] + j] = make_uint4(tid, start[tid] + j * TM, TM, 0u);
-        if (p) list[fstart[NE] + rnk[tid]] = make_uint4(tid, start[tid] + nf * TM, p, 0u);
+        if (p) {
+            uint32_t r = above[p] + srank;
+            for (uint32_t w = 0; w < wave; ++w) r += wsz[w][p];
+            if (fstart[NE] + r < n_tiles) list[fstart[NE] + r] = make_uint4(tid, start[tid] + nf * TM, p, 0u);
+        }
     }
 }
