@@ -36,10 +36,20 @@ __device__ __forceinline__ void prefill_gemm_queue(const uint32_t *meta, uint32_
         __syncthreads();  // every wave has read the word
         return u;
     };
-    // Gate/up units (queue word 0). The unit that completes a tile appends the tile to the
-    // ready list.
+    // Gate/up units. The first round is static (group g takes unit g), the rest come from queue
+    // word 0 (unit = groups + the word's count): a device-scope atomic on one word that every
+    // group of the GPU polls costs about 2 us a take under that contention, and a first round
+    // taken without it measured the launch 6-8% faster. The unit that completes a tile appends
+    // the tile to the ready list.
+    bool first = true;
     for (;;) {
-        const uint32_t u = take(0);
+        uint32_t u;
+        if (first) {
+            u = blockIdx.x;
+            first = false;
+        } else {
+            u = gridDim.x + take(0);
+        }
         if (u >= n_gu) break;  // uniform
         const uint32_t tile = u / nfb, fb = u - tile * nfb;
         gu(tile_list[tile], fb);

@@ -7,8 +7,8 @@
 // and a down unit about a quarter of that. With one launch per kind, the tile count rarely fills
 // the last round of two groups per CU: the last gate/up groups ran nearly alone, and the down
 // kernel could not start before them. Here two groups per CU take all gate/up units (tile by
-// tile, the sort's longest-first order) and then down units, so the down units fill the CUs the
-// gate/up tail leaves idle.
+// tile, the sort's longest-first order; group g takes unit g first, the later ones come from the
+// queue) and then down units, so the down units fill the CUs the gate/up tail leaves idle.
 //
 // A down unit needs its tile's act16 rows from all F / 128 gate/up units of the tile. A gate/up
 // unit writes its rows with device-scope stores, waits for them, and adds 1 to its tile's
@@ -27,9 +27,9 @@
 // Constants: 0 meta_uav 1 order_uav 2 order_off 3 xh16_uav 4 xh16_off (words) 5 base_lo
 // 6 base_hi 7 slot_stride 8 proj_bytes 9 codebook_srv 10 signs_srv (0xffffffff: none) 11 signs_off
 // 12 act16_uav 13 act16_off (words) 14 E 15 F 16 n_used 17 range flag (as moe_prefill_gu)
-// 18 down32_uav 19 down32_off (words) 20 sched_uav (u32: [0] gate/up queue, [1] give-up, [2] down
-// queue, [3] ready count, [64 + t] tile t's finished gate/up units, [64 + tiles + s] ready slot s:
-// tile + 1, 0 while empty) 21 spin limit (polls of a ready slot) 22 small-tile rows SR (read by
+// 18 down32_uav 19 down32_off (words) 20 sched_uav (u32: [0] gate/up queue (units from gridDim.x
+// on), [1] give-up, [2] down queue, [3] ready count, [64 + t] tile t's finished gate/up units,
+// [64 + tiles + s] ready slot s: tile + 1, 0 while empty) 21 spin limit (polls of a ready slot) 22 small-tile rows SR (read by
 // moe_prefill_gemm_s only: 16 or 8, tiles of at most SR rows take the small units of
 // gemm_small.h; 0: none).
 #include "gemm_persistent.h"
