@@ -230,7 +230,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
         float sc;                                                         \
         uint32_t q[gyro_nw<ID>()];                                        \
         gyro_unpack<ID>(dw[s][i], odd[s][i], sc, q);                      \
-        h[i] = gd_rounded(sc * gyro_half_dot<ID>(q, hf, book, x));        \
+        h[i] = sc * gyro_half_dot<ID>(q, hf, book, x);                    \
     }
             GYRO_TYPE_SWITCH(ty[s], DG_CASE)
 #undef DG_CASE
@@ -240,7 +240,7 @@ DG_DEFINE(DG_PIPELINE, 512) {
                 float sc;
                 uint32_t q[8];
                 tq2_unpack(dw[s][i], odd[s][i], sc, q);
-                h[i] = gd_rounded(sc * tq2_half_dot(q, hf, book, x));
+                h[i] = sc * tq2_half_dot(q, hf, book, x);
             }
 #endif
 #pragma unroll

@@ -202,7 +202,7 @@ GG_DEFINE(GG_PIPELINE, 512) {
         float sc;                                                         \
         uint32_t q[gyro_nw<ID>()];                                        \
         gyro_unpack<ID>(dw[s][p], odd[s][p], sc, q);                      \
-        v = gd_rounded(sc * gyro_block_dot<ID>(q, book, xf));             \
+        v = sc * gyro_block_dot<ID>(q, book, xf);                         \
     }
                 GYRO_TYPE_SWITCH(ty[s][p], GG_CASE)
 #undef GG_CASE
@@ -210,7 +210,7 @@ GG_DEFINE(GG_PIPELINE, 512) {
                 float sc;
                 uint32_t q[8];
                 tq2_unpack(dw[s][p], odd[s][p], sc, q);
-                v = gd_rounded(sc * tq2_block_dot(q, book, xf));
+                v = sc * tq2_block_dot(q, book, xf);
 #endif
                 gred[(2u * rr + (uint32_t)p) * nb + b] = v;
             }
