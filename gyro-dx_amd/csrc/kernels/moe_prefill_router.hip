@@ -8,20 +8,22 @@
 // with v_mfma_f32_32x32x2_f32; its waves 0..3 split the range into quarters and their partial
 // tiles are added in wave order through LDS. Range bz writes logit plane bz; the top-k kernel
 // adds the S planes in plane order. The MFMA operands take one row per lane, so each of these
-// waves stages its own 32-wide K chunks of the 32 token rows and the 32 router rows into LDS
-// first: direct global-to-LDS loads (8 lanes per 128-byte row, whole rows per load), the
-// 16-byte chunk q of row r stored at position q ^ (r % 8), four chunks ahead in five buffers per
-// wave; only the wave's own load count is waited for, so the K loop has no barrier. A wave's
-// MFMA holds back that wave's following instructions until it has nearly finished (other waves
-// issue meanwhile), and this wave is the only MFMA wave on its SIMD, so each chunk's sixteen
-// MFMAs carry the chunk's other work one piece at a time: a staging load after each of the
-// first eight, the reads of chunk c + 1 (into the other of two operand sets, no copies) after
-// the next four. Lane half h takes
-// k + 4h .. k + 4h + 3 of every 8 for both operands, so every product x[t][k] W[r][k] enters the
-// sum once. Waves 4..7 meanwhile rotate: all n * E/128 blocks are spread over the rotation
-// waves of the grid, eight blocks per wave at a time, so the rotation's memory traffic and VALU
-// work overlap the MFMA chains on the same SIMDs.
-// Grid: (ceil(n / 32), ceil(n_expert / 32), S); 512 threads. Requires E % (128 S) == 0.
+// waves stages its own 16-wide K chunks of the 32 token rows and the 32 router rows into LDS
+// first: direct global-to-LDS loads (4 lanes per 64-byte row, whole rows per load), the
+// 16-byte chunk q of row r stored at position q ^ ((r / 2) % 4), four chunks ahead in five
+// buffers per wave; only the wave's own load count is waited for, so the K loop has no barrier.
+// A group takes 80 KB of LDS and at most 128 VGPRs, so that grids of more than one group per
+// CU (4096 tokens: 1024 groups) run two groups per CU. A wave's MFMA holds back that wave's
+// following instructions until it has nearly finished (other waves issue meanwhile), so each
+// chunk's eight MFMAs carry the chunk's other work one piece at a time: a staging load after
+// each of the first four, the reads of chunk c + 1 (into the other of two operand sets, no
+// copies) after the next two. Lane half h takes k + 4h .. k + 4h + 3 of every 8 for both operands, so
+// every product x[t][k] W[r][k] enters the sum once. Waves 4..7 meanwhile rotate: all
+// n * E/128 blocks are spread over the rotation waves of the grid, eight blocks per wave at a
+// time, so the rotation's memory traffic and VALU work overlap the MFMA chains on the same
+// SIMDs.
+// Grid: (ceil(n / 32), ceil(n_expert / 32), S); 512 threads, 80 KB of LDS (two groups per CU).
+// Requires E % (128 S) == 0.
 // Constants: 0 x_uav 1 x_off (words; rows of E floats) 2 n_tok 3 E 4 router_srv 5 router_off
 // 6 n_expert 7 bias_srv (0xffffffff: none) 8 bias_off 9 logits_uav 10 logits_off
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
@@ -35,113 +37,114 @@
 #include "fwht.h"
 
 #define RT_WAVES 4
-#define RT_KC 32    // K per staged chunk
-#define RT_NBUF 5    // chunks c .. c + 4 of a wave in LDS: four chunks (32 KB) in flight
+#define RT_KC 16    // K per staged chunk
+#define RT_NBUF 5    // chunks c .. c + 4 of a wave in LDS: four chunks (16 KB) in flight
+#define RT_LOADS 4   // global-to-LDS loads per chunk: two of token rows, two of router rows
 
-// 160 KB: the staging buffers of the four K waves; after its K loop a wave's partial tile
-// (4 KB, fp32) goes over its own first activation buffer.
+// 80 KB, so that two groups share a CU: the staging buffers of the four K waves; after its K
+// loop a wave's partial tile (4 KB, fp32) goes over its own first two activation buffers.
 struct __attribute__((aligned(16))) RtLds {
-    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 128 bytes
+    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 64 bytes
     gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_KC / 4];
 };
-static_assert(sizeof(RtLds) == 163840, "the CU's 160 KB");
+static_assert(sizeof(RtLds) == 81920, "two groups fill the CU's 160 KB");
+static_assert(sizeof(RtLds::x[0]) >= 32 * 32 * 4, "a wave's partial tile fits its activation buffers");
 
-// Waits until chunk c's loads have landed, with `ahead` later chunks (8 loads each) in flight.
+// Swizzled position of 16-byte chunk q of staged row r: the chunk that the 8 lanes of rows
+// m .. m + 7 read at one index sits in 8 different 16-byte bank groups.
+__device__ __forceinline__ uint32_t rt_pos(uint32_t q, uint32_t r) { return q ^ ((r >> 1) & 3u); }
+
+// Waits until chunk c's loads have landed, with `ahead` later chunks (RT_LOADS loads each) in
+// flight.
 __device__ __forceinline__ void rt_wait(uint32_t ahead) {
     switch (ahead) {
-        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
         default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
 
-// Stages chunk c (K = kq + 32 c ..) of this wave's 32 token rows and 32 router rows: 4 + 4
-// loads, lane l of load i carrying row 8 i + l / 8, position l % 8.
+// Stages chunk c (K = kq + 16 c ..) of this wave's 32 token rows and 32 router rows: 2 + 2
+// loads, lane l of load i carrying row 16 i + l / 4, position l % 4.
 __device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf, const void *xbase,
-                                         const void *wbase, const uint32_t xoff[4], const uint32_t woff[4],
+                                         const void *wbase, const uint32_t xoff[2], const uint32_t woff[2],
                                          uint32_t kbytes) {
     const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xbase, xoff[i] + kbytes);
+    for (int i = 0; i < 2; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xbase, xoff[i] + kbytes);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
+    for (int i = 0; i < 2; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
 }
 
-// Operands of one staged chunk for this lane (row m, lane half h): four float4 of the token row
-// and four of the router row, k = 8 j + 4 h .. + 3 of the chunk for j = 0..3.
+// Operands of one staged chunk for this lane (row m, lane half h): two float4 of the token row
+// and two of the router row, k = 8 j + 4 h .. + 3 of the chunk for j = 0, 1.
 struct RtOps {
-    float4 x[4], w[4];
+    float4 x[2], w[2];
 };
 __device__ __forceinline__ void rt_read(const RtLds &sm, uint32_t wave, uint32_t buf, uint32_t m, uint32_t h, RtOps &o) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t p = (2u * (uint32_t)j + h) ^ (m & 7u);
-        o.x[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 8u + p]);
-        o.w[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 8u + p]);
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t p = rt_pos(2u * (uint32_t)j + h, m);
+        o.x[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 4u + p]);
+        o.w[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 4u + p]);
     }
 }
-__device__ __forceinline__ void rt_mfma4(f32x16 &acc, const float4 &x, const float4 &w) {
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.x, w.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.y, w.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.z, w.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x.w, w.w, acc, 0, 0, 0);
-}
-// Chunk c's sixteen MFMAs (operands `cur`) with the chunk's other work between them, so that the
-// matrix pipe always has the next MFMA waiting: the eight loads staging chunk c + 4 (into the
-// buffer of chunk c - 1, read into registers two chunks ago) one after each of the first eight
+// Chunk c's eight MFMAs (operands `cur`) with the chunk's other work between them, so that the
+// matrix pipe always has the next MFMA waiting: the four loads staging chunk c + 4 (into the
+// buffer of chunk c - 1, read into registers two chunks ago) one after each of the first four
 // MFMAs, then the wait for chunk c + 1 and its reads into `next`, two after each of the next
-// four. The following chunk's MFMAs use `next` once the four MFMAs after the reads have issued.
+// two. The following chunk's MFMAs use `next` once the two MFMAs after the reads have issued.
 // STEADY: chunks c + 1 .. c + 4 are all in flight (c + 4 < nc), so the wait is one immediate
 // count; otherwise `ahead` (the chunks issued after chunk c + 1) picks it.
 template <bool STEADY>
 __device__ __forceinline__ void rt_chunk(RtLds &sm, uint32_t wave, uint32_t c, uint32_t nc, uint32_t m, uint32_t h,
-                                         const void *xbase, const void *wbase, const uint32_t xoff[4],
-                                         const uint32_t woff[4], const RtOps &cur, RtOps &next, f32x16 &acc) {
+                                         const void *xbase, const void *wbase, const uint32_t xoff[2],
+                                         const uint32_t woff[2], const RtOps &cur, RtOps &next, f32x16 &acc) {
     const bool stage = STEADY || c + 4u < nc;
     const uint32_t buf = (c + 4u) % RT_NBUF, kbytes = (c + 4u) * RT_KC * 4u;
     const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const float *xj = reinterpret_cast<const float *>(&cur.x[j]), *wj = reinterpret_cast<const float *>(&cur.w[j]);
+    {
+        const float *x0 = reinterpret_cast<const float *>(&cur.x[0]), *w0 = reinterpret_cast<const float *>(&cur.w[0]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xj[q], wj[q], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[q], w0[q], acc, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (stage) {
-                if (j == 0) gg_dma16(lx + (uint32_t)q * 1024u, xbase, xoff[q] + kbytes);
-                else gg_dma16(lw + (uint32_t)q * 1024u, wbase, woff[q] + kbytes);
+                if (q < 2) gg_dma16(lx + (uint32_t)q * 1024u, xbase, xoff[q] + kbytes);
+                else gg_dma16(lw + (uint32_t)(q - 2) * 1024u, wbase, woff[q - 2] + kbytes);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     const bool more = STEADY || c + 1u < nc;
     if (STEADY) {
-        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");  // chunks c + 2 .. c + 4 in flight
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // chunks c + 2 .. c + 4 in flight
     } else if (more) {
         rt_wait(min(nc - 2u - c, RT_NBUF - 2u));
     }
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t rb = (c + 1u) % RT_NBUF;
+    const float *x1 = reinterpret_cast<const float *>(&cur.x[1]), *w1 = reinterpret_cast<const float *>(&cur.w[1]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float *>(&cur.x[2])[q],
-                                                   reinterpret_cast<const float *>(&cur.w[2])[q], acc, 0, 0, 0);
+    for (int q = 0; q < 2; ++q) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[q], w1[q], acc, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         if (more) {
-            const uint32_t p = (2u * (uint32_t)q + h) ^ (m & 7u);
-            next.x[q] = __builtin_bit_cast(float4, sm.x[wave][rb][m * 8u + p]);
-            next.w[q] = __builtin_bit_cast(float4, sm.w[wave][rb][m * 8u + p]);
+            const uint32_t p = rt_pos(2u * (uint32_t)q + h, m);
+            next.x[q] = __builtin_bit_cast(float4, sm.x[wave][rb][m * 4u + p]);
+            next.w[q] = __builtin_bit_cast(float4, sm.w[wave][rb][m * 4u + p]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    rt_mfma4(acc, cur.x[3], cur.w[3]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[2], w1[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[3], w1[3], acc, 0, 0, 0);
     // The operands stay allocated to the end of the chunk: a VGPR written while an MFMA that
     // reads it is in flight holds the write (and the wave) until the MFMA has read it, about 27
     // of its 64 cycles; left free, the compiler reuses them for address arithmetic right after
     // the MFMA that reads them.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
         asm volatile("" ::"v"(cur.x[j].x), "v"(cur.x[j].y), "v"(cur.x[j].z), "v"(cur.x[j].w));
         asm volatile("" ::"v"(cur.w[j].x), "v"(cur.w[j].y), "v"(cur.w[j].z), "v"(cur.w[j].w));
     }
@@ -162,7 +165,7 @@ __device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16]
     d[1] = o[1];
 }
 
-GD_PIPELINE_NAMED(moe_prefill_router, 512) {
+GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
     __shared__ RtLds sm;
     float *red = reinterpret_cast<float *>(&sm.x[0][0][0]);  // red(w) at sm.x[w][0]
     constexpr uint32_t kRedStride = sizeof(sm.x[0]) / 4u;   // floats from one wave's buffers to the next
@@ -179,10 +182,10 @@ GD_PIPELINE_NAMED(moe_prefill_router, 512) {
         // Router tile, K quarter `wave`.
         const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
         const uint32_t kq = z * ES + wave * (ES / 4u), nc = ES / 4u / RT_KC;
-        uint32_t xoff[4], woff[4];
+        uint32_t xoff[2], woff[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = (lane & 7u) ^ (r & 7u);
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t r = 16u * (uint32_t)i + (lane >> 2), q = rt_pos(lane & 3u, r);
             xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
             woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
         }

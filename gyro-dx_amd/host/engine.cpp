@@ -288,6 +288,10 @@ class Engine {
     // Stack prefill: the combine also computes the next layer's RMSNorm (environment's
     // GYRO_STACK_NORM_FUSED=0: moe_stack_norm before every layer instead).
     bool stack_norm_fused = true;
+    // The prefill router's K split doubles while its groups stay within this count (the
+    // environment's GYRO_ROUTER_GROUPS overrides it). One group per CU measured best: a split
+    // that gives 512 groups, two per CU, was no faster at 1024 tokens and adds a logit plane.
+    uint32_t router_groups = 256;
     uint32_t small_rows() const {
         if (E % 512 || F % 512) return 0;
         return E <= 2048 ? 16u : (E <= 4096 ? 8u : 0u);
@@ -445,6 +449,8 @@ class Engine {
         stack_norm_fused = !(snf && snf[0] == '0');
         if (const char *ps = std::getenv("GYRO_PREFILL_SPIN_LIMIT"))
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
+        if (const char *rg = std::getenv("GYRO_ROUTER_GROUPS"))
+            router_groups = std::max(1u, (uint32_t)std::strtoul(rg, nullptr, 10));
     }
 
     // The decode path's own intermediate buffers.
@@ -943,11 +949,13 @@ class Engine {
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
-        // K split of the router: small batches get more groups (up to 256 of 32 x 32 logit tiles),
-        // each K range writing its own logit plane.
+        // K split of the router: small batches get more groups (up to router_groups of 32 x 32
+        // logit tiles), each K range writing its own logit plane.
         const uint32_t rt_tiles = ((n + 31) / 32) * ((NE + 31) / 32);
         uint32_t ks = 1;
-        while (rt_tiles * ks * 2 <= 256 && E % (128 * ks * 2) == 0 && ks * 2 <= 16 && (uint64_t)ks * 2 * n <= max_tok) ks *= 2;
+        while (rt_tiles * ks * 2 <= router_groups && E % (128 * ks * 2) == 0 && ks * 2 <= 16 &&
+               (uint64_t)ks * 2 * n <= max_tok)
+            ks *= 2;
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
