@@ -1,41 +1,57 @@
 // Decode path for layers whose experts and projections mix Gyro types, step 3: SwiGLU and the
 // down-input rotation, the fused dequant-GEMV of the down rows, the route-weighted combine
 // (src/engine.zig:603-641) and, when the layer has one, the shared expert's gated output
-// (src/engine.zig:644-653), structured as moe_decode_down: a group owns 16 output rows of one
+// (src/engine.zig:644-653), structured as moe_decode_down: a group owns R output rows of one
 // token for all 8 selected experts, the partials, signs and codebook are requested ahead of the
 // routes, and wave w forms expert w's down input in 16-lane transform rows. Each expert's down
-// rows and type come from the layer's expert table (ExpertDesc); wave w streams the 16 rows of
-// expert w (64 bb contiguous bytes for blocks of bb bytes, every lane's address clamped into
-// them) and decodes them: lane 4 r + bb takes block bb of row r with the block decoder of the
-// expert's type, uniform per wave. The four block sums of a row are added with DPP; the experts
-// are combined in k order through LDS after a second barrier.
-// Grid: x = E / 16, y = n_tok; 512 threads.
+// rows and type come from the layer's expert table (ExpertDesc); wave w streams the R rows of
+// expert w (4 R bb contiguous bytes for blocks of bb bytes, every lane's address clamped into
+// them) and decodes them with the decoder of the expert's type, uniform per wave. The block or
+// half-block sums of a row are added with DPP; the experts are combined in k order through LDS
+// after a second barrier. Two builds:
+//  - moe_decode_down_x, R = 8, for one token: lane 8 r + 2 b + hf takes half hf of block b of
+//    row r, and E / 8 groups fill the GPU;
+//  - moe_decode_down_xb, R = 16, for 2 to 8 tokens, whose E / 16 groups per token fill it
+//    already: lane 4 r + b takes both halves of block b of row r, and each group's fixed loads
+//    (partials, signs, codebook, routes) serve twice the rows.
+// Both form each half block's scaled dot the same way and add the halves, then the blocks
+// ((b0 + b1) + (b2 + b3)), in the same order, so a token's outputs do not depend on the build
+// that ran it.
+// Grid: x = E / R, y = n_tok; 512 threads.
 // Constants: 0 gu_uav 1 gu_off 2 ids_uav 3 ids_off 4 weights_uav 5 weights_off 6 xtab_srv
 // 7 (unused) 8 (unused) 9 (unused) 10 codebook_srv 11 signs_srv (0xffffffff: none) 12 signs_off
 // 13 out_uav 14 out_off 15 E 16 F 17 n_used 18 n_tok 19 parts 20 n_expert 21 residual (0: none,
 // 1: add) 22 res_uav 23 res_off 24 shared (0: none, 1: the layer's shared expert) 25 sh_h_uav
 // (fp32 [n][2 SF]: W_sg x then W_su x, from moe_router) 26 (unused) 27 shg_uav (g . x [n])
 // 28 shg_off 29 sh_down_srv (bf16 [E][SF]) 30 SF (<= 1024, a multiple of 256). The shared
-// expert's SwiGLU a = silu(W_sg x) * W_su x is formed in LDS and its 16 down rows of the group
-// are dotted with it (32 lanes per row); the combine adds sigmoid(g . x) times that, then the
-// residual.
+// expert's SwiGLU a = silu(W_sg x) * W_su x is formed in LDS and its R down rows of the group
+// are dotted with it (wave w takes rows w and, for R = 16, w + 8: 64 lanes per row, the same
+// sums in either build); the combine adds sigmoid(g . x) times that, then the residual.
 // Requires n_used == 8, F == 512 and at most 2 K-parts.
 #include "gyro_fast.h"
 #include "fwht.h"
 
-#define DN_ROWS 16
+#ifndef DX_PIPELINE
+#define DX_PIPELINE moe_decode_down_x
+#define DN_ROWS 8
+#endif
 #define DN_U 8
 #define DN_F 512
 #define DN_NB (DN_F / 128)
 #define DN_MAX_BB 58
-#define DN_EXPERT_WORDS (DN_ROWS * DN_NB * DN_MAX_BB / 4)  // 16 rows of the widest type
+#define DN_EXPERT_WORDS (DN_ROWS * DN_NB * DN_MAX_BB / 4)  // R rows of the widest type
+#define DN_ROW_LOADS (DN_ROWS / 4)                          // 16-byte loads per lane of a wave's rows
+#define DN_SH_PASSES (DN_ROWS / 8)                          // shared down rows per wave
+static_assert(DN_ROWS == 8 || DN_ROWS == 16, "the two builds");
 #define DN_SH_MAX_F 1024
 #define DN_BLOCK_STRIDE 132  // floats per 128-block in LDS (bank spread)
 
 
+// Half hf of block blk of staged row r (R = 8), or the sum of its two halves (R = 16),
+// against the block's activations x (128 fp32); each half's scaled dot rounded on its own.
 template <int ID>
-__device__ __forceinline__ float dx_unit(const uint32_t *rows_k, uint32_t r, uint32_t blk, const uint32_t *book,
-                                         const float *x) {
+__device__ __forceinline__ float dx_unit(const uint32_t *rows_k, uint32_t r, uint32_t blk, uint32_t hf,
+                                         const uint32_t *book, const float *x) {
     constexpr int BB = GyroT<ID>::BB, NW = gyro_nw<ID>();
     const uint32_t off = r * (DN_NB * BB) + blk * BB;  // even
     const uint32_t *w0 = rows_k + (off >> 2);
@@ -45,10 +61,17 @@ __device__ __forceinline__ float dx_unit(const uint32_t *rows_k, uint32_t r, uin
     float sc;
     uint32_t w[NW];
     gyro_unpack<ID>(d, (off & 2u) != 0u, sc, w);
-    return gd_rounded(sc * gyro_block_dot<ID>(w, book, x));
+#if DN_ROWS == 8
+    return gd_rounded(sc * gyro_half_dot<ID>(w, hf, book, x + 64u * hf));
+#else
+    const float h0 = gd_rounded(sc * gyro_half_dot<ID>(w, 0u, book, x));
+    const float h1 = gd_rounded(sc * gyro_half_dot<ID>(w, 1u, book, x + 64u));
+    return h0 + h1;
+#endif
 }
 
-GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
+#define DX_DEFINE(NAME, WG) GD_PIPELINE_NAMED(NAME, WG)  // expands NAME before it is named
+DX_DEFINE(DX_PIPELINE, 512) {
     __shared__ uint4 book4[512];
     __shared__ uint32_t rows[DN_U * DN_EXPERT_WORDS];
     __shared__ float act[DN_U * DN_NB * DN_BLOCK_STRIDE];
@@ -84,19 +107,23 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
         for (int j = 0; j < 2; ++j) s4[j] = S[j];
     }
     const gd_u32x4 cbv = gd_global4(gd_buf<const uint32_t>(a, a.c[10]))[tid];
-    // Shared expert inputs: thread (r = tid / 32, q = tid % 32) holds 8 bf16 of down row
-    // row0 + r at columns 8 q + 256 m; thread tid holds the gate and up values of columns
-    // tid + 512 i.
+    // Shared expert inputs: lane q of wave w holds 8 bf16 of down row row0 + w + 8 ps (pass
+    // ps) at columns 8 q + 512 m; thread tid holds the gate and up values of columns tid + 512 i.
     const bool shared = a.c[24] != 0u;
     const uint32_t SF = shared ? a.c[30] : 0u;
-    gd_u32x4 sw[DN_SH_MAX_F / 256];
+    constexpr int SHM = DN_SH_MAX_F / 512;
+    gd_u32x4 sw[DN_SH_PASSES][SHM];
     float shgv[DN_SH_MAX_F / 512], shuv[DN_SH_MAX_F / 512];
     if (shared) {
-        const uint32_t *Wsd = gd_buf<const uint32_t>(a, a.c[29]) + ((size_t)(row0 + (tid >> 5)) * SF + 8u * (tid & 31u)) / 2u;
         gd_guint *Hs = gd_global(gd_buf<const uint32_t>(a, a.c[25]) + (size_t)t * 2u * SF);
 #pragma unroll
-        for (int m = 0; m < DN_SH_MAX_F / 256; ++m)
-            if (256u * m < SF) sw[m] = *gd_global4(Wsd + 128u * m);
+        for (int ps = 0; ps < DN_SH_PASSES; ++ps) {
+            const uint32_t *Wsd =
+                gd_buf<const uint32_t>(a, a.c[29]) + ((size_t)(row0 + wave + 8u * ps) * SF + 8u * lane) / 2u;
+#pragma unroll
+            for (int m = 0; m < SHM; ++m)
+                if (8u * lane + 512u * m < SF) sw[ps][m] = *gd_global4(Wsd + 256u * m);
+        }
 #pragma unroll
         for (int m = 0; m < DN_SH_MAX_F / 512; ++m)
             if (tid + 512u * m < SF) {
@@ -105,8 +132,8 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
             }
     }
 
-    // The 16 rows of expert `wave`: 4 bb (at most 232) chunks of 16 bytes, four loads per lane,
-    // every address clamped into the expert's rows.
+    // The R rows of expert `wave`: R bb / 4 (at most 232) chunks of 16 bytes, R / 4 loads per
+    // lane, every address clamped into the expert's rows.
     cuint *ids = as_const(gd_buf<const uint32_t>(a, a.c[2]) + a.c[3] + t * DN_U);
     // The route weights too, so their latency overlaps the rows' (they are read at the end).
     cfloat *wtp = as_const(gd_buf<const float>(a, a.c[4]) + a.c[5] + t * DN_U);
@@ -116,11 +143,12 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[6]);
     const uint32_t ew = min(ids[wave], NE - 1u);
     const uint32_t type_id = (xt[ew].types >> 16) & 0xffu;
-    const uint32_t bbw = block_bytes_of_type(type_id), nch = 4u * bbw;
+    const uint32_t bbw = block_bytes_of_type(type_id), nch = DN_ROWS / 4u * bbw;
     const uint8_t *src = reinterpret_cast<const uint8_t *>(xt[ew].down) + (size_t)row0 * DN_NB * bbw;
-    gd_u32x4 rv[4];
+    gd_u32x4 rv[DN_ROW_LOADS];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) rv[j] = *gd_global4(reinterpret_cast<const uint32_t *>(src + min(lane + 64u * j, nch - 1u) * 16u));
+    for (int j = 0; j < DN_ROW_LOADS; ++j)
+        rv[j] = *gd_global4(reinterpret_cast<const uint32_t *>(src + min(lane + 64u * j, nch - 1u) * 16u));
 
     float v[8];
 #pragma unroll
@@ -183,7 +211,7 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     reinterpret_cast<gd_u32x4 *>(book4)[tid] = cbv;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < DN_ROW_LOADS; ++j) {
         const uint32_t c = lane + 64u * j;
         if (c < nch) {
             uint32_t *rdst = rows + wave * DN_EXPERT_WORDS + c * 4u;
@@ -192,35 +220,49 @@ GD_PIPELINE_NAMED(moe_decode_down_x, 512) {
     }
     __syncthreads();
 
-    {   // Unit (row r = lane / 4, block blk = lane % 4) of expert `wave`, with its down type.
-        const uint32_t r = lane >> 2, blk = lane & 3u;
+    {   // Unit (row r, block blk, half hf) of expert `wave` on lane 8 r + 2 blk + hf (R = 8), or
+        // (row r, block blk, both halves) on lane 4 r + blk (R = 16), with the expert's down type.
+#if DN_ROWS == 8
+        const uint32_t r = lane >> 3, blk = (lane >> 1) & 3u, hf = lane & 1u;
+#else
+        const uint32_t r = lane >> 2, blk = lane & 3u, hf = 0u;
+#endif
         const uint32_t *rows_k = rows + wave * DN_EXPERT_WORDS;
         const uint32_t *book = reinterpret_cast<const uint32_t *>(book4);
         const float *xa = act + (wave * DN_NB + blk) * DN_BLOCK_STRIDE;
         float s = 0.f;
-#define DX_CASE(ID) s = dx_unit<ID>(rows_k, r, blk, book, xa)
+#define DX_CASE(ID) s = dx_unit<ID>(rows_k, r, blk, hf, book, xa)
         GYRO_TYPE_SWITCH(type_id, DX_CASE)
 #undef DX_CASE
+#if DN_ROWS == 8
+        s = s + gd_dpp_f<0xB1>(s);   // the two halves of a block
+        s = s + gd_dpp_f<0x4E>(s);   // b0 + b1, b2 + b3
+        s = s + gd_dpp_f<0x104>(s);  // row_shl:4: (b0 + b1) + (b2 + b3) in lane 8 r
+        if ((lane & 7u) == 0u) dk[wave][r] = s;
+#else
         s = s + gd_dpp_f<0xB1>(s);  // b0 + b1, b2 + b3
         s = s + gd_dpp_f<0x4E>(s);  // (b0 + b1) + (b2 + b3)
         if (blk == 0) dk[wave][r] = s;
+#endif
     }
-    if (shared) {  // shared down row row0 + tid / 32 over 32 lanes
-        float p = 0.f;
-        const uint32_t q = tid & 31u;
+    if (shared) {  // shared down rows row0 + wave + 8 ps over the wave's 64 lanes
 #pragma unroll
-        for (int m = 0; m < DN_SH_MAX_F / 256; ++m) {
-            if (256u * m >= SF) break;
-            const float *av = sh_a + 8u * q + 256u * m;
+        for (int ps = 0; ps < DN_SH_PASSES; ++ps) {
+            float p = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                p += gd_bits_f32(sw[m][e] << 16) * av[2 * e];
-                p += gd_bits_f32(sw[m][e] & 0xffff0000u) * av[2 * e + 1];
+            for (int m = 0; m < SHM; ++m) {
+                if (8u * lane + 512u * m < SF) {
+                    const float *av = sh_a + 8u * lane + 512u * m;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        p += gd_bits_f32(sw[ps][m][e] << 16) * av[2 * e];
+                        p += gd_bits_f32(sw[ps][m][e] & 0xffff0000u) * av[2 * e + 1];
+                    }
+                }
             }
+            p = gd_wave_sum_dpp(p);
+            if (lane == 0u) shs[wave + 8u * ps] = p;
         }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
-        if (q == 0) shs[tid >> 5] = p;
     }
     __syncthreads();
     if (tid < DN_ROWS) {

@@ -909,12 +909,15 @@ class Engine {
                              {B.logits, B.logits_off, NE, U, bits(L.scale), B.ids, B.ids_off, B.weights, B.weights_off, B.xh, B.xh_off,
                               L.xtab.srv, codebook.srv, B.gu, B.gu_off, E, F, n},
                              F / 64, 2 * parts, n * U);
-        dispatch_maybe_timed(bracket == 3, marks, "moe_decode_down_x",
+        // One token: 8 rows per group (E / 8 groups fill the GPU); more: 16 (E / 16 per token),
+        // the same sums in the same order.
+        const bool dx8 = n == 1;
+        dispatch_maybe_timed(bracket == 3, marks, dx8 ? "moe_decode_down_x" : "moe_decode_down_xb",
                              {B.gu, B.gu_off, B.ids, B.ids_off, B.weights, B.weights_off, L.xtab.srv, 0, 0, 0, codebook.srv,
                               L.has_down_signs ? L.signs.srv : kNone, E, out_uav, out_off, E, F, U, n, parts, NE,
                               st.res_uav != kNone ? 1u : 0u, st.res_uav, st.res_off, rsf ? 1u : 0u, B.sh_h, 0,
                               B.sh_g, 0, rsf ? L.sh_down.srv : 0u, rsf},
-                             E / 16, n);
+                             dx8 ? E / 8 : E / 16, n);
     }
 
     // The grouped-GEMM path feeds binary16 weights (block scale x codebook value) to the MFMA;

@@ -58,5 +58,5 @@ def test_kernels_built():
                  "moe_combine", "ew", "gyro_decode", "linalg_smoke", "moe_gyro_x"}
     fast = {"moe_router", "moe_decode_gu", "moe_decode_gu_b", "moe_decode_down", "moe_dequant", "moe_prefill_router",
             "moe_prefill_topk", "moe_prefill_sort", "moe_prefill_gu", "moe_prefill_down", "moe_prefill_combine",
-            "moe_stack_norm", "moe_decode_gu_x", "moe_decode_gu_xb", "moe_decode_down_x", "moe_decode_down_g", "moe_decode_gu_g", "moe_decode_gu_xg", "moe_decode_down_xg", "moe_prefill_gu_x", "moe_prefill_down_x", "gd_table_set"}
+            "moe_stack_norm", "moe_decode_gu_x", "moe_decode_gu_xb", "moe_decode_down_x", "moe_decode_down_xb", "moe_decode_down_g", "moe_decode_gu_g", "moe_decode_gu_xg", "moe_decode_down_xg", "moe_prefill_gu_x", "moe_prefill_down_x", "gd_table_set"}
     assert reference | fast <= kernels, (reference | fast) - kernels

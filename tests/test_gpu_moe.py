@@ -93,17 +93,20 @@ def test_decode_batch_parity(engine, tokens, reference, oracle_mod):
     assert_close(oracle_mod, ref[:4], out, "decode batch 4")
 
 
-@pytest.mark.parametrize("kind", ["tq2_t", "type148", "mixed"])
+@pytest.mark.parametrize("kind", ["tq2_t", "type148", "mixed", "mixed_shared"])
 def test_decode_batch_builds_bit_equal(oracle_mod, kind):
     """The decode gate/up kernels come in two builds of one source: one token per call runs
     moe_decode_gu / moe_decode_gu_x (a block's activations copied into registers at once), 2 to 8
-    tokens run moe_decode_gu_b / moe_decode_gu_xb (read from LDS step by step, fewer VGPRs). Both
-    compute the same products in the same order and round the block scale's product explicitly,
-    so a batch of 8 must equal the 8 tokens run one at a time bit for bit (and meet the oracle
-    bar)."""
+    tokens run moe_decode_gu_b / moe_decode_gu_xb (read from LDS step by step, fewer VGPRs). The
+    type-generic down kernel too: moe_decode_down_x (8 output rows per group, a half block per
+    lane) and moe_decode_down_xb (16 rows, both halves per lane), with the shared expert's down
+    rows summed the same way in both. Each pair computes the same products and sums in the same
+    order and rounds the block scale's product explicitly, so a batch of 8 must equal the 8
+    tokens run one at a time bit for bit (and meet the oracle bar)."""
     L = {"tq2_t": lambda: synth.make_layer(131),
          "type148": lambda: synth.make_layer(132, type_id=148),
-         "mixed": lambda: synth.make_layer(133, mixed_types=True)}[kind]()
+         "mixed": lambda: synth.make_layer(133, mixed_types=True),
+         "mixed_shared": lambda: synth.make_layer(135, mixed_types=True, SF=1024)}[kind]()
     x = synth.make_tokens(134, 8)
     eng = Engine(max_tok=8)
     try:

@@ -113,10 +113,12 @@ def sequence(kind: str, ns):
             down = ("moe_decode_down_gl",) + down[1:]
         return [block(*DECODE_TQ2)[0], gu, down]
     if kind == "decode_x":
-        # The document's rule: moe_decode_gu_xb, same constants and grid, for 2 to 8 tokens.
+        # The document's rules for 2 to 8 tokens: moe_decode_gu_xb with the same constants and
+        # grid, moe_decode_down_xb with the same constants and E / 16 groups per token.
         router, gu, down = block(*DECODE_X)
         if ns.n > 1:
             gu = ("moe_decode_gu_xb",) + gu[1:]
+            down = ("moe_decode_down_xb", down[1], zig_expr("E / 16, n, 1"))
         return [router, gu, down]
     if kind == "decode_xg":
         return [block(*DECODE_TQ2)[0], *block(*DECODE_XG)]
