@@ -1009,7 +1009,7 @@ class Engine {
         if (L.SF) {
             // Shared expert (bracket 7): a = silu(W_g x) * W_u x into sh_a (binary16), then
             // W_d a into sh_o; the combine adds sigmoid(x . shared_gate) * sh_o.
-            const uint32_t tt = (n + 63) / 64;
+            const uint32_t tt = (n + 31) / 32;
             dispatch_maybe_timed(bracket == 7, marks, "moe_prefill_shared",
                                  {0, x16.uav, 0, E, L.sh_gu16.srv, 0, E, sh_a.uav, 0, n, L.SF, bits(L.sh_unscale[0]),
                                   bits(L.sh_unscale[1]), L.SF, flag_uav()},
