@@ -7,15 +7,15 @@
 //   mode 1 (down):     o[t][r] = W_d[r] . a[t]  (fp32)
 // The activations are binary16 rows (x unrotated, from moe_prefill_router).
 //
-// Group: 32 tokens x 128 weight rows, four waves, K blocks of 64 in a three-buffer pipeline of
-// direct global-to-LDS loads (ggemm.h) two blocks ahead. Mode 0 stages gate rows j0 .. j0 + 63
+// Group: 32 tokens x 128 weight rows, four waves, K blocks of 64 in a five-buffer pipeline of
+// direct global-to-LDS loads (ggemm.h) four blocks ahead. Mode 0 stages gate rows j0 .. j0 + 63
 // and up rows j0 .. j0 + 63 (a columns j0 .. + 63); mode 1 stages down rows c0 .. c0 + 127.
 // Wave w computes the 32 tokens against staged rows 32 w .. + 31 with one
 // v_mfma_f32_32x32x16_f16 per K-step, so in mode 0 waves 0, 1 hold gate and waves 2, 3 the
 // matching up products. 32-token groups give 512-token calls 256 groups, one per CU. LDS rows
 // are 128 bytes (8 chunks of 16); chunk c of row r sits at position c ^ ((r / 2) % 8), so the 16
 // lanes of one ds_read_b128 pass (rows r .. r + 15 at one chunk) cover all 64 banks.
-// Grid: mode 0 (SF / 64, ceil(n / 32)), mode 1 (E / 128, ceil(n / 32)); 256 threads; 60 KB LDS.
+// Grid: mode 0 (SF / 64, ceil(n / 32)), mode 1 (E / 128, ceil(n / 32)); 256 threads; 100 KB LDS.
 // Requires K % 64 == 0 and the A rows' and weight rows' lengths multiples of 8 values.
 // Constants: 0 mode 1 a_uav 2 a_off (words) 3 lda (values per A row) 4 w_srv 5 w_off (words)
 // 6 K 7 out_uav 8 out_off (words) 9 n_tok 10 up_row0 (mode 0: first up row, = SF) 11 scale0
@@ -26,18 +26,22 @@
 
 #define SH_TM 32
 #define SH_TN 128
-#define SH_NBUF 3
+#define SH_NBUF 5  // K blocks kb .. kb + 4 in LDS: four blocks ahead
 
 struct __attribute__((aligned(16))) ShLds {
     gd_u32x4 a[SH_NBUF][SH_TM * 8];
     gd_u32x4 b[SH_NBUF][SH_TN * 8];
 };
 
-// Start of K block kb: at most the 5 loads of block kb + 1 (1 activation, 4 weight) are this
-// wave's outstanding ones.
+// Start of K block kb: at most the 5 loads per block (1 activation, 4 weight) of blocks
+// kb + 1 .. kb + 3 are this wave's outstanding ones.
 __device__ __forceinline__ void sh_sync(uint32_t kb, uint32_t nk) {
-    if (kb + 1u < nk) gg_sync<5>();
-    else gg_sync<0>();
+    switch (min(nk - 1u - kb, SH_NBUF - 2u)) {
+        case 3: gg_sync<15>(); break;
+        case 2: gg_sync<10>(); break;
+        case 1: gg_sync<5>(); break;
+        default: gg_sync<0>(); break;
+    }
 }
 
 // Block kb into buffer buf: wave w issues activation load w and weight loads 4 w .. 4 w + 3;
@@ -59,7 +63,7 @@ __device__ __forceinline__ void sh_step(ShLds &sm, uint32_t kb, uint32_t nk, uin
                                         const void *abase, uint32_t aoff, const void *wbase, const uint32_t woff[4],
                                         f32x16 &acc) {
     sh_sync(kb, nk);
-    if (kb + 2u < nk) sh_stage(sm, (BUF + 2) % 3, wave, abase, aoff, wbase, woff, kb + 2u);
+    if (kb + SH_NBUF - 1u < nk) sh_stage(sm, (BUF + SH_NBUF - 1) % SH_NBUF, wave, abase, aoff, wbase, woff, kb + SH_NBUF - 1u);
     const uint32_t rb = wave * 32u + m;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -95,14 +99,16 @@ GD_PIPELINE_NAMED(moe_prefill_shared, 256) {
         woff[i] = row * K * 2u + q * 16u;
     }
     sh_stage(sm, 0, wave, abase, aoff, wbase, woff, 0);
-    if (nk > 1u) sh_stage(sm, 1, wave, abase, aoff, wbase, woff, 1);
+    for (uint32_t b = 1; b < nk && b < SH_NBUF - 1u; ++b) sh_stage(sm, b, wave, abase, aoff, wbase, woff, b);
 
     const uint32_t m = lane & 31u, h = lane >> 5;
     f32x16 acc = {};
-    for (uint32_t kb = 0; kb < nk; kb += 3u) {
+    for (uint32_t kb = 0; kb < nk; kb += SH_NBUF) {
         sh_step<0>(sm, kb, nk, wave, m, h, abase, aoff, wbase, woff, acc);
         if (kb + 1u < nk) sh_step<1>(sm, kb + 1u, nk, wave, m, h, abase, aoff, wbase, woff, acc);
         if (kb + 2u < nk) sh_step<2>(sm, kb + 2u, nk, wave, m, h, abase, aoff, wbase, woff, acc);
+        if (kb + 3u < nk) sh_step<3>(sm, kb + 3u, nk, wave, m, h, abase, aoff, wbase, woff, acc);
+        if (kb + 4u < nk) sh_step<4>(sm, kb + 4u, nk, wave, m, h, abase, aoff, wbase, woff, acc);
     }
     gg_sync<0>();  // every wave is done with the buffers
 
