@@ -74,6 +74,7 @@ ROUTER_BYTES = N_EXPERT * E * 4  # fp32 router matrix read per layer and step
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_gu_traffic.md"
 TRACE_FILE = ROOT / "profiles" / "moe_decode_kernels_b1.md"
 GU_BLOCKS_PER_LAUNCH = TOP_K * 2 * F * (E // 128)  # 131,072 TQ2_T blocks of 128 weights
+BLOCKS_PER_EXPERT = 2 * F * (E // 128) + E * (F // 128)  # 24,576: an expert's gate, up and down blocks
 CUS = 256
 PARITY_TOKENS = 1000
 GEMM_COUNTERS_FILE = ROOT / "profiles" / "moe_prefill_gemm_counters.md"
@@ -396,6 +397,11 @@ def stack_bench(args):
             print(f"stack: {l + 1} of {n_layers} layers resident ({time.perf_counter() - t0:.0f} s)",
                   file=sys.stderr, flush=True)
     bundle_all = n_layers * N_EXPERT * BUNDLE_BYTES
+    # The trellis decode's own ceiling: every decoded 128-weight block costs the codebook gathers
+    # whose chip-wide rate decode_gather_probe measures (both paths gather from the same LDS
+    # codebook, two 4-byte gathers per state). Decode decodes every slot's expert blocks; prefill
+    # every tile's (a tile: up to 128 sorted slots of one expert).
+    probe = gather_probe()
     points = []
     sweep = ((1, PATH_DECODE, 200), (8, PATH_DECODE, 100), (32, PATH_PREFILL, 50), (64, PATH_PREFILL, 50),
              (4096, PATH_PREFILL, 4))
@@ -407,14 +413,16 @@ def stack_bench(args):
         dev_ms, wall_ms = eng.run_stack(path, batch, calls, ids)
         # Measured distinct experts per layer on the first batch: the stack's prefix up to each
         # layer, then that layer's routes.
-        distinct = []
-        if batch <= 64:
-            for l in range(n_layers):
-                eng.forward_stack(ids[:l + 1], x[:batch], path)
-                r, _ = eng.last_routes(batch)
-                distinct.append(int(np.unique(r).size))
-        else:
-            distinct = [N_EXPERT] * n_layers  # every expert at 4096 tokens
+        distinct, tiles = [], []
+        for l in range(n_layers if batch <= 64 else 1):
+            eng.forward_stack(ids[:l + 1], x[:batch], path)
+            r, _ = eng.last_routes(batch)
+            counts = np.bincount(r.ravel(), minlength=N_EXPERT)
+            distinct.append(int((counts > 0).sum()))
+            tiles.append(int(((counts + 127) // 128).sum()))
+        if batch > 64:  # every expert at 4096 tokens; tiles of the first layer for every layer
+            distinct = [N_EXPERT] * n_layers
+            tiles = tiles * n_layers
         step_s = wall_ms / calls * 1e-3
         step_bytes = sum(distinct) * BUNDLE_BYTES + n_layers * ROUTER_BYTES
         flops = batch * n_layers * LAYER_FLOPS_PER_TOKEN
@@ -422,13 +430,21 @@ def stack_bench(args):
         tflops = flops / step_s / 1e12
         bound = "hbm" if step_bytes / (HBM_PEAK_GBS * 1e9) > flops / (MFMA_PEAK_TFLOPS * 1e12) else "mfma"
         frac = hbm_gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / MFMA_PEAK_TFLOPS
+        units = batch * TOP_K * n_layers if path == PATH_DECODE else sum(tiles)
+        blocks = units * BLOCKS_PER_EXPERT
+        gather_ms = blocks / probe["blocks_per_s"] * 1e3
         points.append({"batch": batch, "path": "decode" if path == PATH_DECODE else "prefill", "calls": calls,
                        "tok_s": round(batch / step_s, 1), "ms_per_step": round(step_s * 1e3, 4),
                        "device_ms_per_step": round(dev_ms / calls, 4),
                        "distinct_experts_per_layer": round(sum(distinct) / n_layers, 1),
                        "bytes_per_step": step_bytes, "flops_per_step": flops,
                        "hbm_gbs": round(hbm_gbs, 1), "tflops": round(tflops, 2),
-                       "roofline": {"bound": bound, "frac": round(frac, 4)}})
+                       "roofline": {"bound": bound, "frac": round(frac, 4)},
+                       "gather_roof": {"bound": "lds codebook gathers",
+                                       "decoded_blocks_per_step": blocks,
+                                       "decoded": "slot experts" if path == PATH_DECODE else
+                                                  ("sort tiles" if batch <= 64 else "sort tiles (first layer's x layers)"),
+                                       "ceiling_ms": round(gather_ms, 4), "frac": round(gather_ms / (step_s * 1e3), 4)}})
         print(f"stack: batch {batch}: {points[-1]['tok_s']} tok/s", file=sys.stderr, flush=True)
     eng.close()
     return {
@@ -436,6 +452,7 @@ def stack_bench(args):
                     f"{N_EXPERT} TQ2_T experts per layer, top-{TOP_K}, F {F}",
         "layers": n_layers, "resident_expert_bytes": bundle_all,
         "hbm_peak_gbs": HBM_PEAK_GBS, "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
+        "gather_probe": {"blocks_per_clk_per_cu": probe["blocks_per_clk_per_cu"], "clock_ghz": probe["clock_ghz"]},
         "points": points,
         "cpu_baseline": {"value": round(8 / cpu_s, 2), "unit": "tok/s", "cores": threads, "kind": "port",
                          "sample": f"8 decode tokens through all {n_layers} layers, {cpu_s:.1f} s on {threads} threads"},
