@@ -282,6 +282,9 @@ def prefill_bench(eng, layer, args):
     eng.forward(layers[0], x[:PREFILL_TOKENS], PATH_PREFILL)
     ids, _ = eng.last_routes(PREFILL_TOKENS)
     distinct = int(np.unique(ids).size)
+    n_tiles = int(eng.last_tiles().shape[0])
+    # The GEMMs' decode-gather ceiling: each tile decodes all of its expert's blocks once.
+    gather_s = n_tiles * BLOCKS_PER_EXPERT / gather_probe()["blocks_per_s"]
     t_call = wall_ms / batches * 1e-3
     t_dev = dev_ms / batches * 1e-3
     gemm_s = sum(us[name] for name, _ in gemms) * 1e-6
@@ -298,6 +301,9 @@ def prefill_bench(eng, layer, args):
         "grouped_gemm_tflops": round(PREFILL_FLOPS / gemm_s / 1e12, 1),
         "grouped_gemm_frac_of_peak": round(PREFILL_FLOPS / gemm_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "distinct_experts": distinct, "expert_bytes": distinct * BUNDLE_BYTES,
+        "gather_roof": {"bound": "lds codebook gathers", "kernel": " + ".join(name for name, _ in gemms),
+                        "tiles": n_tiles, "decoded_blocks": n_tiles * BLOCKS_PER_EXPERT,
+                        "ceiling_us": round(gather_s * 1e6, 2), "frac": round(gather_s / gemm_s, 4)},
         "block_scales": BLOCK_SCALES,
         # The grouped GEMMs' roofline: routed-expert FLOPs over the GEMM launch's dispatch time
         # (measured above); the counter pass's MFMA-busy and useful-work fractions of the
