@@ -70,6 +70,17 @@ def test_decode_path_mixed_quant_and_shared(oracle_mod):
     check(oracle_mod, shared, synth.make_tokens(115, 5, shared.E), PATH_DECODE, "decode mixed + shared n=5")
 
 
+def test_decode_path_mixed_hidden_1024(oracle_mod):
+    """The same kernels at hidden 1024 (E / 8 = 128 down groups for one token, 8 rows each;
+    E / 16 per token for 2 to 8 tokens), with a shared expert of width 256 and without."""
+    from gyrodx.engine import PATH_DECODE
+    for seed, SF in ((121, 0), (123, 256)):
+        layer = synth.make_layer(seed, E=1024, F=512, n_expert=64, n_used=8, mixed_types=True, SF=SF)
+        for n in (1, 3, 8):
+            check(oracle_mod, layer, synth.make_tokens(seed + n, n, layer.E), PATH_DECODE,
+                  f"decode mixed E=1024 SF={SF} n={n}")
+
+
 @pytest.mark.parametrize("type_id", [145, 147, 149, 151])
 def test_decode_path_uniform_other_types(oracle_mod, type_id):
     """Uniform non-TQ2_T layers (32- and 64-step trellises) through the type-generic decode."""
