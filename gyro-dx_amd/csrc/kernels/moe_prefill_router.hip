@@ -1,153 +1,181 @@
-// Prefill path, step 1: router logits of many tokens on fp32 MFMA, and the rotated expert
-// input in binary16.
+// Prefill path, step 1: router logits of many tokens on binary16 MFMA with split operands, and
+// the rotated expert input in binary16.
 //   logits[t][r] = W_r[r] . x[t] (+ bias[r])          src/engine.zig:526 (kernels.matmul)
 //   xh16[t]      = H_128 (gate_signs * x[t]) per 128-block, as binary16 pairs
 //                                                      src/engine.zig:547-551
+// Split operands. Each fp32 value v is carried as two binary16 values, v = hi + lo 2^-11 with
+// hi = f16(v) and lo = f16((v - hi) 2^11) (both round to nearest even; v - hi is exact in fp32):
+// 22 significant bits instead of fp32's 24, over the binary16 range of hi. The products that
+// matter, x.w = hi_x hi_w + 2^-11 (hi_x lo_w + lo_x hi_w) (dropping lo_x lo_w, 2^-22 relative),
+// run as three v_mfma_f32_32x32x16_f16 with fp32 accumulation, about a fifth of the issue time of
+// fp32 MFMA. The router rows come split at load time (the layout below), each row scaled by a
+// power of two 2^k_r so that its largest |weight| lies in [2^14, 2^15); the logit is multiplied
+// by 2^-k_r at the end. The tokens are split here as they are staged; a value beyond 65504 sets
+// the range flag (the caller then recomputes the call on fp32 weights and activations).
 // Group (bx, by, bz) computes the 32 x 32 logit tile of tokens 32 bx.. and experts 32 by.. over
-// K range bz of S (the K split, chosen by the host so that small batches still fill the GPU)
-// with v_mfma_f32_32x32x2_f32; its waves 0..3 split the range into quarters and their partial
-// tiles are added in wave order through LDS. Range bz writes logit plane bz; the top-k kernel
-// adds the S planes in plane order. The MFMA operands take one row per lane, so each of these
-// waves stages its own 16-wide K chunks of the 32 token rows and the 32 router rows into LDS
-// first: direct global-to-LDS loads (4 lanes per 64-byte row, whole rows per load), the
-// 16-byte chunk q of row r stored at position q ^ ((r / 2) % 4), four chunks ahead in five
-// buffers per wave; only the wave's own load count is waited for, so the K loop has no barrier.
-// A group takes 80 KB of LDS and at most 128 VGPRs, so that grids of more than one group per
-// CU (4096 tokens: 1024 groups) run two groups per CU. A wave's MFMA holds back that wave's
-// following instructions until it has nearly finished (other waves issue meanwhile), so each
-// chunk's eight MFMAs carry the chunk's other work one piece at a time: a staging load after
-// each of the first four, the reads of chunk c + 1 (into the other of two operand sets, no
-// copies) after the next two. Lane half h takes k + 4h .. k + 4h + 3 of every 8 for both operands, so
-// every product x[t][k] W[r][k] enters the sum once. Waves 4..7 meanwhile rotate: all
-// n * E/128 blocks are spread over the rotation waves of the grid, eight blocks per wave at a
-// time, so the rotation's memory traffic and VALU work overlap the MFMA chains on the same
-// SIMDs.
-// Grid: (ceil(n / 32), ceil(n_expert / 32), S); 512 threads, 80 KB of LDS (two groups per CU).
-// Requires E % (128 S) == 0.
+// K range bz of S (the K split, chosen by the host so that small batches still fill the GPU);
+// its waves 0..3 split the range into quarters and their partial tiles are added in wave order
+// through LDS. Range bz writes logit plane bz; the top-k kernel adds the S planes in plane
+// order. Each of these waves stages its own 32-wide K chunks of the 32 token rows (fp32) and the
+// 32 router rows (split) into LDS first: direct global-to-LDS loads (8 lanes per 128-byte row,
+// so that every load instruction fetches whole cache lines; 64-byte rows took the K loop about
+// 2 µs longer at 1024 tokens), the 16-byte piece q of row r stored at position q ^ (r % 8), two
+// chunks ahead in three buffers per wave; only the wave's own load count is waited for, so the K
+// loop has no barrier. A group takes 96 KB of LDS, one group per CU. Lane half h of a wave takes
+// k = 8h .. 8h + 7 of every 16-K step for both operands (the MFMA's operand layout), so every
+// product x[t][k] W[r][k] enters the sum once. Waves 4..7 meanwhile rotate: all n * E/128
+// blocks are spread over the rotation waves of the grid, eight blocks per wave at a time, so the
+// rotation's memory traffic and VALU work overlap the MFMA chains on the same SIMDs.
+// Grid: (ceil(n / 32), ceil(n_expert / 32), S); 512 threads, 96 KB of LDS. Requires
+// E % (128 S) == 0.
+// Router layout (router_srv, from router_off): row r, chunk c (k = 16 c .. 16 c + 15) at word
+// 16 (r E / 16 + c): the 16 hi values, then the 16 lo values, as binary16; after the n_expert x E
+// words, the n_expert factors 2^-k_r (fp32).
 // Constants: 0 x_uav 1 x_off (words; rows of E floats) 2 n_tok 3 E 4 router_srv 5 router_off
 // 6 n_expert 7 bias_srv (0xffffffff: none) 8 bias_off 9 logits_uav 10 logits_off
 // 11 signs_srv (0xffffffff: no rotation, plain conversion) 12 signs_off 13 xh16_uav
 // 14 xh16_off (words) 15 x16 (1: also write the unrotated input as binary16, for the shared
 // expert; zero when the caller passes 15 constants) 16 x16_uav 17 x16_off (words) 18 S (0 or
 // 1: no split; plane z at logits_off + z n n_expert; the bias enters plane 0) 19 range flag
-// (table index of a word set to 1 when a value written as binary16 is outside its range; 0:
-// none) 20 hist_uav (0: none) 21 hist_off (words) 22 hist_words: the rotation waves zero these
-// words of moe_prefill_topk's chunk histogram.
+// (table index of a word set to 1 when a value written or split as binary16 is outside its
+// range; 0: none) 20 hist_uav (0: none) 21 hist_off (words) 22 hist_words: the rotation waves
+// zero these words of moe_prefill_topk's chunk histogram.
 #include "ggemm.h"
 #include "fwht.h"
 
 #define RT_WAVES 4
-#define RT_KC 16    // K per staged chunk
-#define RT_NBUF 5    // chunks c .. c + 4 of a wave in LDS: four chunks (16 KB) in flight
-#define RT_LOADS 4   // global-to-LDS loads per chunk: two of token rows, two of router rows
+#define RT_KC 32    // K per staged chunk: one 128-byte line of every token row
+#ifndef RT_NBUF
+#define RT_NBUF 3   // chunks c .. c + 2 of a wave in LDS: two chunks (16 KB) in flight
+#endif
+#define RT_LOADS 8  // global-to-LDS loads per chunk: four of token rows, four of router rows
 
-// 80 KB, so that two groups share a CU: the staging buffers of the four K waves; after its K
-// loop a wave's partial tile (4 KB, fp32) goes over its own first two activation buffers.
+// The staging buffers of the four K waves; after its K loop a wave's partial tile (4 KB, fp32)
+// goes over its own first activation buffer.
 struct __attribute__((aligned(16))) RtLds {
-    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 64 bytes
+    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 128 bytes
     gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_KC / 4];
 };
-static_assert(sizeof(RtLds) == 81920, "two groups fill the CU's 160 KB");
+static_assert(sizeof(RtLds) <= 163840, "the CU's 160 KB");
 static_assert(sizeof(RtLds::x[0]) >= 32 * 32 * 4, "a wave's partial tile fits its activation buffers");
 
-// Swizzled position of 16-byte chunk q of staged row r: the chunk that the 8 lanes of rows
+// Swizzled position of 16-byte piece q of staged row r: the piece that the 8 lanes of rows
 // m .. m + 7 read at one index sits in 8 different 16-byte bank groups.
-__device__ __forceinline__ uint32_t rt_pos(uint32_t q, uint32_t r) { return q ^ ((r >> 1) & 3u); }
+__device__ __forceinline__ uint32_t rt_pos(uint32_t q, uint32_t r) { return q ^ (r & 7u); }
 
 // Waits until chunk c's loads have landed, with `ahead` later chunks (RT_LOADS loads each) in
 // flight.
 __device__ __forceinline__ void rt_wait(uint32_t ahead) {
     switch (ahead) {
-        case 3: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
         default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
 
-// Stages chunk c (K = kq + 16 c ..) of this wave's 32 token rows and 32 router rows: 2 + 2
-// loads, lane l of load i carrying row 16 i + l / 4, position l % 4.
-__device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf, const void *xbase,
-                                         const void *wbase, const uint32_t xoff[2], const uint32_t woff[2],
-                                         uint32_t kbytes) {
+// Stages a chunk of this wave's 32 token rows and 32 router rows (xk, wk: the bases advanced to
+// the chunk's K offset): 4 + 4 loads, lane l of load i carrying row 8 i + l / 8, position l % 8.
+__device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf, const char *xk, const char *wk,
+                                         const uint32_t xoff[4], const uint32_t woff[4]) {
     const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xbase, xoff[i] + kbytes);
+    for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xk, xoff[i]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wbase, woff[i] + kbytes);
+    for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
 }
 
-// Operands of one staged chunk for this lane (row m, lane half h): two float4 of the token row
-// and two of the router row, k = 8 j + 4 h .. + 3 of the chunk for j = 0, 1.
+// Operands of one K-step (16 K) for this lane (row m, lane half h; k = 8 h .. 8 h + 7 of the
+// step): the token row's values split into hi and lo, and the router row's hi and lo.
 struct RtOps {
-    float4 x[2], w[2];
+    f16x8 xh, xl, wh, wl;
 };
-__device__ __forceinline__ void rt_read(const RtLds &sm, uint32_t wave, uint32_t buf, uint32_t m, uint32_t h, RtOps &o) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t p = rt_pos(2u * (uint32_t)j + h, m);
-        o.x[j] = __builtin_bit_cast(float4, sm.x[wave][buf][m * 4u + p]);
-        o.w[j] = __builtin_bit_cast(float4, sm.w[wave][buf][m * 4u + p]);
-    }
+// The step's raw reads from LDS (step s of the chunk in buffer buf): two 16-byte pieces of the
+// token row (fp32), one of the router row's hi values and one of its lo values. A staged router
+// row holds, per 16 K, the 16 hi values then the 16 lo values.
+struct RtRaw {
+    gd_u32x4 x[2], wh, wl;
+};
+__device__ __forceinline__ void rt_read(const RtLds &sm, uint32_t wave, uint32_t buf, uint32_t s, uint32_t m,
+                                        uint32_t h, RtRaw &o) {
+    o.x[0] = sm.x[wave][buf][m * 8u + rt_pos(4u * s + 2u * h, m)];
+    o.x[1] = sm.x[wave][buf][m * 8u + rt_pos(4u * s + 2u * h + 1u, m)];
+    o.wh = sm.w[wave][buf][m * 8u + rt_pos(4u * s + h, m)];
+    o.wl = sm.w[wave][buf][m * 8u + rt_pos(4u * s + 2u + h, m)];
 }
-// Chunk c's eight MFMAs (operands `cur`) with the chunk's other work between them, so that the
-// matrix pipe always has the next MFMA waiting: the four loads staging chunk c + 4 (into the
-// buffer of chunk c - 1, read into registers two chunks ago) one after each of the first four
-// MFMAs, then the wait for chunk c + 1 and its reads into `next`, two after each of the next
-// two. The following chunk's MFMAs use `next` once the two MFMAs after the reads have issued.
-// STEADY: chunks c + 1 .. c + 4 are all in flight (c + 4 < nc), so the wait is one immediate
-// count; otherwise `ahead` (the chunks issued after chunk c + 1) picks it.
-template <bool STEADY>
-__device__ __forceinline__ void rt_chunk(RtLds &sm, uint32_t wave, uint32_t c, uint32_t nc, uint32_t m, uint32_t h,
-                                         const void *xbase, const void *wbase, const uint32_t xoff[2],
-                                         const uint32_t woff[2], const RtOps &cur, RtOps &next, f32x16 &acc) {
-    const bool stage = STEADY || c + 4u < nc;
-    const uint32_t buf = (c + 4u) % RT_NBUF, kbytes = (c + 4u) * RT_KC * 4u;
-    const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
-    {
-        const float *x0 = reinterpret_cast<const float *>(&cur.x[0]), *w0 = reinterpret_cast<const float *>(&cur.w[0]);
+// hi = f16(v), lo = f16((v - hi) 2^11) of the eight token values; xmax tracks max |v|. The lo
+// value is one mixed-precision fused multiply-add, 2^11 v - 2^11 hi (exact before its rounding
+// to binary16), that reads hi from its half of the packed conversion.
+__device__ __forceinline__ void rt_split(const RtRaw &r, RtOps &o, float &xmax) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    gd_u32x4 xh, xl;
+    const float m2048 = -2048.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[q], w0[q], acc, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (stage) {
-                if (q < 2) gg_dma16(lx + (uint32_t)q * 1024u, xbase, xoff[q] + kbytes);
-                else gg_dma16(lw + (uint32_t)(q - 2) * 1024u, wbase, woff[q - 2] + kbytes);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int j = 0; j < 4; ++j) {
+        const float v0 = gd_bits_f32(r.x[j >> 1][2 * (j & 1)]), v1 = gd_bits_f32(r.x[j >> 1][2 * (j & 1) + 1]);
+        const h2v hi = {(_Float16)v0, (_Float16)v1};
+        const uint32_t hp = __builtin_bit_cast(uint32_t, hi);
+        uint32_t lo;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(hp), "s"(m2048), "v"(v0 * 2048.0f));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(lo)
+            : "v"(hp), "s"(m2048), "v"(v1 * 2048.0f));
+        xh[j] = hp;
+        xl[j] = lo;
+        xmax = fmaxf(xmax, __builtin_fabsf(v0));
+        xmax = fmaxf(xmax, __builtin_fabsf(v1));
     }
-    const bool more = STEADY || c + 1u < nc;
-    if (STEADY) {
-        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // chunks c + 2 .. c + 4 in flight
-    } else if (more) {
-        rt_wait(min(nc - 2u - c, RT_NBUF - 2u));
+    o.xh = __builtin_bit_cast(f16x8, xh);
+    o.xl = __builtin_bit_cast(f16x8, xl);
+    o.wh = __builtin_bit_cast(f16x8, r.wh);
+    o.wl = __builtin_bit_cast(f16x8, r.wl);
+}
+// One K-step's three MFMAs (operands `cur`) with the step's other work between them, so that
+// the matrix pipe has the next MFMA waiting. A chunk takes two steps:
+//  - the first (SECOND false) issues the eight loads staging chunk c + RT_NBUF - 1 (into buffer
+//    bstage, that of chunk c - 1, whose reads are done) around its first two MFMAs, then reads
+//    the chunk's second step from the same buffer (bcur);
+//  - the second waits for chunk c + 1 and reads its first step (buffer bnext).
+// The reads are split into `next` after the third MFMA. The cross products go to acc_x, hi x hi
+// to acc.
+template <bool SECOND>
+__device__ __forceinline__ void rt_step(RtLds &sm, uint32_t wave, uint32_t c, uint32_t nc, uint32_t m, uint32_t h,
+                                        const char *xk, const char *wk, const uint32_t xoff[4], const uint32_t woff[4],
+                                        uint32_t bstage, uint32_t bcur, uint32_t bnext, const RtOps &cur, RtOps &next,
+                                        f32x16 &acc, f32x16 &acc_x, float &xmax) {
+    const bool stage = !SECOND && c + RT_NBUF - 1u < nc;
+    const uint32_t lx = gg_lds_addr(&sm.x[wave][bstage][0]), lw = gg_lds_addr(&sm.w[wave][bstage][0]);
+    acc_x = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wl, acc_x, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (stage) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xk, xoff[i]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t rb = (c + 1u) % RT_NBUF;
-    const float *x1 = reinterpret_cast<const float *>(&cur.x[1]), *w1 = reinterpret_cast<const float *>(&cur.w[1]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wh, acc, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (stage) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[q], w1[q], acc, 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (more) {
-            const uint32_t p = rt_pos(2u * (uint32_t)q + h, m);
-            next.x[q] = __builtin_bit_cast(float4, sm.x[wave][rb][m * 4u + p]);
-            next.w[q] = __builtin_bit_cast(float4, sm.w[wave][rb][m * 4u + p]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
     }
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[2], w1[2], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[3], w1[3], acc, 0, 0, 0);
-    // The operands stay allocated to the end of the chunk: a VGPR written while an MFMA that
-    // reads it is in flight holds the write (and the wave) until the MFMA has read it, about 27
-    // of its 64 cycles; left free, the compiler reuses them for address arithmetic right after
-    // the MFMA that reads them.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        asm volatile("" ::"v"(cur.x[j].x), "v"(cur.x[j].y), "v"(cur.x[j].z), "v"(cur.x[j].w));
-        asm volatile("" ::"v"(cur.w[j].x), "v"(cur.w[j].y), "v"(cur.w[j].z), "v"(cur.w[j].w));
+    const bool more = !SECOND || c + 1u < nc;
+    if (SECOND && more) {
+        if (c + RT_NBUF <= nc) rt_wait(RT_NBUF - 2u);  // chunks c + 2 .. c + RT_NBUF - 1 in flight
+        else rt_wait(nc - 2u - c);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    RtRaw raw;
+    if (more) rt_read(sm, wave, SECOND ? bnext : bcur, SECOND ? 0u : 1u, m, h, raw);
+    __builtin_amdgcn_sched_barrier(0);
+    acc_x = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xl, cur.wh, acc_x, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) rt_split(raw, next, xmax);
+    // The operands stay allocated to the end of the step: a VGPR written while an MFMA that
+    // reads it is in flight holds the write (and the wave) until the MFMA has read it.
+    const gd_u32x4 k0 = __builtin_bit_cast(gd_u32x4, cur.xh), k1 = __builtin_bit_cast(gd_u32x4, cur.xl);
+    const gd_u32x4 k2 = __builtin_bit_cast(gd_u32x4, cur.wh), k3 = __builtin_bit_cast(gd_u32x4, cur.wl);
+    asm volatile("" ::"v"(k0[0]), "v"(k0[1]), "v"(k0[2]), "v"(k0[3]), "v"(k1[0]), "v"(k1[1]), "v"(k1[2]), "v"(k1[3]));
+    asm volatile("" ::"v"(k2[0]), "v"(k2[1]), "v"(k2[2]), "v"(k2[3]), "v"(k3[0]), "v"(k3[1]), "v"(k3[2]), "v"(k3[3]));
 }
 
 // Sixteen values as binary16 pairs (32 bytes) at dst; `bad` records a value outside the range.
@@ -182,67 +210,93 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
         // Router tile, K quarter `wave`.
         const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
         const uint32_t kq = z * ES + wave * (ES / 4u), nc = ES / 4u / RT_KC;
-        uint32_t xoff[2], woff[2];
+        uint32_t xoff[4], woff[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t r = 16u * (uint32_t)i + (lane >> 2), q = rt_pos(lane & 3u, r);
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = rt_pos(lane & 7u, r);
             xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
             woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
         }
-        for (uint32_t c = 0; c < nc && c < RT_NBUF - 1u; ++c) rt_stage(sm, wave, c, X, W, xoff, woff, c * RT_KC * 4u);
+        const char *xb = reinterpret_cast<const char *>(X), *wb = reinterpret_cast<const char *>(W);
+        for (uint32_t c = 0; c < nc && c < RT_NBUF - 1u; ++c)
+            rt_stage(sm, wave, c, xb + c * RT_KC * 4u, wb + c * RT_KC * 4u, xoff, woff);
         // Rows beyond n or n_expert were staged as copies of the last row (finite values); they
         // reach only tile rows and columns that are never stored.
         RtOps ops[2];
-        rt_wait(min(nc - 1u, RT_NBUF - 2u));  // chunks 1 .. 3 may be in flight
-        rt_read(sm, wave, 0, m, h, ops[0]);
-        uint32_t c = 0;
-        for (; c + 5u < nc; c += 2u) {  // chunks c + 4 and c + 5 exist: steady state
-            rt_chunk<true>(sm, wave, c, nc, m, h, X, W, xoff, woff, ops[0], ops[1], acc);
-            rt_chunk<true>(sm, wave, c + 1u, nc, m, h, X, W, xoff, woff, ops[1], ops[0], acc);
+        f32x16 acc_x = {};
+        float xmax = 0.f;
+        rt_wait(min(nc - 1u, RT_NBUF - 2u));  // the chunks after chunk 0 may be in flight
+        {
+            RtRaw raw;
+            rt_read(sm, wave, 0, 0, m, h, raw);
+            rt_split(raw, ops[0], xmax);
         }
-        for (; c < nc; c += 2u) {
-            rt_chunk<false>(sm, wave, c, nc, m, h, X, W, xoff, woff, ops[0], ops[1], acc);
-            if (c + 1u < nc) rt_chunk<false>(sm, wave, c + 1u, nc, m, h, X, W, xoff, woff, ops[1], ops[0], acc);
+        // Chunk c sits in buffer c % RT_NBUF (b); its first step stages chunk c + RT_NBUF - 1
+        // into chunk c - 1's buffer.
+        uint32_t b = 0;
+        for (uint32_t c = 0; c < nc; ++c) {
+            const uint32_t bn = b + 1u == RT_NBUF ? 0u : b + 1u, bs = b == 0u ? RT_NBUF - 1u : b - 1u;
+            const uint32_t kb = (c + RT_NBUF - 1u) * RT_KC * 4u;
+            rt_step<false>(sm, wave, c, nc, m, h, xb + kb, wb + kb, xoff, woff, bs, b, bn, ops[0], ops[1], acc, acc_x,
+                           xmax);
+            rt_step<true>(sm, wave, c, nc, m, h, xb + kb, wb + kb, xoff, woff, bs, b, bn, ops[1], ops[0], acc, acc_x,
+                          xmax);
+            b = bn;
         }
+        gd_range_flag(a.table, a.c[19], !(xmax <= 65504.0f));
         // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m. The wave's
         // buffers are free: its last LDS reads were waited for before its last MFMAs.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[wave * kRedStride + ((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[r];
+        for (int r = 0; r < 16; ++r)
+            red[wave * kRedStride + ((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[r] + acc_x[r] * (1.0f / 2048.0f);
     } else {
         // Rotation share of this group's waves 4..7: each wave transforms eight 128-blocks at a
         // time, an 8-lane group per block holding 16 consecutive values per lane
-        // (gd_fwht128_x16); the blocks b = 8 (first + waves j) + lane / 8.
+        // (gd_fwht128_x16); the blocks b = 8 (first + waves j) + lane / 8. Two such steps run
+        // together, every load of both issued before the first transform.
         const uint32_t nblk = E / 128u, total = n * nblk;
         const uint32_t waves = gridDim.x * gridDim.y * gridDim.z * RT_WAVES;
         const uint32_t first = ((z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * RT_WAVES + (wave - RT_WAVES);
         const bool has_signs = a.c[11] != 0xffffffffu;
-        const float *S = has_signs ? gd_buf<const float>(a, a.c[11]) + a.c[12] : nullptr;
+        const uint32_t *S = has_signs ? gd_buf<const uint32_t>(a, a.c[11]) + a.c[12] : nullptr;
+        const uint32_t *XU = reinterpret_cast<const uint32_t *>(X);
         uint32_t *XH = gd_buf<uint32_t>(a, a.c[13]) + a.c[14];
         const uint32_t l8 = lane & 7u;
         bool bad = false;
-        for (uint32_t g = first; g * 8u < total; g += waves) {
-            const uint32_t b = g * 8u + (lane >> 3);
-            if (b < total) {
-                const uint32_t t = b / nblk, blk = b - t * nblk, i = blk * 128u + 16u * l8;
-                float v[16];
-                const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)t * E + i);
+        for (uint32_t g = first; g * 8u < total; g += 2u * waves) {
+            gd_u32x4 xv[2][4], sv[2][4];
+            uint32_t tk[2], bk[2];
+            bool ok[2];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 f = src[q];
-                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-                }
-                if (a.c[15]) rt_store_h16(gd_buf<uint32_t>(a, a.c[16]) + a.c[17] + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v, bad);
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t b = (g + (uint32_t)u * waves) * 8u + (lane >> 3);
+                ok[u] = b < total;  // the same for the 8 lanes of a block
+                const uint32_t bb = ok[u] ? b : 0u;  // a block that exists: loaded, not used
+                tk[u] = bb / nblk;
+                bk[u] = bb - tk[u] * nblk;
+                const uint32_t i = bk[u] * 128u + 16u * l8;
+                gd_gu32x4 *src = gd_global4(XU + (size_t)tk[u] * E + i);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[u][q] = src[q];
                 if (has_signs) {
-                    const float4 *sg = reinterpret_cast<const float4 *>(S + i);
+                    gd_gu32x4 *sg = gd_global4(S + i);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float4 f = sg[q];
-                        v[4 * q] *= f.x; v[4 * q + 1] *= f.y; v[4 * q + 2] *= f.z; v[4 * q + 3] *= f.w;
-                    }
+                    for (int q = 0; q < 4; ++q) sv[u][q] = sg[q];
                 }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                if (!ok[u]) continue;
+                const uint32_t t = tk[u], blk = bk[u];
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = gd_bits_f32(xv[u][j >> 2][j & 3]);
+                if (a.c[15]) rt_store_h16(gd_buf<uint32_t>(a, a.c[16]) + a.c[17] + (size_t)t * (E / 2u) + blk * 64u + 8u * l8, v, bad);
                 // The DPP stages read lanes of the same 8-lane group only, and whole groups share
                 // b < total, so every source lane is active.
                 if (has_signs) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[j] *= gd_bits_f32(sv[u][j >> 2][j & 3]);
                     gd_fwht128_x16(v, l8);
 #pragma unroll
                     for (int j = 0; j < 16; ++j) v[j] *= GD_INV_SQRT128;
@@ -261,6 +315,7 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
     __syncthreads();
     const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;
     float *L = gd_buf<float>(a, a.c[9]) + a.c[10] + (size_t)z * n * NE;
+    const float *unscale = gd_buf<const float>(a, a.c[4]) + a.c[5] + (size_t)NE * E;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const uint32_t idx = tid + 512u * q, i = idx >> 5, j = idx & 31u;
@@ -269,6 +324,7 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
             float v = red[idx];
 #pragma unroll
             for (int w = 1; w < RT_WAVES; ++w) v += red[w * kRedStride + idx];
+            v *= unscale[r];
             if (has_bias) v += gd_buf<const float>(a, a.c[7])[a.c[8] + r];
             L[(size_t)t * NE + r] = v;
         }

@@ -68,6 +68,7 @@ static_assert(sizeof(ExpertDesc) == 32, "expert descriptor layout");
 
 struct Layer {
     Buffer router, bias, signs, xtab;
+    Buffer router16;  // the router rows split into binary16 pairs for moe_prefill_router
     bool has_bias = false, has_gate_signs = false, has_down_signs = false;
     float scale = 0;
     uint32_t type_id = 0;     // uniform Gyro type, 0 when projections mix types
@@ -161,6 +162,38 @@ float floats_to_scaled_half(const float *src, size_t n, std::vector<uint16_t> &d
     dst.resize(n);
     for (size_t i = 0; i < n; ++i) dst[i] = float_to_half(std::ldexp(src[i], k));
     return std::ldexp(1.0f, -k);
+}
+
+// The router rows as moe_prefill_router takes them: row r scaled by 2^k_r, k_r chosen so that its
+// largest finite |weight| lands in [2^14, 2^15), and each scaled value v carried as hi = f16(v)
+// and lo = f16((v - hi) 2^11) (round to nearest even; v - hi is exact). Row r, chunk c (k = 16 c
+// .. 16 c + 15) takes words 16 (r E / 16 + c) ..: the 16 hi values, then the 16 lo values; after
+// the NE x E words come the NE factors 2^-k_r.
+std::vector<uint32_t> split_router_rows(const float *w, uint32_t NE, uint32_t E) {
+    std::vector<uint32_t> out((size_t)NE * E + NE);
+    uint16_t *h = reinterpret_cast<uint16_t *>(out.data());
+    for (uint32_t r = 0; r < NE; ++r) {
+        const float *row = w + (size_t)r * E;
+        float mx = 0;
+        for (uint32_t k = 0; k < E; ++k) {
+            const float v = std::fabs(row[k]);
+            if (v == v && v != INFINITY) mx = std::max(mx, v);
+        }
+        int ex = 0;
+        if (mx > 0) std::frexp(mx, &ex);  // mx < 2^ex
+        const int kr = mx > 0 ? 15 - ex : 0;
+        for (uint32_t k = 0; k < E; ++k) {
+            const float v = std::ldexp(row[k], kr);
+            const uint16_t hi = float_to_half(v);
+            const uint16_t lo = float_to_half((v - half_to_float(hi)) * 2048.0f);
+            const size_t at = ((size_t)r * E + (k & ~15u)) * 2 + (k & 15u);
+            h[at] = hi;
+            h[at + 16] = lo;
+        }
+        const float unscale = std::ldexp(1.0f, -kr);
+        std::memcpy(&out[(size_t)NE * E + r], &unscale, 4);
+    }
+    return out;
 }
 
 // Shared-expert row formats: bytes of a source row of `cols` values (as gm_layer_desc gives it)
@@ -289,8 +322,8 @@ class Engine {
     // GYRO_STACK_NORM_FUSED=0: moe_stack_norm before every layer instead).
     bool stack_norm_fused = true;
     // The prefill router's K split doubles while its groups stay within this count (the
-    // environment's GYRO_ROUTER_GROUPS overrides it). One group per CU measured best: a split
-    // that gives 512 groups, two per CU, was no faster at 1024 tokens and adds a logit plane.
+    // environment's GYRO_ROUTER_GROUPS overrides it). One group per CU (96 KB of LDS each)
+    // measured best: splits that give 512 or 1024 groups were slower at 256 and 1024 tokens.
     uint32_t router_groups = 256;
     uint32_t small_rows() const {
         if (E % 512 || F % 512) return 0;
@@ -579,6 +612,11 @@ class Engine {
         upload(L.xtab, 0, desc.data(), NE * sizeof(ExpertDesc));
         L.router = dev.buffer((uint64_t)NE * E * 4, Kind::device);
         upload(L.router, 0, d.router, (uint64_t)NE * E * 4);
+        if (NE <= 256 && E % 256 == 0) {  // the prefill path's router shapes
+            const std::vector<uint32_t> sp = split_router_rows(d.router, NE, E);
+            L.router16 = dev.buffer(sp.size() * 4, Kind::device);
+            upload(L.router16, 0, sp.data(), sp.size() * 4);
+        }
         if (d.router_bias) {
             L.has_bias = true;
             L.bias = dev.buffer(NE * 4, Kind::device);
@@ -960,7 +998,7 @@ class Engine {
                (uint64_t)ks * 2 * n <= max_tok)
             ks *= 2;
         dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
-                             {x_uav, x_off, n, E, L.router.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
+                             {x_uav, x_off, n, E, L.router16.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
                               L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks, flag_uav(), hist.uav, 0, hist_words(n)},
                              (n + 31) / 32, (NE + 31) / 32, ks);

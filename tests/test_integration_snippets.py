@@ -166,6 +166,21 @@ CASES = [
 IDS = [f"{c[0]}-E{c[1]}-F{c[2]}-x{c[3]}-top{c[4]}-n{c[5]}" + "".join(f"-{k}" for k in c[6]) for c in CASES]
 
 
+def split_router_rows(w: np.ndarray) -> np.ndarray:
+    """The document's router16 layout of fp32 router rows w [NE][E], as u32 words."""
+    w = np.asarray(w, np.float32)
+    NE, E = w.shape
+    a = np.abs(w)
+    mx = np.where(np.isfinite(a), a, 0).max(axis=1)
+    k = np.where(mx > 0, 15 - np.frexp(mx)[1], 0).astype(np.int32)
+    v = np.ldexp(w, k[:, None]).astype(np.float32)
+    hi = v.astype(np.float16)
+    lo = ((v - hi.astype(np.float32)) * np.float32(2048)).astype(np.float16)
+    chunks = np.stack([hi.reshape(NE, E // 16, 16), lo.reshape(NE, E // 16, 16)], axis=2)  # [NE][E/16][2][16]
+    unscale = np.ldexp(np.float32(1), -k).astype(np.float32)
+    return np.concatenate([chunks.reshape(-1).view(np.uint32), unscale.view(np.uint32)])
+
+
 def names(L, n: int, cus: int, buffer):
     """The document's names for layer L and a call of n tokens. buffer(nbytes, data) makes a
     resource (an object with .uav, .srv and .gpu) holding `data` (bytes or None) at its start."""
@@ -195,6 +210,7 @@ def names(L, n: int, cus: int, buffer):
         xtab[e, 3] = int(t[0]) | int(t[1]) << 8 | int(t[2]) << 16
     l.xtab = buffer(xtab.nbytes, xtab.tobytes())
     l.router = buffer(L.router.nbytes, L.router.tobytes())
+    l.router16 = buffer(4 * (NE * E + NE), split_router_rows(L.router).tobytes())
     ns.bias_srv = buffer(NE * 4, L.router_bias.astype(np.float32).tobytes()).srv if L.router_bias is not None else NONE
     if L.gate_signs is not None:
         signs = np.concatenate([L.gate_signs, L.down_signs]).astype(np.float32)
