@@ -45,16 +45,21 @@
 
 #define RT_WAVES 4
 #define RT_KC 32    // K per staged chunk: one 128-byte line of every token row
-#ifndef RT_NBUF
-#define RT_NBUF 3   // chunks c .. c + 2 of a wave in LDS: two chunks (16 KB) in flight
+#define RT_NBUF 3   // chunks c .. c + 2 of a wave in LDS: two chunks in flight
+#ifndef RT_PIPELINE
+// This build: each MFMA wave takes one 32-expert column tile over a quarter of the group's K
+// range (the group's tile is 32 x 32, the four partial tiles added through LDS).
+#define RT_PIPELINE moe_prefill_router
+#define RT_TW 1
 #endif
-#define RT_LOADS 8  // global-to-LDS loads per chunk: four of token rows, four of router rows
+// Loads per chunk and wave: four of token rows, four per 32-expert column tile.
+#define RT_LOADS (4 * (1 + RT_TW))
 
-// The staging buffers of the four K waves; after its K loop a wave's partial tile (4 KB, fp32)
-// goes over its own first activation buffer.
+// The staging buffers of the four MFMA waves; in the one-tile build a wave's partial tile (4 KB,
+// fp32) goes over its own first activation buffer after its K loop.
 struct __attribute__((aligned(16))) RtLds {
-    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];  // 32 rows x 128 bytes
-    gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_KC / 4];
+    gd_u32x4 x[RT_WAVES][RT_NBUF][32 * RT_KC / 4];          // 32 rows x 128 bytes
+    gd_u32x4 w[RT_WAVES][RT_NBUF][32 * RT_TW * RT_KC / 4];  // 32 RT_TW rows x 128 bytes
 };
 static_assert(sizeof(RtLds) <= 163840, "the CU's 160 KB");
 static_assert(sizeof(RtLds::x[0]) >= 32 * 32 * 4, "a wave's partial tile fits its activation buffers");
@@ -63,45 +68,47 @@ static_assert(sizeof(RtLds::x[0]) >= 32 * 32 * 4, "a wave's partial tile fits it
 // m .. m + 7 read at one index sits in 8 different 16-byte bank groups.
 __device__ __forceinline__ uint32_t rt_pos(uint32_t q, uint32_t r) { return q ^ (r & 7u); }
 
-// Waits until chunk c's loads have landed, with `ahead` later chunks (RT_LOADS loads each) in
+// Waits until chunk c's loads have landed, with `ahead` (0 or 1) later chunks of RT_LOADS loads in
 // flight.
 __device__ __forceinline__ void rt_wait(uint32_t ahead) {
-    switch (ahead) {
-        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    }
+    if (ahead) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RT_LOADS) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Stages a chunk of this wave's 32 token rows and 32 router rows (xk, wk: the bases advanced to
-// the chunk's K offset): 4 + 4 loads, lane l of load i carrying row 8 i + l / 8, position l % 8.
+// Stages a chunk of this wave's 32 token rows and 32 RT_TW router rows (xk, wk: the bases advanced
+// to the chunk's K offset): 4 + 4 RT_TW loads, lane l of load i carrying row 8 i + l / 8,
+// position l % 8.
 __device__ __forceinline__ void rt_stage(RtLds &sm, uint32_t wave, uint32_t buf, const char *xk, const char *wk,
-                                         const uint32_t xoff[4], const uint32_t woff[4]) {
+                                         const uint32_t xoff[4], const uint32_t woff[4 * RT_TW]) {
     const uint32_t lx = gg_lds_addr(&sm.x[wave][buf][0]), lw = gg_lds_addr(&sm.w[wave][buf][0]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xk, xoff[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
+    for (int i = 0; i < 4 * RT_TW; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
 }
 
 // Operands of one K-step (16 K) for this lane (row m, lane half h; k = 8 h .. 8 h + 7 of the
-// step): the token row's values split into hi and lo, and the router row's hi and lo.
+// step): the token row's values split into hi and lo, and the hi and lo of the router row of
+// each column tile.
 struct RtOps {
-    f16x8 xh, xl, wh, wl;
+    f16x8 xh, xl, wh[RT_TW], wl[RT_TW];
 };
 // The step's raw reads from LDS (step s of the chunk in buffer buf): two 16-byte pieces of the
-// token row (fp32), one of the router row's hi values and one of its lo values. A staged router
-// row holds, per 16 K, the 16 hi values then the 16 lo values.
+// token row (fp32), and per column tile one of the router row's hi values and one of its lo
+// values. A staged router row holds, per 16 K, the 16 hi values then the 16 lo values.
 struct RtRaw {
-    gd_u32x4 x[2], wh, wl;
+    gd_u32x4 x[2], wh[RT_TW], wl[RT_TW];
 };
 __device__ __forceinline__ void rt_read(const RtLds &sm, uint32_t wave, uint32_t buf, uint32_t s, uint32_t m,
                                         uint32_t h, RtRaw &o) {
     o.x[0] = sm.x[wave][buf][m * 8u + rt_pos(4u * s + 2u * h, m)];
     o.x[1] = sm.x[wave][buf][m * 8u + rt_pos(4u * s + 2u * h + 1u, m)];
-    o.wh = sm.w[wave][buf][m * 8u + rt_pos(4u * s + h, m)];
-    o.wl = sm.w[wave][buf][m * 8u + rt_pos(4u * s + 2u + h, m)];
+#pragma unroll
+    for (int j = 0; j < RT_TW; ++j) {
+        const uint32_t r = m + 32u * (uint32_t)j;
+        o.wh[j] = sm.w[wave][buf][r * 8u + rt_pos(4u * s + h, r)];
+        o.wl[j] = sm.w[wave][buf][r * 8u + rt_pos(4u * s + 2u + h, r)];
+    }
 }
 // hi = f16(v), lo = f16((v - hi) 2^11) of the eight token values; xmax tracks max |v|. The lo
 // value is one mixed-precision fused multiply-add, 2^11 v - 2^11 hi (exact before its rounding
@@ -127,55 +134,71 @@ __device__ __forceinline__ void rt_split(const RtRaw &r, RtOps &o, float &xmax) 
     }
     o.xh = __builtin_bit_cast(f16x8, xh);
     o.xl = __builtin_bit_cast(f16x8, xl);
-    o.wh = __builtin_bit_cast(f16x8, r.wh);
-    o.wl = __builtin_bit_cast(f16x8, r.wl);
+#pragma unroll
+    for (int j = 0; j < RT_TW; ++j) {
+        o.wh[j] = __builtin_bit_cast(f16x8, r.wh[j]);
+        o.wl[j] = __builtin_bit_cast(f16x8, r.wl[j]);
+    }
 }
-// One K-step's three MFMAs (operands `cur`) with the step's other work between them, so that
-// the matrix pipe has the next MFMA waiting. A chunk takes two steps:
-//  - the first (SECOND false) issues the eight loads staging chunk c + RT_NBUF - 1 (into buffer
-//    bstage, that of chunk c - 1, whose reads are done) around its first two MFMAs, then reads
-//    the chunk's second step from the same buffer (bcur);
+// One K-step's MFMAs (operands `cur`; three per column tile) with the step's other work between
+// them, so that the matrix pipe has the next MFMA waiting. A chunk takes two steps:
+//  - the first (SECOND false) issues the loads staging chunk c + RT_NBUF - 1 (into buffer
+//    bstage, that of chunk c - 1, whose reads are done) around its first MFMAs, then reads the
+//    chunk's second step from the same buffer (bcur);
 //  - the second waits for chunk c + 1 and reads its first step (buffer bnext).
-// The reads are split into `next` after the third MFMA. The cross products go to acc_x, hi x hi
+// The reads are split into `next` after the last MFMAs. The cross products go to acc_x, hi x hi
 // to acc.
 template <bool SECOND>
 __device__ __forceinline__ void rt_step(RtLds &sm, uint32_t wave, uint32_t c, uint32_t nc, uint32_t m, uint32_t h,
-                                        const char *xk, const char *wk, const uint32_t xoff[4], const uint32_t woff[4],
-                                        uint32_t bstage, uint32_t bcur, uint32_t bnext, const RtOps &cur, RtOps &next,
-                                        f32x16 &acc, f32x16 &acc_x, float &xmax) {
+                                        const char *xk, const char *wk, const uint32_t xoff[4],
+                                        const uint32_t woff[4 * RT_TW], uint32_t bstage, uint32_t bcur, uint32_t bnext,
+                                        const RtOps &cur, RtOps &next, f32x16 (&acc)[RT_TW], f32x16 (&acc_x)[RT_TW],
+                                        float &xmax) {
     const bool stage = !SECOND && c + RT_NBUF - 1u < nc;
     const uint32_t lx = gg_lds_addr(&sm.x[wave][bstage][0]), lw = gg_lds_addr(&sm.w[wave][bstage][0]);
-    acc_x = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wl, acc_x, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (stage) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xk, xoff[i]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wh, acc, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (stage) {
+    for (int j = 0; j < RT_TW; ++j) {
+        acc_x[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wl[j], acc_x[j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (stage) {
+            if (j == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
+                for (int i = 0; i < 4; ++i) gg_dma16(lx + (uint32_t)i * 1024u, xk, xoff[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)(4 + i) * 1024u, wk, woff[4 + i]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xh, cur.wh[j], acc[j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (stage && j == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gg_dma16(lw + (uint32_t)i * 1024u, wk, woff[i]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     const bool more = !SECOND || c + 1u < nc;
-    if (SECOND && more) {
-        if (c + RT_NBUF <= nc) rt_wait(RT_NBUF - 2u);  // chunks c + 2 .. c + RT_NBUF - 1 in flight
-        else rt_wait(nc - 2u - c);
-    }
+    if (SECOND && more) rt_wait(c + RT_NBUF <= nc ? 1u : 0u);  // chunk c + 2 may stay in flight
     __builtin_amdgcn_sched_barrier(0);
     RtRaw raw;
     if (more) rt_read(sm, wave, SECOND ? bnext : bcur, SECOND ? 0u : 1u, m, h, raw);
     __builtin_amdgcn_sched_barrier(0);
-    acc_x = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xl, cur.wh, acc_x, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < RT_TW; ++j) {
+        acc_x[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xl, cur.wh[j], acc_x[j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if (more) rt_split(raw, next, xmax);
     // The operands stay allocated to the end of the step: a VGPR written while an MFMA that
     // reads it is in flight holds the write (and the wave) until the MFMA has read it.
     const gd_u32x4 k0 = __builtin_bit_cast(gd_u32x4, cur.xh), k1 = __builtin_bit_cast(gd_u32x4, cur.xl);
-    const gd_u32x4 k2 = __builtin_bit_cast(gd_u32x4, cur.wh), k3 = __builtin_bit_cast(gd_u32x4, cur.wl);
     asm volatile("" ::"v"(k0[0]), "v"(k0[1]), "v"(k0[2]), "v"(k0[3]), "v"(k1[0]), "v"(k1[1]), "v"(k1[2]), "v"(k1[3]));
-    asm volatile("" ::"v"(k2[0]), "v"(k2[1]), "v"(k2[2]), "v"(k2[3]), "v"(k3[0]), "v"(k3[1]), "v"(k3[2]), "v"(k3[3]));
+#pragma unroll
+    for (int j = 0; j < RT_TW; ++j) {
+        const gd_u32x4 k2 = __builtin_bit_cast(gd_u32x4, cur.wh[j]), k3 = __builtin_bit_cast(gd_u32x4, cur.wl[j]);
+        asm volatile("" ::"v"(k2[0]), "v"(k2[1]), "v"(k2[2]), "v"(k2[3]), "v"(k3[0]), "v"(k3[1]), "v"(k3[2]), "v"(k3[3]));
+    }
 }
 
 // Sixteen values as binary16 pairs (32 bytes) at dst; `bad` records a value outside the range.
@@ -193,29 +216,43 @@ __device__ __forceinline__ void rt_store_h16(uint32_t *dst, const float (&v)[16]
     d[1] = o[1];
 }
 
-GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
+// One group: waves 0..3 the router tile, waves 4..7 the rotation share. The name expands before
+// the pipeline macro stringises it.
+#define RT_DEFINE(NAME, OCC) GD_PIPELINE_NAMED_OCC(NAME, 512, OCC)
+RT_DEFINE(RT_PIPELINE, RT_TW == 1 ? 4 : 2) {
     __shared__ RtLds sm;
-    float *red = reinterpret_cast<float *>(&sm.x[0][0][0]);  // red(w) at sm.x[w][0]
-    constexpr uint32_t kRedStride = sizeof(sm.x[0]) / 4u;   // floats from one wave's buffers to the next
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = a.c[2], E = a.c[3], NE = a.c[6];
     const float *X = gd_buf<const float>(a, a.c[0]) + a.c[1];
-    const uint32_t t0 = blockIdx.x * 32u, r0 = blockIdx.y * 32u, z = blockIdx.z;
+    const uint32_t t0 = blockIdx.x * 32u, z = blockIdx.z;
+    // The group's first expert; in the wide build wave w takes experts r0 + 32 RT_TW w ...
+    const uint32_t r0 = blockIdx.y * (RT_TW == 1 ? 32u : 32u * RT_TW * RT_WAVES);
+    const uint32_t rw = RT_TW == 1 ? r0 : r0 + 32u * RT_TW * wave;
     const uint32_t S = a.c[18] > 1u ? a.c[18] : 1u, ES = E / S;
     const uint32_t m = lane & 31u, h = lane >> 5;
-    f32x16 acc = {};
+    const float *unscale = gd_buf<const float>(a, a.c[4]) + a.c[5] + (size_t)NE * E;
+    const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;
+    float *L = gd_buf<float>(a, a.c[9]) + a.c[10] + (size_t)z * n * NE;
+    f32x16 acc[RT_TW];
+#pragma unroll
+    for (int j = 0; j < RT_TW; ++j) acc[j] = (f32x16){};
 
-    if (wave < RT_WAVES) {
-        // Router tile, K quarter `wave`.
+    if (wave < RT_WAVES && rw < NE) {  // uniform per wave; the wide build's waves past n_expert idle
+        // Router tile: K quarter `wave` of range z (one-tile build) or all of range z.
         const float *W = gd_buf<const float>(a, a.c[4]) + a.c[5];
-        const uint32_t kq = z * ES + wave * (ES / 4u), nc = ES / 4u / RT_KC;
-        uint32_t xoff[4], woff[4];
+        const uint32_t kq = RT_TW == 1 ? z * ES + wave * (ES / 4u) : z * ES;
+        const uint32_t nc = (RT_TW == 1 ? ES / 4u : ES) / RT_KC;
+        uint32_t xoff[4], woff[4 * RT_TW];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = rt_pos(lane & 7u, r);
             xoff[i] = (min(t0 + r, n - 1u) * E + kq + 4u * q) * 4u;
-            woff[i] = (min(r0 + r, NE - 1u) * E + kq + 4u * q) * 4u;
+        }
+#pragma unroll
+        for (int i = 0; i < 4 * RT_TW; ++i) {
+            const uint32_t r = 8u * (uint32_t)i + (lane >> 3), q = rt_pos(lane & 7u, r);
+            woff[i] = (min(rw + r, NE - 1u) * E + kq + 4u * q) * 4u;
         }
         const char *xb = reinterpret_cast<const char *>(X), *wb = reinterpret_cast<const char *>(W);
         for (uint32_t c = 0; c < nc && c < RT_NBUF - 1u; ++c)
@@ -223,9 +260,11 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
         // Rows beyond n or n_expert were staged as copies of the last row (finite values); they
         // reach only tile rows and columns that are never stored.
         RtOps ops[2];
-        f32x16 acc_x = {};
+        f32x16 acc_x[RT_TW];
+#pragma unroll
+        for (int j = 0; j < RT_TW; ++j) acc_x[j] = (f32x16){};
         float xmax = 0.f;
-        rt_wait(min(nc - 1u, RT_NBUF - 2u));  // the chunks after chunk 0 may be in flight
+        rt_wait(min(nc - 1u, RT_NBUF - 2u));  // chunk 1 may be in flight
         {
             RtRaw raw;
             rt_read(sm, wave, 0, 0, m, h, raw);
@@ -244,12 +283,28 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
             b = bn;
         }
         gd_range_flag(a.table, a.c[19], !(xmax <= 65504.0f));
-        // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m. The wave's
-        // buffers are free: its last LDS reads were waited for before its last MFMAs.
+        // Accumulator register r holds tile row 8 (r / 4) + 4 h + r % 4, column m.
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            red[wave * kRedStride + ((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[r] + acc_x[r] * (1.0f / 2048.0f);
-    } else {
+        for (int j = 0; j < RT_TW; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[j][r] += acc_x[j][r] * (1.0f / 2048.0f);
+        if (RT_TW > 1) {
+            // Wide build: the wave's tiles are whole logits of plane z.
+#pragma unroll
+            for (int j = 0; j < RT_TW; ++j) {
+                const uint32_t col = rw + 32u * (uint32_t)j + m;
+                if (col < NE) {
+                    const float us = unscale[col];
+                    const float bias = has_bias ? gd_buf<const float>(a, a.c[7])[a.c[8] + col] : 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t t = t0 + (uint32_t)((r / 4) * 8 + (r % 4)) + 4u * h;
+                        if (t < n) L[(size_t)t * NE + col] = acc[j][r] * us + bias;
+                    }
+                }
+            }
+        }
+    } else if (wave >= RT_WAVES) {
         // Rotation share of this group's waves 4..7: each wave transforms eight 128-blocks at a
         // time, an 8-lane group per block holding 16 consecutive values per lane
         // (gd_fwht128_x16); the blocks b = 8 (first + waves j) + lane / 8. Two such steps run
@@ -312,21 +367,28 @@ GD_PIPELINE_NAMED_OCC(moe_prefill_router, 512, 4) {
             for (uint32_t i = first * 64u + lane; i < a.c[22]; i += waves * 64u) H[i] = 0u;
         }
     }
-    __syncthreads();
-    const bool has_bias = a.c[7] != 0xffffffffu && z == 0u;
-    float *L = gd_buf<float>(a, a.c[9]) + a.c[10] + (size_t)z * n * NE;
-    const float *unscale = gd_buf<const float>(a, a.c[4]) + a.c[5] + (size_t)NE * E;
+    if (RT_TW == 1) {
+        // One-tile build: the four K quarters added in wave order. The waves' buffers are free:
+        // their last LDS reads were waited for before their last MFMAs.
+        float *red = reinterpret_cast<float *>(&sm.x[0][0][0]);  // red(w) at sm.x[w][0]
+        constexpr uint32_t kRedStride = sizeof(sm.x[0]) / 4u;   // floats from one wave's buffers to the next
+        if (wave < RT_WAVES) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const uint32_t idx = tid + 512u * q, i = idx >> 5, j = idx & 31u;
-        const uint32_t t = t0 + i, r = r0 + j;
-        if (t < n && r < NE) {
-            float v = red[idx];
+            for (int r = 0; r < 16; ++r) red[wave * kRedStride + ((r / 4) * 8 + h * 4 + (r % 4)) * 32 + m] = acc[0][r];
+        }
+        __syncthreads();
 #pragma unroll
-            for (int w = 1; w < RT_WAVES; ++w) v += red[w * kRedStride + idx];
-            v *= unscale[r];
-            if (has_bias) v += gd_buf<const float>(a, a.c[7])[a.c[8] + r];
-            L[(size_t)t * NE + r] = v;
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t idx = tid + 512u * q, i = idx >> 5, j = idx & 31u;
+            const uint32_t t = t0 + i, r = r0 + j;
+            if (t < n && r < NE) {
+                float v = red[idx];
+#pragma unroll
+                for (int w = 1; w < RT_WAVES; ++w) v += red[w * kRedStride + idx];
+                v *= unscale[r];
+                if (has_bias) v += gd_buf<const float>(a, a.c[7])[a.c[8] + r];
+                L[(size_t)t * NE + r] = v;
+            }
         }
     }
 }

@@ -325,6 +325,11 @@ class Engine {
     // environment's GYRO_ROUTER_GROUPS overrides it). One group per CU (96 KB of LDS each)
     // measured best: splits that give 512 or 1024 groups were slower at 256 and 1024 tokens.
     uint32_t router_groups = 256;
+    // Calls of at least this many tokens take the wide router build (moe_prefill_router_w: 32
+    // tokens x 256 experts per group, each wave two 32-expert tiles over its group's whole K
+    // range), which stages a quarter fewer bytes per logit and needs a quarter of the groups; the
+    // environment's GYRO_ROUTER_WIDE_MIN overrides it (0: never).
+    uint32_t router_wide_min = 2048;
     uint32_t small_rows() const {
         if (E % 512 || F % 512) return 0;
         return E <= 2048 ? 16u : (E <= 4096 ? 8u : 0u);
@@ -484,6 +489,8 @@ class Engine {
             prefill_spin_limit = (uint32_t)std::strtoul(ps, nullptr, 10);
         if (const char *rg = std::getenv("GYRO_ROUTER_GROUPS"))
             router_groups = std::max(1u, (uint32_t)std::strtoul(rg, nullptr, 10));
+        if (const char *rw = std::getenv("GYRO_ROUTER_WIDE_MIN"))
+            router_wide_min = (uint32_t)std::strtoul(rw, nullptr, 10);
     }
 
     // The decode path's own intermediate buffers.
@@ -495,7 +502,7 @@ class Engine {
     void allocate_activations() {
         const uint64_t T = max_tok, f = 4;
         x_in = dev.buffer(T * E * f, Kind::device);
-        router_out = dev.buffer(T * NE * f, Kind::device);
+        router_out = dev.buffer(2 * T * NE * f, Kind::device);  // two logit planes of max_tok rows
         ids = dev.buffer(T * U * 4, Kind::device);
         weights = dev.buffer(T * U * f, Kind::device);
         table = dev.buffer(T * U * 24, Kind::device);
@@ -990,18 +997,20 @@ class Engine {
         const uint32_t base_lo = (uint32_t)L.base, base_hi = (uint32_t)(L.base >> 32);
         const uint32_t tiles = max_tiles(n);
         const uint32_t signs = L.has_down_signs ? L.signs.srv : kNone;
-        // K split of the router: small batches get more groups (up to router_groups of 32 x 32
-        // logit tiles), each K range writing its own logit plane.
-        const uint32_t rt_tiles = ((n + 31) / 32) * ((NE + 31) / 32);
+        // K split of the router: small batches get more groups (up to router_groups), each K
+        // range writing its own logit plane (at most two planes of max_tok rows).
+        const bool wide = router_wide_min && n >= router_wide_min;
+        const uint32_t rt_gy = wide ? (NE + 255) / 256 : (NE + 31) / 32;
+        const uint32_t rt_tiles = ((n + 31) / 32) * rt_gy;
         uint32_t ks = 1;
         while (rt_tiles * ks * 2 <= router_groups && E % (128 * ks * 2) == 0 && ks * 2 <= 16 &&
-               (uint64_t)ks * 2 * n <= max_tok)
+               (uint64_t)ks * 2 * n <= (wide ? 2ull : 1ull) * max_tok)
             ks *= 2;
-        dispatch_maybe_timed(bracket == 1, marks, "moe_prefill_router",
+        dispatch_maybe_timed(bracket == 1, marks, wide ? "moe_prefill_router_w" : "moe_prefill_router",
                              {x_uav, x_off, n, E, L.router16.srv, 0, NE, L.has_bias ? L.bias.srv : kNone, 0,
                               router_out.uav, 0, L.has_gate_signs ? L.signs.srv : kNone, 0, xh.uav, 0,
                               L.SF ? 1u : 0u, L.SF ? x16.uav : 0u, 0, ks, flag_uav(), hist.uav, 0, hist_words(n)},
-                             (n + 31) / 32, (NE + 31) / 32, ks);
+                             (n + 31) / 32, rt_gy, ks);
         dispatch_maybe_timed(bracket == 4, marks, "moe_prefill_topk",
                              {router_out.uav, 0, NE, n, bits(L.scale), ids.uav, 0, weights.uav, 0, ks, n * NE, U,
                               hist.uav, 0},

@@ -56,7 +56,7 @@ def test_kernels_built():
     kernels = {p.stem for p in (BUILD / "kernels").glob("*.co")}
     reference = {"mv_f32", "mv_bf16", "mv_q8", "q8_repack", "moe_route", "moe_resolve", "moe_gyro", "moe_act", "rotate128",
                  "moe_combine", "ew", "gyro_decode", "linalg_smoke", "moe_gyro_x"}
-    fast = {"moe_router", "moe_decode_gu", "moe_decode_gu_b", "moe_decode_down", "moe_dequant", "moe_prefill_router",
+    fast = {"moe_router", "moe_decode_gu", "moe_decode_gu_b", "moe_decode_down", "moe_dequant", "moe_prefill_router", "moe_prefill_router_w",
             "moe_prefill_topk", "moe_prefill_sort", "moe_prefill_gu", "moe_prefill_down", "moe_prefill_combine",
             "moe_stack_norm", "moe_decode_gu_x", "moe_decode_gu_xb", "moe_decode_down_x", "moe_decode_down_xb", "moe_decode_down_g", "moe_decode_gu_g", "moe_decode_gu_xg", "moe_decode_down_xg", "moe_prefill_gu_x", "moe_prefill_down_x", "gd_table_set"}
     assert reference | fast <= kernels, (reference | fast) - kernels

@@ -105,6 +105,23 @@ def test_prefill_4096_tokens(oracle_mod):
     assert len(eng_tiles[0]) == 32768
 
 
+def test_prefill_wide_router_build(oracle_mod, monkeypatch):
+    """The wide router build (moe_prefill_router_w, which the engine takes for 2048 tokens and
+    more) forced on every call: ragged token counts, 32, 64, 128 and 256 experts (waves and
+    column tiles past n_expert idle), hidden 2560 with top-10, a layer without rotations and the
+    Zipf layer with its bias, each against the oracle."""
+    monkeypatch.setenv("GYRO_ROUTER_WIDE_MIN", "1")
+    cases = [
+        (synth.make_layer(31, E=1024, F=256, n_expert=64, n_used=8), 37, 64, "64 experts, n=37"),
+        (synth.make_layer(41, E=1024, F=256, n_expert=32, n_used=8), 5, 64, "32 experts, n=5"),
+        (synth.make_layer(71, E=2560, F=640, n_expert=128, n_used=10, zipf=1.1), 150, 160, "hidden 2560, top-10"),
+        (synth.make_layer(51, E=1024, F=512, n_expert=64, n_used=8, signs=False), 70, 128, "no signs"),
+        (synth.make_layer(20261201, zipf=1.1), 256, 256, "full zipf"),
+    ]
+    for layer, n, max_tok, what in cases:
+        run_case(oracle_mod, layer, synth.make_tokens(700 + n, n, layer.E, bf16=True), max_tok, f"wide router: {what}")
+
+
 def test_prefill_single_and_ragged(oracle_mod):
     layer = synth.make_layer(31, E=1024, F=256, n_expert=64, n_used=8)
     for n in (1, 37):
