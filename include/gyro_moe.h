@@ -140,7 +140,9 @@ GM_API int gm_read_outputs(gm_engine *e, float *out, uint32_t n_total);
  * array of GM_NOALLOC_SCRATCH_BYTES per GPU, and a small kernel points two table entries at x and
  * out. A layer shape whose buffers exceed that array is refused with an error. Every call on one
  * GPU shares the array and those two entries: calls that overlap on one GPU race, so a caller
- * serialises them (one stream, or its own ordering). Results equal gm_forward's bit for bit. */
+ * serialises them (one stream, or its own ordering). Results equal gm_forward's bit for bit: the
+ * decode path keeps its activations in fp32, so no call of it is ever recomputed on another path
+ * (the binary16 range recompute of gm_forward concerns GM_PATH_PREFILL only). */
 GM_API int gm_forward_decode_noalloc(gm_engine *e, uint32_t layer, const float *x, uint32_t n, float *out,
                                      void *stream);
 
