@@ -7,8 +7,9 @@
 // s[t] * ((W_r[r] * w) . x[t]).
 // The rotated input is written in fp32 (xh[t][i]), the precision of src/engine.zig:547-551, which
 // the gate/up kernels multiply by fp32 codebook values.
-// Grid: x = max(n_expert, E / 128); 256 threads. Group r < n_expert computes router row r;
-// groups r < E / 128 also rotate block r of every token (wave 0).
+// Grid: x = n_expert + E / 128; 256 threads. Group r < n_expert computes router row r; group
+// n_expert + b rotates block b of every token (wave 0), beside the router rows rather than after
+// them in the same wave (with the norm, its four waves first sum the tokens' squares).
 // Constants: 0 x_uav 1 x_off 2 x_stride 3 n_tok 4 router_srv 5 router_off 6 n_expert 7 E
 // 8 bias_srv (0xffffffff: none) 9 bias_off 10 logits_uav 11 logits_off 12 signs_srv
 // (0xffffffff: copy) 13 signs_off 14 xh_uav (fp32 [n_tok][E]) 15 xh_off (words) 16 norm (0: none, 1: RMSNorm
@@ -16,7 +17,7 @@
 // 18 norm_w_off 19 eps (fp32 bits) 20 shared rows (2 SF; 0: no shared expert) 21 sh_w_srv (bf16
 // [2 SF][E]: gate rows then up rows) 22 sh_h_uav (fp32 [n][2 SF]) 23 sh_gate_srv (fp32 [E])
 // 24 sh_g_uav (fp32 [n]). With a shared expert (src/engine.zig:644-653) the grid has 2 SF / 4 + 1
-// further groups after the max(n_expert, E / 128) above: each of the first computes 4 bf16 rows
+// further groups after the n_expert + E / 128 above: each of the first computes 4 bf16 rows
 // (one per wave) of W_sg x and W_su x on the unrotated input, the last the gate dot g . x. The
 // shared groups require E <= 2048.
 // Every load is a global load issued ahead of its use, and the wave sums run on DPP.
@@ -73,7 +74,7 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     const float *X = gd_buf<const float>(a, a.c[0]);
     {
         // Shared-expert groups follow the router and rotation groups (uniform per group).
-        const uint32_t first_sh = max(NE, E / 128u);
+        const uint32_t first_sh = NE + E / 128u;
         if (a.c[20] && row >= first_sh) {
             const uint32_t sg = row - first_sh, n_sg = a.c[20] / SH_ROWS_PER_GROUP;
             if (sg < n_sg) {
@@ -104,10 +105,12 @@ GD_PIPELINE_NAMED(moe_router, 256) {
         }
     }
     const float *NW = norm == 2u ? gd_buf<const float>(a, a.c[17]) + a.c[18] : nullptr;
-    const bool rotate_here = wave == 0 && row < E / 128u;
-    // Rotation inputs first (independent of the router row): in pass p, lane l of wave 0 holds
-    // values 8 (l % 16) .. + 7 of block `row` of token 4 p + l / 16.
-    const uint32_t l16 = lane & 15u, ri = row * 128u + l16 * 8u;
+    const bool dot = row < NE;  // uniform per group
+    const bool rot = !dot && row < NE + E / 128u;  // a rotation group: block row - NE
+    const bool rotate_here = rot && wave == 0;
+    // Rotation inputs first: in pass p, lane l of wave 0 holds values 8 (l % 16) .. + 7 of the
+    // group's block of token 4 p + l / 16.
+    const uint32_t l16 = lane & 15u, blk = rot ? row - NE : 0u, ri = blk * 128u + l16 * 8u;
     const bool has_signs = a.c[12] != 0xffffffffu;
     float rx[2][8], rs[8];
 #pragma unroll
@@ -138,8 +141,7 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     }
     // Groups with a router row compute its dot products; with the norm, every group that has a
     // router row or a rotation block also needs the tokens' sums of squares.
-    const bool dot = row < NE;  // uniform per group
-    if (dot || (norm && row < E / 128u)) {
+    if (dot || (norm && rot)) {
         const uint32_t *W = gd_buf<const uint32_t>(a, a.c[4]) + a.c[5] + (size_t)(dot ? row : 0u) * E;
         constexpr int PER = ROUTER_MAX_E / 1024;
         float4 w[PER];
@@ -260,7 +262,7 @@ GD_PIPELINE_NAMED(moe_router, 256) {
                     o0[j] = gd_f32_bits(v[j]);
                     o1[j] = gd_f32_bits(v[4 + j]);
                 }
-                gd_u32x4 *dst = reinterpret_cast<gd_u32x4 *>(XH + t * E + row * 128u + l16 * 8u);
+                gd_u32x4 *dst = reinterpret_cast<gd_u32x4 *>(XH + t * E + blk * 128u + l16 * 8u);
                 dst[0] = o0;
                 dst[1] = o1;
             }

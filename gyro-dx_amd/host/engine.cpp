@@ -908,7 +908,7 @@ class Engine {
                               st.on ? (L.has_norm ? 2u : 1u) : 0u, L.has_norm ? L.norm.srv : 0u, 0,
                               bits(L.norm_eps), 2 * rsf, rsf ? L.sh_gu.srv : 0u, rsf ? B.sh_h : 0u,
                               rsf ? L.sh_gate.srv : 0u, rsf ? B.sh_g : 0u},
-                             std::max(NE, E / 128) + (rsf ? 2 * rsf / 4 + 1 : 0));
+                             NE + E / 128 + (rsf ? 2 * rsf / 4 + 1 : 0));
         if (!generic || !decode_generic_tuned()) {
             if (!generic && decode_tuned_tq2()) {
                 // One token: the build that holds a block's activations in registers at once;
