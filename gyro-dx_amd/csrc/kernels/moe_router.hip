@@ -112,6 +112,10 @@ GD_PIPELINE_NAMED(moe_router, 256) {
     // group's block of token 4 p + l / 16.
     const uint32_t l16 = lane & 15u, blk = rot ? row - NE : 0u, ri = blk * 128u + l16 * 8u;
     const bool has_signs = a.c[12] != 0xffffffffu;
+    // The row's bias, requested first so that its latency is not added after the barrier.
+    const bool has_bias = a.c[8] != 0xffffffffu;
+    float bias_v = 0.f;
+    if (dot && has_bias && tid < n_tok) bias_v = gd_bits_f32(*gd_global(gd_buf<const uint32_t>(a, a.c[8]) + a.c[9] + row));
     float rx[2][8], rs[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) rs[j] = 1.f;
@@ -194,7 +198,7 @@ GD_PIPELINE_NAMED(moe_router, 256) {
             const float q = (reds[0][tid] + reds[1][tid]) + (reds[2][tid] + reds[3][tid]);
             v *= 1.0f / sqrtf(q / (float)E + gd_bits_f32(a.c[19]));
         }
-        if (a.c[8] != 0xffffffffu) v += gd_buf<const float>(a, a.c[8])[a.c[9] + row];
+        if (has_bias) v += bias_v;
         gd_buf<float>(a, a.c[10])[a.c[11] + tid * NE + row] = v;
     }
     if (rotate_here) {
