@@ -140,6 +140,12 @@ DX_DEFINE(DX_PIPELINE, 512) {
     float wts[DN_U];
 #pragma unroll
     for (int kx = 0; kx < DN_U; ++kx) wts[kx] = wtp[kx];
+    // The shared expert's gate dot and the residual of the output rows, read at the end too.
+    float sh_gate = 0.f, res_v = 0.f;
+    if (tid < DN_ROWS) {
+        if (shared) sh_gate = gd_bits_f32(*gd_global(gd_buf<const uint32_t>(a, a.c[27]) + a.c[28] + t));
+        if (a.c[21]) res_v = gd_bits_f32(*gd_global(gd_buf<const uint32_t>(a, a.c[22]) + a.c[23] + t * E + row0 + tid));
+    }
     const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[6]);
     const uint32_t ew = min(ids[wave], NE - 1u);
     const uint32_t type_id = (xt[ew].types >> 16) & 0xffu;
@@ -270,10 +276,10 @@ DX_DEFINE(DX_PIPELINE, 512) {
 #pragma unroll
         for (int k = 0; k < DN_U; ++k) acc += wts[k] * dk[k][tid];
         if (shared) {
-            const float g = gd_sigmoid_accurate(gd_buf<const float>(a, a.c[27])[a.c[28] + t]);
+            const float g = gd_sigmoid_accurate(sh_gate);
             acc += g * shs[tid];
         }
-        if (a.c[21]) acc = gd_buf<const float>(a, a.c[22])[a.c[23] + t * E + row0 + tid] + acc;
+        if (a.c[21]) acc = res_v + acc;
         gd_buf<float>(a, a.c[13])[a.c[14] + t * E + row0 + tid] = acc;
     }
 }
