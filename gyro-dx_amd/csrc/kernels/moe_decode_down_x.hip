@@ -146,11 +146,36 @@ DX_DEFINE(DX_PIPELINE, 512) {
         if (shared) sh_gate = gd_bits_f32(*gd_global(gd_buf<const uint32_t>(a, a.c[27]) + a.c[28] + t));
         if (a.c[21]) res_v = gd_bits_f32(*gd_global(gd_buf<const uint32_t>(a, a.c[22]) + a.c[23] + t * E + row0 + tid));
     }
-    const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[6]);
+    // The expert table's down entries, lane l holding experts l + 64 j (row address and types,
+    // j < 4), requested beside the routes: once the route names the wave's expert, its entry is
+    // read from a register instead of a load that depends on the route.
+    uint32_t tlo[4], thi[4], tty[4];
+    {
+        const uint32_t *XT = gd_buf<const uint32_t>(a, a.c[6]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ex = min(lane + 64u * (uint32_t)j, NE - 1u);
+            gd_guint *ent = gd_global(XT + (size_t)ex * (sizeof(ExpertDesc) / 4u));
+            tlo[j] = ent[4];
+            thi[j] = ent[5];
+            tty[j] = ent[6];
+        }
+    }
     const uint32_t ew = min(ids[wave], NE - 1u);
-    const uint32_t type_id = (xt[ew].types >> 16) & 0xffu;
+    const uint32_t ej = ew >> 6, el = ew & 63u;  // uniform per wave
+    uint32_t vlo = tlo[0], vhi = thi[0], vty = tty[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+        if (ej == (uint32_t)j) {
+            vlo = tlo[j];
+            vhi = thi[j];
+            vty = tty[j];
+        }
+    const uint32_t type_id = ((uint32_t)__builtin_amdgcn_readlane((int)vty, (int)el) >> 16) & 0xffu;
+    const uint64_t down_addr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)vhi, (int)el) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)vlo, (int)el);
     const uint32_t bbw = block_bytes_of_type(type_id), nch = DN_ROWS / 4u * bbw;
-    const uint8_t *src = reinterpret_cast<const uint8_t *>(xt[ew].down) + (size_t)row0 * DN_NB * bbw;
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(down_addr) + (size_t)row0 * DN_NB * bbw;
     gd_u32x4 rv[DN_ROW_LOADS];
 #pragma unroll
     for (int j = 0; j < DN_ROW_LOADS; ++j)

@@ -59,6 +59,24 @@ GX_DEFINE(GX_PIPELINE, 512) {
     // Thread tid stages words 2 tid, 2 tid + 1 of the part (moe_decode_gu's layout).
     gd_guint *xg = gd_global(gd_buf<const uint32_t>(a, a.c[9]) + a.c[10] + t * E + part * 1024u + 2u * tid);
     const uint32_t xw0 = xg[0], xw1 = xg[1];
+#if !GX_STEPWISE
+    // The expert table's entries of this group's projection, lane l holding experts l + 64 j
+    // (row address and types, j < 4): requested with the other inputs, so that routing names the
+    // expert and its entry is read from a register instead of a dependent load (the batch build
+    // keeps its registers for occupancy and reads the table after routing).
+    uint32_t tlo[4], thi[4], tty[4];
+    {
+        const uint32_t *XT = gd_buf<const uint32_t>(a, a.c[11]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ex = min(lane + 64u * (uint32_t)j, NE - 1u);
+            gd_guint *ent = gd_global(XT + (size_t)ex * (sizeof(ExpertDesc) / 4u));
+            tlo[j] = ent[2u * proj];
+            thi[j] = ent[2u * proj + 1u];
+            tty[j] = ent[6];
+        }
+    }
+#endif
 
     // Routing to this group's rank k only; the recording group runs every round (moe_decode_gu).
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && k == 0;
@@ -90,12 +108,27 @@ GX_DEFINE(GX_PIPELINE, 512) {
         }
     }
 
+#if GX_STEPWISE
     const ExpertDesc *xt = gd_buf<const ExpertDesc>(a, a.c[11]);
     const uint32_t types = __builtin_amdgcn_readfirstlane(xt[e].types);
+    const uint64_t addr = proj ? xt[e].up : xt[e].gate;
+#else
+    const uint32_t ej = e >> 6, el = e & 63u;  // uniform
+    uint32_t vlo = tlo[0], vhi = thi[0], vty = tty[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+        if (ej == (uint32_t)j) {
+            vlo = tlo[j];
+            vhi = thi[j];
+            vty = tty[j];
+        }
+    const uint32_t types = (uint32_t)__builtin_amdgcn_readlane((int)vty, (int)el);
+    const uint64_t addr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)vhi, (int)el) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)vlo, (int)el);
+#endif
     const uint32_t type_id = (types >> (8u * proj)) & 0xffu;
     GyroType gt;
     if (!gd_type(type_id, gt)) return;  // uniform: the host admits only the eight types
-    const uint64_t addr = proj ? xt[e].up : xt[e].gate;
     const uint32_t bb = gt.block_bytes, row_bytes = E / 128u * bb;
     const uint8_t *row = reinterpret_cast<const uint8_t *>(addr) + (uint64_t)(row0 + r) * row_bytes + part * 8u * bb;
     const uint32_t off = b * bb;  // even
