@@ -179,11 +179,12 @@ def test_zipf_bias_routing(oracle_mod):
 
 
 @pytest.mark.parametrize("E,F,NE,U", [(2560, 640, 128, 10), (1024, 384, 64, 6), (3072, 1024, 64, 16),
-                                      (2048, 512, 64, 4)])
+                                      (2048, 512, 64, 4), (2048, 512, 12, 8), (4096, 512, 16, 8)])
 def test_decode_path_other_shapes(oracle_mod, E, F, NE, U):
     """The decode path at the real model's expert shapes (hidden 2560, F 640, top-10: a partial
     last K-part of the gate/up kernel and moe_decode_down_g) and at other widths and top-k,
-    for 1, 3 and 8 tokens, with the residual of a stack step on the last case."""
+    for 1, 3 and 8 tokens; the last two have fewer router rows than 128-blocks, so most of
+    moe_router's groups only rotate."""
     L = synth.make_layer(200 + U, E=E, F=F, n_expert=NE, n_used=U)
     ol = oracle_mod.OracleLayer(L)
     eng = Engine(max_tok=8)
